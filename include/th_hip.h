@@ -1,0 +1,224 @@
+/*
+ * th_hip.h -- C ABI of libth_hip.so, the MI355X (gfx950) kernel library that
+ * executes torch-helion OpIR kernels.
+ *
+ * Every entry point is extern "C", takes plain pointers and sizes, and never
+ * aborts: it returns TH_OK (0) or a negative th_status and leaves a message in
+ * th_last_error() (thread-local). Launches are asynchronous on the stream
+ * passed in (a hipStream_t, NULL = the default stream). The caller owns every
+ * device buffer. Descriptors are validated on the host before any launch.
+ *
+ * In the reference, one OpIR KernelSpec becomes one generated Helion kernel
+ * module whose host function allocates its outputs and returns them
+ * (reference: src/torch_helion/codegen/emit.py:188-221 gemm, :254-324 ssd,
+ * :327-357 attention, driven by emit_program at codegen/emit.py:500-520 and
+ * executed numerically only by codegen/interpret.py:18-51). Here the same
+ * KernelSpec becomes one call below with caller-allocated outputs.
+ */
+#ifndef TH_HIP_H
+#define TH_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TH_ABI_VERSION 1
+
+typedef enum th_status {
+  TH_OK = 0,
+  TH_ERR_INVALID = -1,     /* bad descriptor: null pointer, bad shape/stride */
+  TH_ERR_UNSUPPORTED = -2, /* valid request this build has no kernel for */
+  TH_ERR_HIP = -3,         /* a HIP runtime call failed */
+  TH_ERR_NOT_INIT = -4     /* th_init was not called for the current device */
+} th_status;
+
+typedef enum th_dtype {
+  TH_F32 = 0,
+  TH_BF16 = 1,
+  TH_F16 = 2,
+  TH_F8E4M3 = 3, /* OCP float8_e4m3fn (max 448) */
+  TH_I32 = 4,
+  TH_I64 = 5
+} th_dtype;
+
+/* ------------------------------------------------------------------ setup */
+
+/* ABI version of the loaded library (TH_ABI_VERSION it was built with). */
+int th_abi_version(void);
+
+/* Select and initialise a device: checks it is gfx950 and raises the LDS
+ * limit of the kernels that need more than 64 KiB. Call once per device. */
+int th_init(int device);
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* th_last_error(void);
+
+/* --------------------------------------------------------------- gemm kind
+ * OpIR `gemm` KernelSpec (reference: optimizer/opir.py:13-20, executed by
+ * codegen/interpret.py:22-35, emitted by codegen/emit.py:188-221):
+ *   acc_i = lhs[M, K] @ rhs_i[K, N]          (i < n_acc, all sharing lhs)
+ *   r     = (sumsq * inv_k + eps) ^ -1/2,    sumsq = sum_k lhs^2   (optional)
+ *   a_i   = acc_i * r  if bit i of rscale_mask else acc_i
+ * followed by a fixed catalogue of fused output ops (th_epi_op) that the
+ * Python lowering matches against the kernel's epilogue SSA. Epilogues
+ * outside the catalogue run as TH_EPI_ACC (fp32) + th_epilogue_vm.
+ */
+typedef enum th_epi_op {
+  TH_EPI_ACC = 0,          /* a_i                                            */
+  TH_EPI_ROPE = 1,         /* a_i*cos + rotate_half_heads(a_i)*sin           */
+  TH_EPI_ROPE_PAIR = 2,    /* a_i*cos + a_j*sin  (a_j = pre-rotated acc)     */
+  TH_EPI_SILU = 3,         /* a_i * sigmoid(a_i)                             */
+  TH_EPI_SWIGLU = 4,       /* (a_i * sigmoid(a_i)) * a_j                     */
+  TH_EPI_ADD = 5,          /* a_i + extra_e                                  */
+  TH_EPI_SOFTPLUS_ADD = 6, /* log(1 + exp(a_i + extra_e))                    */
+  TH_EPI_MUL = 7           /* a_i * extra_e                                  */
+} th_epi_op;
+
+#define TH_MAX_ACC 4
+#define TH_MAX_OUT 6
+#define TH_MAX_EXTRA 4
+
+typedef struct th_epi_out {
+  int32_t op;     /* th_epi_op */
+  int32_t a, b;   /* accumulator indices (b only for ROPE_PAIR / SWIGLU) */
+  int32_t e;      /* extra operand index for ADD / SOFTPLUS_ADD / MUL, else -1 */
+  void* ptr;      /* [M, N] row-major output */
+  int64_t ld;     /* row stride of ptr, in elements */
+  int32_t dtype;  /* TH_F32 or TH_BF16 */
+  int32_t pad_;
+} th_epi_out;
+
+typedef struct th_gemm_desc {
+  int64_t M, N, K;
+  int32_t n_acc;          /* 0 .. TH_MAX_ACC */
+  int32_t in_dtype;       /* TH_BF16 (MFMA bf16) or TH_F32 (MFMA f32) */
+  const void* lhs;        /* [M, K] row-major, in_dtype */
+  int64_t ld_lhs;
+  const void* rhs_packed; /* th_gemm_pack_rhs output for (N, K, n_acc, in_dtype) */
+  int32_t sumsq;          /* 1: compute the RMS row scale r */
+  uint32_t rscale_mask;
+  float inv_k, eps;
+  int32_t n_extra;
+  int32_t pad_;
+  const void* extra[TH_MAX_EXTRA]; /* [M, N] operands read at the output tile */
+  int64_t ld_extra[TH_MAX_EXTRA];
+  int32_t extra_dtype[TH_MAX_EXTRA];
+  const float* rope_cos;  /* [rope_period, rope_head_dim] fp32 (ROPE ops) */
+  const float* rope_sin;
+  int32_t rope_head_dim;  /* columns of one head; rotation pairs n, n+hd/2 */
+  int32_t rope_period;    /* table row = output row % rope_period */
+  int32_t n_out;
+  int32_t pad2_;
+  th_epi_out out[TH_MAX_OUT];
+  float* sumsq_out;       /* optional [M] fp32: raw sum_k lhs^2 */
+} th_gemm_desc;
+
+/* Per-accumulator column tile th_gemm uses for (N, n_acc, in_dtype); a block
+ * computes n_acc * tile columns. Fused RoPE (TH_EPI_ROPE) needs the tile to
+ * be a multiple of the head dim. Returns 0 for invalid arguments. */
+int th_gemm_acc_tile(int64_t N, int32_t n_acc, int32_t in_dtype);
+
+/* Bytes of the packed right-hand side for th_gemm (weights are packed once
+ * at upload; activation operands are packed per call into a workspace). */
+int64_t th_gemm_packed_bytes(int64_t N, int64_t K, int32_t n_acc, int32_t in_dtype);
+
+/* Pack n_acc row-major [K, N] operands (dtype src_dtype, row stride ld_src)
+ * into the K-contiguous, accumulator-interleaved layout th_gemm reads.
+ * Replaces the reference's per-kernel weight arguments w0..w{n-1}
+ * (optimizer/partition.py:121-124, bound at codegen/emit.py:469-476). */
+int th_gemm_pack_rhs(const void* const* src, const int64_t* ld_src, int32_t src_dtype,
+                     int64_t N, int64_t K, int32_t n_acc, int32_t in_dtype,
+                     void* packed, void* stream);
+
+/* One OpIR gemm KernelSpec. */
+int th_gemm(const th_gemm_desc* desc, void* stream);
+
+/* ------------------------------------------------------------ RMSNorm
+ * The stand-alone normalisation kernel (gemm kind with gemms=[] and sumsq;
+ * reference: optimizer/partition.py:165-177, optimizer/passes.py:357-370):
+ *   out[m, :] = x[m, :] * (sum_k x[m,k]^2 * inv_k + eps)^-1/2 * gain[:]
+ */
+typedef struct th_rmsnorm_desc {
+  int64_t M, K;
+  const void* x; int64_t ld_x; int32_t x_dtype;
+  int32_t out_dtype;
+  const float* gain;      /* [K] fp32 */
+  void* out; int64_t ld_out;
+  float inv_k, eps;
+} th_rmsnorm_desc;
+
+int th_rmsnorm(const th_rmsnorm_desc* desc, void* stream);
+
+/* --------------------------------------------------------- attention kind
+ * softmax(q k^T * scale [+ causal mask]) v over [B, S, H, d] views of
+ * token-major [B*S, H*d] tensors (reference: optimizer/evaluate.py:139-146,
+ * codegen/emit.py:327-357). Extended with grouped KV heads (heads_q is a
+ * multiple of heads_kv; q head h reads kv head h / (heads_q / heads_kv)) and
+ * a causal flag (query i sees keys j <= i + seq_kv - seq_q).
+ */
+typedef struct th_attn_desc {
+  int32_t batch, seq_q, seq_kv, heads_q, heads_kv, head_dim;
+  float scale;
+  int32_t causal;
+  int32_t dtype;          /* TH_BF16 or TH_F32 for q, k, v and o */
+  int32_t pad_;
+  const void* q; int64_t ld_q;  /* row stride in elements (>= heads*head_dim) */
+  const void* k; int64_t ld_k;
+  const void* v; int64_t ld_v;
+  void* o; int64_t ld_o;
+} th_attn_desc;
+
+int th_attention_prefill(const th_attn_desc* desc, void* stream);
+
+/* ------------------------------------------------- epilogue VM (fallback)
+ * Evaluates an OpIR epilogue SSA (registered ops, reference:
+ * capture/ops.py:34-37, executed as in codegen/interpret.py:27-34) that the
+ * fused catalogue does not cover. Operands are [M, N] tensors or [M, 1]
+ * columns; values live in fp32 slots of a caller-provided workspace of
+ * n_slots * M * N floats. One pass per op.
+ */
+typedef enum th_vm_code {
+  TH_VM_LOAD = 0,   /* slot <- operand a (column operands broadcast) */
+  TH_VM_ADD = 1, TH_VM_SUB = 2, TH_VM_MUL = 3, TH_VM_DIV = 4, TH_VM_MAX = 5, TH_VM_POW = 6,
+  TH_VM_EXP = 7, TH_VM_LOG = 8,
+  TH_VM_ROW_SUM = 9, TH_VM_ROW_MAX = 10, /* result broadcast over the row */
+  TH_VM_COPY = 11
+} th_vm_code;
+
+#define TH_VM_MAX_IN 16
+#define TH_VM_MAX_OPS 96
+#define TH_VM_MAX_OUT 8
+
+typedef struct th_vm_operand {
+  const void* ptr; int64_t ld; int32_t dtype;
+  int32_t column;         /* 1: [M, 1] operand broadcast along the row */
+} th_vm_operand;
+
+typedef struct th_vm_op {
+  int32_t code, dst, a, b; /* slots; for LOAD, a is an operand index */
+  float scalar;
+  int32_t mode;            /* 0: slot op slot, 1: slot op scalar, 2: scalar op slot */
+} th_vm_op;
+
+typedef struct th_vm_out {
+  void* ptr; int64_t ld; int32_t dtype; int32_t slot;
+} th_vm_out;
+
+typedef struct th_vm_desc {
+  int64_t M, N;
+  int32_t n_in, n_ops, n_out, n_slots;
+  th_vm_operand in[TH_VM_MAX_IN];
+  th_vm_op ops[TH_VM_MAX_OPS];
+  th_vm_out out[TH_VM_MAX_OUT];
+  float* workspace;        /* n_slots * M * N fp32 */
+} th_vm_desc;
+
+int th_epilogue_vm(const th_vm_desc* desc, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TH_HIP_H */

@@ -1,0 +1,251 @@
+"""Kernel-level parity: each libth_hip.so entry point vs a torch fp32 CPU reference.
+
+Tolerances: fp32 kernels 1e-4 relative to the output's max magnitude; bf16
+kernels 2e-2 max-abs against the fp32 reference computed from the same
+(bf16-rounded) inputs, the north-star bound.
+"""
+
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+
+from conftest import announce
+
+pytestmark = pytest.mark.gpu
+
+BF16_TOL = 2e-2
+F32_REL = 1e-4
+
+
+def _rel(a: torch.Tensor, b: torch.Tensor) -> float:
+    a, b = a.float().cpu(), b.float().cpu()
+    return float((a - b).abs().max() / (b.abs().max() + 1e-6))
+
+
+def _maxabs(a: torch.Tensor, b: torch.Tensor) -> float:
+    return float((a.float().cpu() - b.float().cpu()).abs().max())
+
+
+def _rope_tables(seq: int, hd: int, theta: float = 10000.0):
+    inv = 1.0 / (theta ** (torch.arange(0, hd, 2, dtype=torch.float32) / hd))
+    f = torch.outer(torch.arange(seq, dtype=torch.float32), inv)
+    e = torch.cat((f, f), -1)
+    return e.cos(), e.sin()
+
+
+def _rot_heads(x: torch.Tensor, hd: int) -> torch.Tensor:
+    x4 = x.reshape(*x.shape[:-1], x.shape[-1] // hd, hd)
+    h = hd // 2
+    return torch.cat((-x4[..., h:], x4[..., :h]), -1).reshape(x.shape)
+
+
+@pytest.mark.parametrize("M,N,K", [(300, 200, 136), (1024, 256, 512), (8192, 4096, 256)])
+def test_gemm_bf16_plain(gpu, M, N, K):
+    from torch_helion.hip import abi, ops
+
+    announce(f"gemm bf16 plain M={M} N={N} K={K}")
+    g = torch.Generator().manual_seed(M + N + K)
+    a = torch.randn(M, K, generator=g).bfloat16()
+    w = (torch.randn(K, N, generator=g) * 0.05).bfloat16()
+    ref = a.float() @ w.float()
+    ad, wd = a.to(gpu), w.to(gpu)
+    packed = ops.pack_rhs([wd], torch.bfloat16)
+    o16 = torch.empty(M, N, dtype=torch.bfloat16, device=gpu)
+    o32 = torch.empty(M, N, dtype=torch.float32, device=gpu)
+    ops.gemm(ops.GemmCall(M, N, K, 1, ad, packed, [ops.EpiSpec(abi.EPI_ACC, o16), ops.EpiSpec(abi.EPI_ACC, o32)]))
+    torch.cuda.synchronize()
+    assert _rel(o32, ref) < 1e-5
+    assert _maxabs(o16, ref) < BF16_TOL
+
+
+def test_gemm_bf16_rms_swiglu(gpu):
+    from torch_helion.hip import abi, ops
+
+    announce("gemm bf16 n_acc=2 sumsq swiglu")
+    M, N, K, eps = 1000, 384, 512, 1e-5
+    g = torch.Generator().manual_seed(1)
+    x = torch.randn(M, K, generator=g).bfloat16()
+    wg = (torch.randn(K, N, generator=g) * 0.02).bfloat16()
+    wu = (torch.randn(K, N, generator=g) * 0.02).bfloat16()
+    xf = x.float()
+    r = ((xf * xf).sum(-1, keepdim=True) / K + eps).pow(-0.5)
+    hg, hu = (xf @ wg.float()) * r, (xf @ wu.float()) * r
+    ref = hg * torch.sigmoid(hg) * hu
+    xd = x.to(gpu)
+    packed = ops.pack_rhs([wg.to(gpu), wu.to(gpu)], torch.bfloat16)
+    out = torch.empty(M, N, dtype=torch.bfloat16, device=gpu)
+    ss = torch.empty(M, dtype=torch.float32, device=gpu)
+    ops.gemm(ops.GemmCall(M, N, K, 2, xd, packed, [ops.EpiSpec(abi.EPI_SWIGLU, out, a=0, b=1)], sumsq=True,
+                          rscale_mask=0b11, inv_k=1.0 / K, eps=eps, sumsq_out=ss))
+    torch.cuda.synchronize()
+    assert _maxabs(out, ref) < BF16_TOL
+    assert _rel(ss, (xf * xf).sum(-1)) < 1e-5
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_gemm_qkv_rope(gpu, dtype):
+    """QKV with the RMS fold and RoPE: fused rotation vs the pre-rotated accumulator."""
+    from torch_helion.hip import abi, ops
+
+    announce(f"gemm qkv rope {dtype}")
+    B, S, H, hd, K, eps = 2, 96, 4, 64, 256, 1e-6
+    M, N = B * S, H * hd
+    g = torch.Generator().manual_seed(2)
+    x = torch.randn(M, K, generator=g).to(dtype)
+    wq, wk, wv = [(torch.randn(K, N, generator=g) * 0.05).to(dtype) for _ in range(3)]
+    cos, sin = _rope_tables(S, hd)
+    xf = x.float()
+    r = ((xf * xf).sum(-1, keepdim=True) / K + eps).pow(-0.5)
+    q, k, v = [(xf @ w.float()) * r for w in (wq, wk, wv)]
+    cf, sf = cos.repeat(B, H), sin.repeat(B, H)
+    q_ref = q * cf + _rot_heads(q, hd) * sf
+    k_ref = k * cf + _rot_heads(k, hd) * sf
+    xd = x.to(gpu)
+    packed = ops.pack_rhs([w.to(gpu) for w in (wq, wk, wv)], dtype)
+    wkr = _rot_heads(wk.float(), hd).contiguous().to(dtype)  # W @ R: rotate W's output columns
+    packed2 = ops.pack_rhs([wk.to(gpu), wkr.to(gpu)], dtype)
+    oq, ok, ov, ok2 = [torch.empty(M, N, dtype=dtype, device=gpu) for _ in range(4)]
+    cd, sd = cos.to(gpu).contiguous(), sin.to(gpu).contiguous()
+    common = dict(sumsq=True, inv_k=1.0 / K, eps=eps, rope_cos=cd, rope_sin=sd, rope_head_dim=hd, rope_period=S)
+    ops.gemm(ops.GemmCall(M, N, K, 3, xd, packed, [ops.EpiSpec(abi.EPI_ROPE, oq, a=0), ops.EpiSpec(abi.EPI_ROPE, ok, a=1),
+                                                    ops.EpiSpec(abi.EPI_ACC, ov, a=2)], rscale_mask=0b111, **common))
+    ops.gemm(ops.GemmCall(M, N, K, 2, xd, packed2, [ops.EpiSpec(abi.EPI_ROPE_PAIR, ok2, a=0, b=1)], rscale_mask=0b11, **common))
+    torch.cuda.synchronize()
+    if dtype == torch.float32:
+        for o, ref in ((oq, q_ref), (ok, k_ref), (ov, v), (ok2, k_ref)):
+            assert _rel(o, ref) < F32_REL
+    else:
+        for o, ref in ((oq, q_ref), (ok, k_ref), (ov, v), (ok2, k_ref)):
+            assert _maxabs(o, ref) < BF16_TOL
+
+
+def test_gemm_extra_ops(gpu):
+    from torch_helion.hip import abi, ops
+
+    announce("gemm bf16 add/softplus/mul extras")
+    M, N, K = 513, 160, 64
+    g = torch.Generator().manual_seed(3)
+    a = torch.randn(M, K, generator=g).bfloat16()
+    w = (torch.randn(K, N, generator=g) * 0.1).bfloat16()
+    e0 = torch.randn(M, N, generator=g).bfloat16()
+    e1 = torch.randn(M, N, generator=g).float()
+    acc = a.float() @ w.float()
+    ad = a.to(gpu)
+    packed = ops.pack_rhs([w.to(gpu)], torch.bfloat16)
+    o = [torch.empty(M, N, dtype=torch.bfloat16, device=gpu) for _ in range(3)]
+    o.append(torch.empty(M, N, dtype=torch.float32, device=gpu))
+    ops.gemm(ops.GemmCall(M, N, K, 1, ad, packed,
+                          [ops.EpiSpec(abi.EPI_ADD, o[0], e=0), ops.EpiSpec(abi.EPI_SOFTPLUS_ADD, o[1], e=1),
+                           ops.EpiSpec(abi.EPI_MUL, o[2], e=1), ops.EpiSpec(abi.EPI_SILU, o[3])],
+                          extras=[e0.to(gpu), e1.to(gpu)]))
+    torch.cuda.synchronize()
+    assert _maxabs(o[0], acc + e0.float()) < BF16_TOL
+    assert _maxabs(o[1], torch.log(1 + torch.exp(acc + e1))) < BF16_TOL
+    assert _maxabs(o[2], acc * e1) < BF16_TOL
+    assert _rel(o[3], acc * torch.sigmoid(acc)) < 1e-5
+
+
+def test_gemm_f32_small(gpu):
+    from torch_helion.hip import abi, ops
+
+    announce("gemm f32 M=128 N=1376 K=512 + residual")
+    M, N, K = 128, 1376, 512
+    g = torch.Generator().manual_seed(4)
+    a = torch.randn(M, K, generator=g)
+    w = torch.randn(K, N, generator=g) * 0.02
+    res = torch.randn(M, N, generator=g)
+    ref = res + a @ w
+    packed = ops.pack_rhs([w.to(gpu)], torch.float32)
+    out = torch.empty(M, N, device=gpu)
+    ops.gemm(ops.GemmCall(M, N, K, 1, a.to(gpu), packed, [ops.EpiSpec(abi.EPI_ADD, out, e=0)], extras=[res.to(gpu)]))
+    torch.cuda.synchronize()
+    assert _rel(out, ref) < F32_REL
+
+
+def _attn_ref(q, k, v, B, S, Hq, Hkv, hd, scale, causal):
+    q4 = q.float().reshape(B, S, Hq, hd).transpose(1, 2)
+    k4 = k.float().reshape(B, S, Hkv, hd).transpose(1, 2).repeat_interleave(Hq // Hkv, dim=1)
+    v4 = v.float().reshape(B, S, Hkv, hd).transpose(1, 2).repeat_interleave(Hq // Hkv, dim=1)
+    s = (q4 @ k4.transpose(-1, -2)) * scale
+    if causal:
+        s = s.masked_fill(torch.triu(torch.ones(S, S, dtype=torch.bool), 1), float("-inf"))
+    return (torch.softmax(s, -1) @ v4).transpose(1, 2).reshape(B * S, Hq * hd)
+
+
+@pytest.mark.parametrize("B,S,Hq,Hkv,hd,causal", [(2, 200, 4, 2, 128, True), (1, 256, 8, 8, 64, False),
+                                                  (2, 384, 8, 2, 128, False), (1, 130, 4, 1, 64, True)])
+def test_attention_bf16(gpu, B, S, Hq, Hkv, hd, causal):
+    from torch_helion.hip import ops
+
+    announce(f"attention bf16 B={B} S={S} Hq={Hq} Hkv={Hkv} hd={hd} causal={causal}")
+    g = torch.Generator().manual_seed(S + hd)
+    q = torch.randn(B * S, Hq * hd, generator=g).bfloat16()
+    k = torch.randn(B * S, Hkv * hd, generator=g).bfloat16()
+    v = torch.randn(B * S, Hkv * hd, generator=g).bfloat16()
+    scale = hd ** -0.5
+    ref = _attn_ref(q, k, v, B, S, Hq, Hkv, hd, scale, causal)
+    out = torch.empty(B * S, Hq * hd, dtype=torch.bfloat16, device=gpu)
+    ops.attention_prefill(q.to(gpu), k.to(gpu), v.to(gpu), out, batch=B, seq_q=S, seq_kv=S, heads_q=Hq, heads_kv=Hkv,
+                          head_dim=hd, scale=scale, causal=causal)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all()
+    assert _maxabs(out, ref) < BF16_TOL
+
+
+def test_attention_f32(gpu):
+    from torch_helion.hip import ops
+
+    announce("attention f32 B=1 S=128 H=8 hd=64 causal")
+    B, S, H, hd = 1, 128, 8, 64
+    g = torch.Generator().manual_seed(9)
+    q, k, v = [torch.randn(B * S, H * hd, generator=g) for _ in range(3)]
+    ref = _attn_ref(q, k, v, B, S, H, H, hd, hd ** -0.5, True)
+    out = torch.empty(B * S, H * hd, device=gpu)
+    ops.attention_prefill(q.to(gpu), k.to(gpu), v.to(gpu), out, batch=B, seq_q=S, seq_kv=S, heads_q=H, heads_kv=H,
+                          head_dim=hd, scale=hd ** -0.5, causal=True)
+    torch.cuda.synchronize()
+    assert _rel(out, ref) < F32_REL
+
+
+@pytest.mark.parametrize("dtype,M,K", [(torch.bfloat16, 1000, 4096), (torch.float32, 77, 512), (torch.bfloat16, 33, 40960)])
+def test_rmsnorm(gpu, dtype, M, K):
+    from torch_helion.hip import ops
+
+    announce(f"rmsnorm {dtype} M={M} K={K}")
+    g = torch.Generator().manual_seed(K)
+    x = torch.randn(M, K, generator=g).to(dtype)
+    gain = torch.rand(K, generator=g) + 0.5
+    xf = x.float()
+    ref = xf * ((xf * xf).mean(-1, keepdim=True) + 1e-5).rsqrt() * gain
+    out = torch.empty(M, K, dtype=dtype, device=gpu)
+    ops.rmsnorm(x.to(gpu), gain.to(gpu), 1e-5, out)
+    torch.cuda.synchronize()
+    if dtype == torch.float32:
+        assert _rel(out, ref) < F32_REL
+    else:
+        assert _maxabs(out, ref) < BF16_TOL
+
+
+def test_epilogue_vm(gpu):
+    from torch_helion.hip import abi, ops
+
+    announce("epilogue vm")
+    M, N = 70, 50
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(M, N, generator=g)
+    col = torch.rand(M, 1, generator=g) + 0.5
+    # y = exp(x * col - rowmax(x)) / rowsum(...)   (a softmax-like chain)
+    ref_t = x * col
+    ref_e = torch.exp(ref_t - ref_t.amax(-1, keepdim=True))
+    ref = ref_e / ref_e.sum(-1, keepdim=True)
+    ws = torch.empty(6 * M * N, device=gpu)
+    out = torch.empty(M, N, dtype=torch.bfloat16, device=gpu)
+    ops_ = [(abi.VM_LOAD, 0, 0, -1, 0.0, 0), (abi.VM_LOAD, 1, 1, -1, 0.0, 0), (abi.VM_MUL, 2, 0, 1, 0.0, 0),
+            (abi.VM_ROW_MAX, 3, 2, -1, 0.0, 0), (abi.VM_SUB, 4, 2, 3, 0.0, 0), (abi.VM_EXP, 4, 4, -1, 0.0, 0),
+            (abi.VM_ROW_SUM, 5, 4, -1, 0.0, 0), (abi.VM_DIV, 4, 4, 5, 0.0, 0), (abi.VM_MUL, 4, 4, -1, 1.0, 1)]
+    ops.epilogue_vm(M, N, [(x.to(gpu), False), (col.to(gpu), True)], ops_, [(out, 4)], 6, ws)
+    torch.cuda.synchronize()
+    assert _maxabs(out, ref) < 1e-2

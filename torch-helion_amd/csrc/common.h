@@ -1,0 +1,77 @@
+// Shared device/host helpers for the gfx950 kernels of libth_hip.so.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <string>
+
+#include "th_hip.h"
+
+namespace th {
+
+// MFMA operand / accumulator vector types (CDNA4 v_mfma_*_bf16 take 8 bf16
+// per lane; the 32x32 variants return 16 fp32 per lane).
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
+typedef __attribute__((ext_vector_type(16))) float f32x16_t;
+typedef __attribute__((ext_vector_type(4))) float f32x4_t;
+
+// ------------------------------------------------------------ bf16 helpers
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) {
+  return __uint_as_float(((uint32_t)h) << 16);
+}
+
+// Round-to-nearest-even fp32 -> bf16 (what torch's .to(bfloat16) does).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+__device__ __forceinline__ float load_elem(const void* p, int64_t i, int dtype) {
+  if (dtype == TH_BF16) return bf16_to_f32(((const uint16_t*)p)[i]);
+  return ((const float*)p)[i];
+}
+
+__device__ __forceinline__ void store_elem(void* p, int64_t i, int dtype, float v) {
+  if (dtype == TH_BF16)
+    ((uint16_t*)p)[i] = f32_to_bf16(v);
+  else
+    ((float*)p)[i] = v;
+}
+
+__device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + __expf(-x)); }
+
+// --------------------------------------------------------------- host side
+void set_error(const char* fmt, ...);
+bool device_ready();  // th_init was called for the current device
+
+#define TH_CHECK_ARG(cond, ...)            \
+  do {                                     \
+    if (!(cond)) {                         \
+      ::th::set_error(__VA_ARGS__);        \
+      return TH_ERR_INVALID;               \
+    }                                      \
+  } while (0)
+
+#define TH_CHECK_HIP(expr)                                                     \
+  do {                                                                         \
+    hipError_t e_ = (expr);                                                    \
+    if (e_ != hipSuccess) {                                                    \
+      ::th::set_error("%s failed: %s", #expr, hipGetErrorString(e_));          \
+      return TH_ERR_HIP;                                                       \
+    }                                                                          \
+  } while (0)
+
+#define TH_CHECK_LAUNCH()                                                      \
+  do {                                                                         \
+    hipError_t e_ = hipGetLastError();                                         \
+    if (e_ != hipSuccess) {                                                    \
+      ::th::set_error("kernel launch failed: %s", hipGetErrorString(e_));      \
+      return TH_ERR_HIP;                                                       \
+    }                                                                          \
+  } while (0)
+
+inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+}  // namespace th

@@ -1,0 +1,687 @@
+// OpIR `gemm` kind on CDNA4 MFMA (reference semantics: codegen/interpret.py:22-35;
+// Helion template it replaces: codegen/emit.py:71-221).
+//
+// Layout and tiling
+//   lhs    [M, K] row-major (K contiguous), bf16 or fp32.
+//   rhs    packed once by th_gemm_pack_rhs into a K-contiguous [Ncat, K] matrix
+//          whose rows interleave the n_acc operands tile by tile: block tile n
+//          holds rows (n*n_acc + i)*bn + j = column n*bn + j of operand i. A
+//          block therefore computes every accumulator of its output columns with
+//          one plain "A * B^T" main loop.
+//   bf16:  block tile BM x BNC x 64, 4 waves in a 2x2 grid, each wave a
+//          (BM/2) x (BNC/2) sub-tile of v_mfma_f32_32x32x16_bf16 ops; LDS double
+//          buffered with an XOR swizzle on 16-byte chunks (conflict-free
+//          ds_read_b128 of MFMA operands); global loads for tile k+1 are issued
+//          before the MFMAs of tile k. The RMS sum of squares of lhs rows is
+//          accumulated from the staged registers, so it costs no extra traffic.
+//   fp32:  64 x BNC x 16 tiles of v_mfma_f32_32x32x2f32.
+//   Epilogue: accumulators are staged as fp32 through LDS one half-tile at a
+//          time; every output op then reads its operands (its own column, the
+//          RoPE partner column, other accumulators) from LDS and writes 4
+//          consecutive columns per thread, so global stores are coalesced.
+#include <algorithm>
+
+#include "common.h"
+
+namespace th {
+
+struct EpiOutK {
+  int op, a, b, e;
+  void* ptr;
+  int64_t ld;
+  int dtype, vec;
+};
+
+struct GemmK {
+  const void* A;
+  int64_t lda;
+  const void* B;
+  int64_t ldb;
+  int64_t M, N, K;
+  int tiles_m, tiles_n;
+  int bn, n_acc;
+  int sumsq;
+  unsigned rscale_mask;
+  float inv_k, eps;
+  const void* extra[TH_MAX_EXTRA];
+  int64_t ld_extra[TH_MAX_EXTRA];
+  int extra_dtype[TH_MAX_EXTRA];
+  int extra_vec[TH_MAX_EXTRA];
+  const float* rcos;
+  const float* rsin;
+  int hd, period;
+  int n_out;
+  EpiOutK out[TH_MAX_OUT];
+  float* sumsq_out;
+};
+
+// Block id -> output tile. Consecutive workgroups are dealt round-robin to the
+// 8 XCDs; remap so each XCD owns a contiguous range of logical tiles, then walk
+// that range in groups of 8 tile-rows so neighbouring blocks on one XCD share
+// lhs rows and rhs columns in that XCD's L2.
+__device__ __forceinline__ void map_tile(int tiles_m, int tiles_n, int& tm, int& tn) {
+  const int nb = tiles_m * tiles_n;
+  int pid = blockIdx.x;
+  if ((nb & 7) == 0) pid = (pid & 7) * (nb >> 3) + (pid >> 3);
+  const int G = 8;
+  const int group = pid / (G * tiles_n);
+  const int first = group * G;
+  const int gm = min(tiles_m - first, G);
+  const int in_group = pid - group * G * tiles_n;
+  tm = first + in_group % gm;
+  tn = in_group / gm;
+}
+
+__device__ __forceinline__ float4 load4(const void* p, int64_t off, int dtype, bool vec, int valid) {
+  float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (vec && valid >= 4) {
+    if (dtype == TH_BF16) {
+      const uint2 w = *(const uint2*)((const uint16_t*)p + off);
+      v.x = __uint_as_float(w.x << 16);
+      v.y = __uint_as_float(w.x & 0xffff0000u);
+      v.z = __uint_as_float(w.y << 16);
+      v.w = __uint_as_float(w.y & 0xffff0000u);
+    } else {
+      v = *(const float4*)((const float*)p + off);
+    }
+    return v;
+  }
+  float t[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int q = 0; q < 4 && q < valid; ++q) t[q] = load_elem(p, off + q, dtype);
+  return make_float4(t[0], t[1], t[2], t[3]);
+}
+
+__device__ __forceinline__ void store4(void* p, int64_t off, int dtype, bool vec, int valid, float4 v) {
+  if (vec && valid >= 4) {
+    if (dtype == TH_BF16) {
+      uint2 w;
+      w.x = (uint32_t)f32_to_bf16(v.x) | ((uint32_t)f32_to_bf16(v.y) << 16);
+      w.y = (uint32_t)f32_to_bf16(v.z) | ((uint32_t)f32_to_bf16(v.w) << 16);
+      *(uint2*)((uint16_t*)p + off) = w;
+    } else {
+      *(float4*)((float*)p + off) = v;
+    }
+    return;
+  }
+  const float t[4] = {v.x, v.y, v.z, v.w};
+  for (int q = 0; q < 4 && q < valid; ++q) store_elem(p, off + q, dtype, t[q]);
+}
+
+// Evaluate every output op for the `rows` slab rows staged in LDS.
+// slab[r * srow + i * bn + j] = acc_i(row0 + r, tile_n * bn + j).
+__device__ void epilogue_slab(const GemmK& p, const float* slab, int srow, int rows,
+                              const float* rs, int64_t row0, int tile_n, int tid) {
+  const int bn = p.bn;
+  const int q4 = bn >> 2;
+  const int units = rows * q4;
+  const int64_t col0 = (int64_t)tile_n * bn;
+  for (int o = 0; o < p.n_out; ++o) {
+    const EpiOutK& eo = p.out[o];
+    const int op = eo.op;
+    const int ia = eo.a, ib = eo.b;
+    const float sa = 1.f, sb = 1.f;
+    const bool scale_a = (p.rscale_mask >> ia) & 1u;
+    const bool scale_b = ib >= 0 && ((p.rscale_mask >> ib) & 1u);
+    for (int u = tid; u < units; u += 256) {
+      const int r = u / q4;
+      const int j = (u - r * q4) << 2;
+      const int64_t gm = row0 + r;
+      const int64_t gn = col0 + j;
+      if (gm >= p.M || gn >= p.N) continue;
+      const int valid = (int)min((int64_t)4, p.N - gn);
+      const float rr = p.sumsq ? rs[r] : 1.f;
+      const float* srow_p = slab + r * srow;
+      float4 a = *(const float4*)(srow_p + ia * bn + j);
+      if (scale_a) { a.x *= rr; a.y *= rr; a.z *= rr; a.w *= rr; }
+      float4 v;
+      switch (op) {
+        case TH_EPI_ACC:
+          v = a;
+          break;
+        case TH_EPI_ROPE:
+        case TH_EPI_ROPE_PAIR: {
+          float4 rot;
+          if (op == TH_EPI_ROPE) {
+            const int hd = p.hd, half = hd >> 1;
+            const int within = (int)(gn % hd);
+            const int pj = within < half ? j + half : j - half;
+            const float sg = within < half ? -1.f : 1.f;
+            rot = *(const float4*)(srow_p + ia * bn + pj);
+            const float s2 = scale_a ? sg * rr : sg;
+            rot.x *= s2; rot.y *= s2; rot.z *= s2; rot.w *= s2;
+          } else {
+            rot = *(const float4*)(srow_p + ib * bn + j);
+            if (scale_b) { rot.x *= rr; rot.y *= rr; rot.z *= rr; rot.w *= rr; }
+          }
+          const int64_t toff = (gm % p.period) * p.hd + (gn % p.hd);
+          const float4 c = *(const float4*)(p.rcos + toff);
+          const float4 s = *(const float4*)(p.rsin + toff);
+          v.x = a.x * c.x + rot.x * s.x;
+          v.y = a.y * c.y + rot.y * s.y;
+          v.z = a.z * c.z + rot.z * s.z;
+          v.w = a.w * c.w + rot.w * s.w;
+          break;
+        }
+        case TH_EPI_SILU:
+          v.x = a.x * sigmoidf_(a.x);
+          v.y = a.y * sigmoidf_(a.y);
+          v.z = a.z * sigmoidf_(a.z);
+          v.w = a.w * sigmoidf_(a.w);
+          break;
+        case TH_EPI_SWIGLU: {
+          float4 b = *(const float4*)(srow_p + ib * bn + j);
+          if (scale_b) { b.x *= rr; b.y *= rr; b.z *= rr; b.w *= rr; }
+          v.x = a.x * sigmoidf_(a.x) * b.x;
+          v.y = a.y * sigmoidf_(a.y) * b.y;
+          v.z = a.z * sigmoidf_(a.z) * b.z;
+          v.w = a.w * sigmoidf_(a.w) * b.w;
+          break;
+        }
+        case TH_EPI_ADD:
+        case TH_EPI_SOFTPLUS_ADD:
+        case TH_EPI_MUL: {
+          const int e = eo.e;
+          const float4 x = load4(p.extra[e], gm * p.ld_extra[e] + gn, p.extra_dtype[e],
+                                 p.extra_vec[e] != 0, valid);
+          if (op == TH_EPI_MUL) {
+            v.x = a.x * x.x; v.y = a.y * x.y; v.z = a.z * x.z; v.w = a.w * x.w;
+          } else {
+            v.x = a.x + x.x; v.y = a.y + x.y; v.z = a.z + x.z; v.w = a.w + x.w;
+            if (op == TH_EPI_SOFTPLUS_ADD) {
+              v.x = __logf(1.f + __expf(v.x));
+              v.y = __logf(1.f + __expf(v.y));
+              v.z = __logf(1.f + __expf(v.z));
+              v.w = __logf(1.f + __expf(v.w));
+            }
+          }
+          break;
+        }
+        default:
+          v = a;
+          break;
+      }
+      (void)sa; (void)sb;
+      store4(eo.ptr, gm * eo.ld + gn, eo.dtype, eo.vec != 0, valid, v);
+    }
+  }
+}
+
+__device__ __forceinline__ float sumsq8_bf16(uint4 w) {
+  float s = 0.f;
+  const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const float lo = __uint_as_float(ws[q] << 16);
+    const float hi = __uint_as_float(ws[q] & 0xffff0000u);
+    s += lo * lo + hi * hi;
+  }
+  return s;
+}
+
+// --------------------------------------------------------------- bf16 MFMA
+template <int BM, int BNC>
+__global__ void __launch_bounds__(256, 1) gemm_bf16_kernel(GemmK p) {
+  constexpr int BK = 64;
+  constexpr int WM = BM / 2, WN = BNC / 2;
+  constexpr int TM = WM / 32, TN = WN / 32;
+  constexpr int AC = BM / 32, BC = BNC / 32;  // 16-byte chunks per thread
+  constexpr int TILE_BYTES = (BM + BNC) * BK * 2;
+  constexpr int SROW = BNC + 8;
+  constexpr int EPI_BYTES = WM * SROW * 4;
+  constexpr int MAIN_BYTES = 2 * TILE_BYTES;
+  constexpr int BODY = MAIN_BYTES > EPI_BYTES ? MAIN_BYTES : EPI_BYTES;
+  __shared__ __attribute__((aligned(16))) char smem[BODY + BM * 4];
+  float* rs = (float*)(smem + BODY);
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  int tmi, tni;
+  map_tile(p.tiles_m, p.tiles_n, tmi, tni);
+  const int64_t m0 = (int64_t)tmi * BM;
+  const uint16_t* A = (const uint16_t*)p.A;
+  const uint16_t* B = (const uint16_t*)p.B + (int64_t)tni * BNC * p.ldb;
+  const int lrow = tid >> 3, lch = tid & 7;
+  const int nk = (int)((p.K + BK - 1) / BK);
+
+  uint4 ra[AC], rb[BC];
+  float ss[AC];
+  f32x16_t acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < AC; ++i) ss[i] = 0.f;
+#pragma unroll
+  for (int t = 0; t < TM; ++t)
+#pragma unroll
+    for (int u = 0; u < TN; ++u)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[t][u][r] = 0.f;
+
+  auto gload = [&](int kt) {
+    const int64_t k = (int64_t)kt * BK + lch * 8;
+    const bool kin = k < p.K;
+#pragma unroll
+    for (int i = 0; i < AC; ++i) {
+      const int64_t r = m0 + lrow + 32 * i;
+      ra[i] = (kin && r < p.M) ? *(const uint4*)(A + r * p.lda + k) : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < BC; ++i)
+      rb[i] = kin ? *(const uint4*)(B + (int64_t)(lrow + 32 * i) * p.ldb + k) : make_uint4(0, 0, 0, 0);
+  };
+  auto sstore = [&](int buf) {
+    char* sa = smem + buf * TILE_BYTES;
+    char* sb = sa + BM * BK * 2;
+    const int sw = lch ^ (lrow & 7);
+#pragma unroll
+    for (int i = 0; i < AC; ++i) *(uint4*)(sa + (lrow + 32 * i) * 128 + (sw << 4)) = ra[i];
+#pragma unroll
+    for (int i = 0; i < BC; ++i) *(uint4*)(sb + (lrow + 32 * i) * 128 + (sw << 4)) = rb[i];
+    if (p.sumsq) {
+#pragma unroll
+      for (int i = 0; i < AC; ++i) ss[i] += sumsq8_bf16(ra[i]);
+    }
+  };
+  auto compute = [&](int buf) {
+    const char* sa = smem + buf * TILE_BYTES;
+    const char* sb = sa + BM * BK * 2;
+#pragma unroll
+    for (int ks = 0; ks < BK / 16; ++ks) {
+      const int c = ((ks * 2 + (lane >> 5)) ^ (lane & 7)) << 4;
+      bf16x8_t af[TM], bfv[TN];
+#pragma unroll
+      for (int t = 0; t < TM; ++t)
+        af[t] = *(const bf16x8_t*)(sa + (wm * WM + t * 32 + (lane & 31)) * 128 + c);
+#pragma unroll
+      for (int u = 0; u < TN; ++u)
+        bfv[u] = *(const bf16x8_t*)(sb + (wn * WN + u * 32 + (lane & 31)) * 128 + c);
+#pragma unroll
+      for (int t = 0; t < TM; ++t)
+#pragma unroll
+        for (int u = 0; u < TN; ++u)
+          acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[t], bfv[u], acc[t][u], 0, 0, 0);
+    }
+  };
+
+  gload(0);
+  sstore(0);
+  __syncthreads();
+  for (int kt = 0; kt < nk; ++kt) {
+    const int cur = kt & 1;
+    if (kt + 1 < nk) gload(kt + 1);
+    compute(cur);
+    if (kt + 1 < nk) sstore(cur ^ 1);
+    __syncthreads();
+  }
+
+  if (p.sumsq) {
+#pragma unroll
+    for (int i = 0; i < AC; ++i) {
+      float v = ss[i];
+      v += __shfl_xor(v, 1);
+      v += __shfl_xor(v, 2);
+      v += __shfl_xor(v, 4);
+      if (lch == 0) {
+        const int r = lrow + 32 * i;
+        rs[r] = rsqrtf(v * p.inv_k + p.eps);
+        const int64_t gr = m0 + r;
+        if (p.sumsq_out && tni == 0 && gr < p.M) p.sumsq_out[gr] = v;
+      }
+    }
+  }
+
+  float* slab = (float*)smem;
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    if (wm == s) {
+#pragma unroll
+      for (int t = 0; t < TM; ++t)
+#pragma unroll
+        for (int u = 0; u < TN; ++u)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int row = t * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            const int col = wn * WN + u * 32 + (lane & 31);
+            slab[row * SROW + col] = acc[t][u][r];
+          }
+    }
+    __syncthreads();
+    epilogue_slab(p, slab, SROW, WM, rs + s * WM, m0 + s * WM, tni, tid);
+    __syncthreads();
+  }
+}
+
+// --------------------------------------------------------------- fp32 MFMA
+template <int BNC>
+__global__ void __launch_bounds__(256, 1) gemm_f32_kernel(GemmK p) {
+  constexpr int BM = 64, BK = 16, RSF = 20;  // LDS row stride in floats (80 B)
+  constexpr int WM = 32, WN = BNC / 2, TN = WN / 32;
+  constexpr int BC = BNC / 64;
+  constexpr int TILE_FLOATS = (BM + BNC) * RSF;
+  constexpr int SROW = BNC + 8;
+  constexpr int EPI_FLOATS = WM * SROW;
+  constexpr int MAIN_FLOATS = 2 * TILE_FLOATS;
+  constexpr int BODY = MAIN_FLOATS > EPI_FLOATS ? MAIN_FLOATS : EPI_FLOATS;
+  __shared__ __attribute__((aligned(16))) float smem[BODY + BM];
+  float* rs = smem + BODY;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  int tmi, tni;
+  map_tile(p.tiles_m, p.tiles_n, tmi, tni);
+  const int64_t m0 = (int64_t)tmi * BM;
+  const float* A = (const float*)p.A;
+  const float* B = (const float*)p.B + (int64_t)tni * BNC * p.ldb;
+  const int lrow = tid >> 2, lch = tid & 3;
+  const int nk = (int)((p.K + BK - 1) / BK);
+
+  float4 ra, rb[BC];
+  float ss = 0.f;
+  f32x16_t acc[TN];
+#pragma unroll
+  for (int u = 0; u < TN; ++u)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[u][r] = 0.f;
+
+  auto gload = [&](int kt) {
+    const int64_t k = (int64_t)kt * BK + lch * 4;
+    const bool kin = k < p.K;
+    const int64_t r = m0 + lrow;
+    ra = (kin && r < p.M) ? *(const float4*)(A + r * p.lda + k) : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int i = 0; i < BC; ++i)
+      rb[i] = kin ? *(const float4*)(B + (int64_t)(lrow + 64 * i) * p.ldb + k) : make_float4(0.f, 0.f, 0.f, 0.f);
+  };
+  auto sstore = [&](int buf) {
+    float* sa = smem + buf * TILE_FLOATS;
+    float* sb = sa + BM * RSF;
+    *(float4*)(sa + lrow * RSF + lch * 4) = ra;
+#pragma unroll
+    for (int i = 0; i < BC; ++i) *(float4*)(sb + (lrow + 64 * i) * RSF + lch * 4) = rb[i];
+    if (p.sumsq) ss += ra.x * ra.x + ra.y * ra.y + ra.z * ra.z + ra.w * ra.w;
+  };
+  auto compute = [&](int buf) {
+    const float* sa = smem + buf * TILE_FLOATS;
+    const float* sb = sa + BM * RSF;
+#pragma unroll
+    for (int ks = 0; ks < BK / 2; ++ks) {
+      const int k = ks * 2 + (lane >> 5);
+      const float a = sa[(wm * WM + (lane & 31)) * RSF + k];
+#pragma unroll
+      for (int u = 0; u < TN; ++u) {
+        const float b = sb[(wn * WN + u * 32 + (lane & 31)) * RSF + k];
+        acc[u] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, acc[u], 0, 0, 0);
+      }
+    }
+  };
+
+  gload(0);
+  sstore(0);
+  __syncthreads();
+  for (int kt = 0; kt < nk; ++kt) {
+    const int cur = kt & 1;
+    if (kt + 1 < nk) gload(kt + 1);
+    compute(cur);
+    if (kt + 1 < nk) sstore(cur ^ 1);
+    __syncthreads();
+  }
+
+  if (p.sumsq) {
+    float v = ss;
+    v += __shfl_xor(v, 1);
+    v += __shfl_xor(v, 2);
+    if (lch == 0) {
+      rs[lrow] = rsqrtf(v * p.inv_k + p.eps);
+      const int64_t gr = m0 + lrow;
+      if (p.sumsq_out && tni == 0 && gr < p.M) p.sumsq_out[gr] = v;
+    }
+  }
+
+  float* slab = smem;
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    if (wm == s) {
+#pragma unroll
+      for (int u = 0; u < TN; ++u)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int row = 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+          const int col = wn * WN + u * 32 + (lane & 31);
+          slab[row * SROW + col] = acc[u][r];
+        }
+    }
+    __syncthreads();
+    epilogue_slab(p, slab, SROW, WM, rs + s * WM, m0 + s * WM, tni, tid);
+    __syncthreads();
+  }
+}
+
+// ------------------------------------------------------------------ packing
+struct PackK {
+  const void* src[TH_MAX_ACC];
+  int64_t ld[TH_MAX_ACC];
+  int src_dtype, out_dtype;
+  int64_t N, K, Kp, rows;
+  int bn, bnc;
+  void* out;
+};
+
+// out[r][k] = src_i[k][t*bn + j] with r = t*bnc + i*bn + j; zero outside N, K.
+__global__ void __launch_bounds__(256) pack_rhs_kernel(PackK p) {
+  __shared__ float tile[32][33];
+  const int64_t k0 = (int64_t)blockIdx.x * 32, r0 = (int64_t)blockIdx.y * 32;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+  {
+    const int64_t r = r0 + tx;
+    const int64_t t = r / p.bnc, rem = r - t * p.bnc;
+    const int i = (int)(rem / p.bn);
+    const int64_t n = t * p.bn + (rem - (int64_t)i * p.bn);
+    for (int yy = ty; yy < 32; yy += 8) {
+      const int64_t k = k0 + yy;
+      float v = 0.f;
+      if (r < p.rows && k < p.K && n < p.N) v = load_elem(p.src[i], k * p.ld[i] + n, p.src_dtype);
+      tile[yy][tx] = v;
+    }
+  }
+  __syncthreads();
+  for (int yy = ty; yy < 32; yy += 8) {
+    const int64_t r = r0 + yy, k = k0 + tx;
+    if (r < p.rows && k < p.Kp) store_elem(p.out, r * p.Kp + k, p.out_dtype, tile[tx][yy]);
+  }
+}
+
+// Per-accumulator column tile bn; the block tile is n_acc * bn columns.
+static int choose_bn(int64_t N, int n_acc, int in_dtype) {
+  if (in_dtype == TH_F32) {
+    switch (n_acc) {
+      case 1: return N > 64 ? 128 : 64;
+      case 2: return N > 32 ? 64 : 32;
+      case 3: return 64;
+      default: return N > 32 ? 64 : 32;
+    }
+  }
+  switch (n_acc) {
+    case 1: return N >= 192 ? 256 : (N > 64 ? 128 : 64);
+    case 2: return N >= 128 ? 128 : (N > 32 ? 64 : 32);
+    case 3: return 64;
+    default: return N > 32 ? 64 : 32;
+  }
+}
+
+static int64_t packed_kp(int64_t K, int in_dtype) {
+  const int64_t a = in_dtype == TH_F32 ? 4 : 8;
+  return (K + a - 1) / a * a;
+}
+
+static bool aligned(const void* p, int bytes) { return ((uintptr_t)p % bytes) == 0; }
+
+}  // namespace th
+
+using namespace th;
+
+extern "C" int th_gemm_acc_tile(int64_t N, int32_t n_acc, int32_t in_dtype) {
+  if (N <= 0 || n_acc < 1 || n_acc > TH_MAX_ACC) return 0;
+  return choose_bn(N, n_acc, in_dtype);
+}
+
+extern "C" int64_t th_gemm_packed_bytes(int64_t N, int64_t K, int32_t n_acc, int32_t in_dtype) {
+  if (N <= 0 || K <= 0 || n_acc < 1 || n_acc > TH_MAX_ACC) return -1;
+  if (in_dtype != TH_BF16 && in_dtype != TH_F32) return -1;
+  const int bn = choose_bn(N, n_acc, in_dtype);
+  const int64_t rows = cdiv(N, bn) * bn * n_acc;
+  return rows * packed_kp(K, in_dtype) * (in_dtype == TH_F32 ? 4 : 2);
+}
+
+extern "C" int th_gemm_pack_rhs(const void* const* src, const int64_t* ld_src, int32_t src_dtype,
+                                int64_t N, int64_t K, int32_t n_acc, int32_t in_dtype, void* packed,
+                                void* stream) {
+  TH_CHECK_ARG(src && ld_src && packed, "th_gemm_pack_rhs: null pointer argument");
+  TH_CHECK_ARG(N > 0 && K > 0, "th_gemm_pack_rhs: N=%lld K=%lld must be positive", (long long)N, (long long)K);
+  TH_CHECK_ARG(n_acc >= 1 && n_acc <= TH_MAX_ACC, "th_gemm_pack_rhs: n_acc=%d out of range", n_acc);
+  TH_CHECK_ARG(in_dtype == TH_BF16 || in_dtype == TH_F32, "th_gemm_pack_rhs: in_dtype %d unsupported", in_dtype);
+  TH_CHECK_ARG(src_dtype == TH_BF16 || src_dtype == TH_F32, "th_gemm_pack_rhs: src_dtype %d unsupported", src_dtype);
+  PackK p{};
+  for (int i = 0; i < n_acc; ++i) {
+    TH_CHECK_ARG(src[i] != nullptr, "th_gemm_pack_rhs: src[%d] is null", i);
+    TH_CHECK_ARG(ld_src[i] >= N, "th_gemm_pack_rhs: ld_src[%d]=%lld < N", i, (long long)ld_src[i]);
+    p.src[i] = src[i];
+    p.ld[i] = ld_src[i];
+  }
+  if (!device_ready()) {
+    set_error("th_gemm_pack_rhs: th_init was not called for the current device");
+    return TH_ERR_NOT_INIT;
+  }
+  p.src_dtype = src_dtype;
+  p.out_dtype = in_dtype;
+  p.N = N;
+  p.K = K;
+  p.Kp = packed_kp(K, in_dtype);
+  p.bn = choose_bn(N, n_acc, in_dtype);
+  p.bnc = p.bn * n_acc;
+  p.rows = cdiv(N, p.bn) * p.bnc;
+  p.out = packed;
+  dim3 grid((unsigned)cdiv(p.Kp, 32), (unsigned)cdiv(p.rows, 32));
+  hipLaunchKernelGGL(pack_rhs_kernel, grid, dim3(256), 0, (hipStream_t)stream, p);
+  TH_CHECK_LAUNCH();
+  return TH_OK;
+}
+
+template <int BM, int BNC>
+static void launch_bf16(const GemmK& k, hipStream_t s) {
+  hipLaunchKernelGGL((gemm_bf16_kernel<BM, BNC>), dim3(k.tiles_m * k.tiles_n), dim3(256), 0, s, k);
+}
+
+template <int BNC>
+static void launch_f32(const GemmK& k, hipStream_t s) {
+  hipLaunchKernelGGL((gemm_f32_kernel<BNC>), dim3(k.tiles_m * k.tiles_n), dim3(256), 0, s, k);
+}
+
+extern "C" int th_gemm(const th_gemm_desc* d, void* stream) {
+  TH_CHECK_ARG(d != nullptr, "th_gemm: null descriptor");
+  TH_CHECK_ARG(d->M > 0 && d->N > 0 && d->K > 0, "th_gemm: M=%lld N=%lld K=%lld must be positive",
+               (long long)d->M, (long long)d->N, (long long)d->K);
+  TH_CHECK_ARG(d->n_acc >= 1 && d->n_acc <= TH_MAX_ACC, "th_gemm: n_acc=%d out of range 1..%d", d->n_acc, TH_MAX_ACC);
+  TH_CHECK_ARG(d->in_dtype == TH_BF16 || d->in_dtype == TH_F32, "th_gemm: in_dtype %d unsupported", d->in_dtype);
+  TH_CHECK_ARG(d->lhs && d->rhs_packed, "th_gemm: null lhs or rhs_packed");
+  const int align = d->in_dtype == TH_F32 ? 4 : 8;
+  TH_CHECK_ARG(d->K % align == 0, "th_gemm: K=%lld must be a multiple of %d", (long long)d->K, align);
+  TH_CHECK_ARG(d->ld_lhs >= d->K && d->ld_lhs % align == 0, "th_gemm: ld_lhs=%lld invalid", (long long)d->ld_lhs);
+  TH_CHECK_ARG(aligned(d->lhs, 16) && aligned(d->rhs_packed, 16), "th_gemm: lhs/rhs_packed must be 16-byte aligned");
+  TH_CHECK_ARG(d->n_out >= 1 && d->n_out <= TH_MAX_OUT, "th_gemm: n_out=%d out of range", d->n_out);
+  TH_CHECK_ARG(d->n_extra >= 0 && d->n_extra <= TH_MAX_EXTRA, "th_gemm: n_extra=%d out of range", d->n_extra);
+  TH_CHECK_ARG(d->rscale_mask == 0 || d->sumsq, "th_gemm: rscale_mask set without sumsq");
+  const int bn = choose_bn(d->N, d->n_acc, d->in_dtype);
+  GemmK k{};
+  k.A = d->lhs;
+  k.lda = d->ld_lhs;
+  k.B = d->rhs_packed;
+  k.ldb = packed_kp(d->K, d->in_dtype);
+  k.M = d->M;
+  k.N = d->N;
+  k.K = d->K;
+  k.bn = bn;
+  k.n_acc = d->n_acc;
+  k.sumsq = d->sumsq ? 1 : 0;
+  k.rscale_mask = d->rscale_mask;
+  k.inv_k = d->inv_k;
+  k.eps = d->eps;
+  for (int e = 0; e < d->n_extra; ++e) {
+    TH_CHECK_ARG(d->extra[e] != nullptr, "th_gemm: extra[%d] is null", e);
+    TH_CHECK_ARG(d->extra_dtype[e] == TH_BF16 || d->extra_dtype[e] == TH_F32, "th_gemm: extra_dtype[%d] unsupported", e);
+    TH_CHECK_ARG(d->ld_extra[e] >= d->N, "th_gemm: ld_extra[%d] < N", e);
+    k.extra[e] = d->extra[e];
+    k.ld_extra[e] = d->ld_extra[e];
+    k.extra_dtype[e] = d->extra_dtype[e];
+    const int eb = d->extra_dtype[e] == TH_F32 ? 16 : 8;
+    k.extra_vec[e] = aligned(d->extra[e], eb) && d->ld_extra[e] % 4 == 0;
+  }
+  bool need_rope = false;
+  for (int o = 0; o < d->n_out; ++o) {
+    const th_epi_out& eo = d->out[o];
+    TH_CHECK_ARG(eo.op >= TH_EPI_ACC && eo.op <= TH_EPI_MUL, "th_gemm: out[%d].op=%d unknown", o, eo.op);
+    TH_CHECK_ARG(eo.a >= 0 && eo.a < d->n_acc, "th_gemm: out[%d].a=%d out of range", o, eo.a);
+    const bool uses_b = eo.op == TH_EPI_ROPE_PAIR || eo.op == TH_EPI_SWIGLU;
+    TH_CHECK_ARG(!uses_b || (eo.b >= 0 && eo.b < d->n_acc), "th_gemm: out[%d].b=%d out of range", o, eo.b);
+    const bool uses_e = eo.op == TH_EPI_ADD || eo.op == TH_EPI_SOFTPLUS_ADD || eo.op == TH_EPI_MUL;
+    TH_CHECK_ARG(!uses_e || (eo.e >= 0 && eo.e < d->n_extra), "th_gemm: out[%d].e=%d out of range", o, eo.e);
+    TH_CHECK_ARG(eo.ptr != nullptr && eo.ld >= d->N, "th_gemm: out[%d] null or ld < N", o);
+    TH_CHECK_ARG(eo.dtype == TH_BF16 || eo.dtype == TH_F32, "th_gemm: out[%d].dtype unsupported", o);
+    need_rope |= eo.op == TH_EPI_ROPE || eo.op == TH_EPI_ROPE_PAIR;
+    k.out[o].op = eo.op;
+    k.out[o].a = eo.a;
+    k.out[o].b = uses_b ? eo.b : -1;
+    k.out[o].e = uses_e ? eo.e : -1;
+    k.out[o].ptr = eo.ptr;
+    k.out[o].ld = eo.ld;
+    k.out[o].dtype = eo.dtype;
+    const int ob = eo.dtype == TH_F32 ? 16 : 8;
+    k.out[o].vec = aligned(eo.ptr, ob) && eo.ld % 4 == 0;
+    if (eo.op == TH_EPI_ROPE) {
+      TH_CHECK_ARG(d->rope_head_dim > 0 && bn % d->rope_head_dim == 0,
+                   "th_gemm: fused RoPE needs the column tile (%d) to hold whole heads (head_dim %d)", bn,
+                   d->rope_head_dim);
+    }
+  }
+  k.n_out = d->n_out;
+  if (need_rope) {
+    TH_CHECK_ARG(d->rope_cos && d->rope_sin, "th_gemm: RoPE output without cos/sin tables");
+    TH_CHECK_ARG(d->rope_head_dim >= 4 && d->rope_head_dim % 8 == 0 && d->N % d->rope_head_dim == 0,
+                 "th_gemm: rope_head_dim=%d invalid for N=%lld", d->rope_head_dim, (long long)d->N);
+    TH_CHECK_ARG(d->rope_period > 0, "th_gemm: rope_period must be positive");
+    TH_CHECK_ARG(aligned(d->rope_cos, 16) && aligned(d->rope_sin, 16), "th_gemm: RoPE tables must be 16-byte aligned");
+  }
+  k.rcos = d->rope_cos;
+  k.rsin = d->rope_sin;
+  k.hd = d->rope_head_dim > 0 ? d->rope_head_dim : 1;
+  k.period = d->rope_period > 0 ? d->rope_period : 1;
+  k.sumsq_out = d->sumsq_out;
+  if (!device_ready()) {
+    set_error("th_gemm: th_init was not called for the current device");
+    return TH_ERR_NOT_INIT;
+  }
+
+  hipStream_t s = (hipStream_t)stream;
+  const int bnc = bn * d->n_acc;
+  k.tiles_n = (int)cdiv(d->N, bn);
+  if (d->in_dtype == TH_F32) {
+    k.tiles_m = (int)cdiv(d->M, 64);
+    switch (bnc) {
+      case 64: launch_f32<64>(k, s); break;
+      case 128: launch_f32<128>(k, s); break;
+      case 192: launch_f32<192>(k, s); break;
+      case 256: launch_f32<256>(k, s); break;
+      default: set_error("th_gemm: no fp32 kernel for tile %d", bnc); return TH_ERR_UNSUPPORTED;
+    }
+  } else {
+    const int64_t big_blocks = cdiv(d->M, 256) * k.tiles_n;
+    const bool big = big_blocks >= 512;
+    k.tiles_m = (int)cdiv(d->M, big ? 256 : 128);
+    switch (bnc) {
+      case 64: big ? launch_bf16<256, 64>(k, s) : launch_bf16<128, 64>(k, s); break;
+      case 128: big ? launch_bf16<256, 128>(k, s) : launch_bf16<128, 128>(k, s); break;
+      case 192: big ? launch_bf16<256, 192>(k, s) : launch_bf16<128, 192>(k, s); break;
+      case 256: big ? launch_bf16<256, 256>(k, s) : launch_bf16<128, 256>(k, s); break;
+      default: set_error("th_gemm: no bf16 kernel for tile %d", bnc); return TH_ERR_UNSUPPORTED;
+    }
+  }
+  TH_CHECK_LAUNCH();
+  return TH_OK;
+}

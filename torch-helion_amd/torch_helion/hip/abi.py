@@ -1,0 +1,177 @@
+"""ctypes mirror of ``include/th_hip.h`` and loader of ``libth_hip.so``.
+
+The structures below follow the header field by field (the CPU test
+``tests/test_abi.py`` compiles the header with gcc and compares every
+offset). The library is loaded lazily, after ``import torch``, so it binds to
+the HIP runtime torch has already mapped.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+from pathlib import Path
+
+from .build import LIB_PATH
+
+ABI_VERSION = 1
+
+# th_status
+TH_OK = 0
+TH_ERR_INVALID = -1
+TH_ERR_UNSUPPORTED = -2
+TH_ERR_HIP = -3
+TH_ERR_NOT_INIT = -4
+
+# th_dtype
+TH_F32, TH_BF16, TH_F16, TH_F8E4M3, TH_I32, TH_I64 = range(6)
+
+# th_epi_op
+EPI_ACC, EPI_ROPE, EPI_ROPE_PAIR, EPI_SILU, EPI_SWIGLU, EPI_ADD, EPI_SOFTPLUS_ADD, EPI_MUL = range(8)
+
+MAX_ACC, MAX_OUT, MAX_EXTRA = 4, 6, 4
+VM_MAX_IN, VM_MAX_OPS, VM_MAX_OUT = 16, 96, 8
+
+# th_vm_code
+(VM_LOAD, VM_ADD, VM_SUB, VM_MUL, VM_DIV, VM_MAX, VM_POW, VM_EXP, VM_LOG,
+ VM_ROW_SUM, VM_ROW_MAX, VM_COPY) = range(12)
+
+TORCH_TO_TH = {"float32": TH_F32, "bfloat16": TH_BF16, "float16": TH_F16, "float8_e4m3fn": TH_F8E4M3,
+               "int32": TH_I32, "int64": TH_I64}
+
+_p = C.c_void_p
+_i32 = C.c_int32
+_i64 = C.c_int64
+
+
+class EpiOut(C.Structure):
+    _fields_ = [("op", _i32), ("a", _i32), ("b", _i32), ("e", _i32), ("ptr", _p), ("ld", _i64),
+                ("dtype", _i32), ("pad_", _i32)]
+
+
+class GemmDesc(C.Structure):
+    _fields_ = [
+        ("M", _i64), ("N", _i64), ("K", _i64),
+        ("n_acc", _i32), ("in_dtype", _i32),
+        ("lhs", _p), ("ld_lhs", _i64), ("rhs_packed", _p),
+        ("sumsq", _i32), ("rscale_mask", C.c_uint32), ("inv_k", C.c_float), ("eps", C.c_float),
+        ("n_extra", _i32), ("pad_", _i32),
+        ("extra", _p * MAX_EXTRA), ("ld_extra", _i64 * MAX_EXTRA), ("extra_dtype", _i32 * MAX_EXTRA),
+        ("rope_cos", _p), ("rope_sin", _p),
+        ("rope_head_dim", _i32), ("rope_period", _i32), ("n_out", _i32), ("pad2_", _i32),
+        ("out", EpiOut * MAX_OUT),
+        ("sumsq_out", _p),
+    ]
+
+
+class RmsNormDesc(C.Structure):
+    _fields_ = [
+        ("M", _i64), ("K", _i64),
+        ("x", _p), ("ld_x", _i64), ("x_dtype", _i32), ("out_dtype", _i32),
+        ("gain", _p), ("out", _p), ("ld_out", _i64), ("inv_k", C.c_float), ("eps", C.c_float),
+    ]
+
+
+class AttnDesc(C.Structure):
+    _fields_ = [
+        ("batch", _i32), ("seq_q", _i32), ("seq_kv", _i32), ("heads_q", _i32), ("heads_kv", _i32),
+        ("head_dim", _i32), ("scale", C.c_float), ("causal", _i32), ("dtype", _i32), ("pad_", _i32),
+        ("q", _p), ("ld_q", _i64), ("k", _p), ("ld_k", _i64), ("v", _p), ("ld_v", _i64),
+        ("o", _p), ("ld_o", _i64),
+    ]
+
+
+class VmOperand(C.Structure):
+    _fields_ = [("ptr", _p), ("ld", _i64), ("dtype", _i32), ("column", _i32)]
+
+
+class VmOp(C.Structure):
+    _fields_ = [("code", _i32), ("dst", _i32), ("a", _i32), ("b", _i32), ("scalar", C.c_float), ("mode", _i32)]
+
+
+class VmOut(C.Structure):
+    _fields_ = [("ptr", _p), ("ld", _i64), ("dtype", _i32), ("slot", _i32)]
+
+
+class VmDesc(C.Structure):
+    _fields_ = [
+        ("M", _i64), ("N", _i64),
+        ("n_in", _i32), ("n_ops", _i32), ("n_out", _i32), ("n_slots", _i32),
+        ("in_", VmOperand * VM_MAX_IN), ("ops", VmOp * VM_MAX_OPS), ("out", VmOut * VM_MAX_OUT),
+        ("workspace", _p),
+    ]
+
+
+# entry point name -> (restype, argtypes); every symbol include/th_hip.h declares
+SIGNATURES: dict[str, tuple] = {
+    "th_abi_version": (_i32, []),
+    "th_init": (_i32, [_i32]),
+    "th_last_error": (C.c_char_p, []),
+    "th_gemm_acc_tile": (_i32, [_i64, _i32, _i32]),
+    "th_gemm_packed_bytes": (_i64, [_i64, _i64, _i32, _i32]),
+    "th_gemm_pack_rhs": (_i32, [C.POINTER(_p), C.POINTER(_i64), _i32, _i64, _i64, _i32, _i32, _p, _p]),
+    "th_gemm": (_i32, [C.POINTER(GemmDesc), _p]),
+    "th_rmsnorm": (_i32, [C.POINTER(RmsNormDesc), _p]),
+    "th_attention_prefill": (_i32, [C.POINTER(AttnDesc), _p]),
+    "th_epilogue_vm": (_i32, [C.POINTER(VmDesc), _p]),
+}
+
+
+class HipBackendError(RuntimeError):
+    """A libth_hip.so entry point returned an error status."""
+
+    def __init__(self, entry: str, status: int, message: str, kernel: str | None = None) -> None:
+        where = f" [{kernel}]" if kernel else ""
+        super().__init__(f"{entry}{where} failed with status {status}: {message}")
+        self.entry, self.status, self.kernel = entry, status, kernel
+
+
+_LIB: C.CDLL | None = None
+
+
+def library_path() -> Path:
+    return LIB_PATH
+
+
+def load(path: str | Path | None = None) -> C.CDLL:
+    """Load libth_hip.so (raises if it has not been built)."""
+    global _LIB
+    if _LIB is not None and path is None:
+        return _LIB
+    p = Path(path) if path else LIB_PATH
+    if not p.exists():
+        raise HipBackendError("load", TH_ERR_NOT_INIT,
+                              f"{p} is missing; build it with __graft_entry__.build() "
+                              f"or python torch-helion_amd/torch_helion/hip/build.py")
+    import torch  # noqa: F401  -- map torch's HIP runtime first (one runtime per process)
+
+    lib = C.CDLL(str(p))
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    if lib.th_abi_version() != ABI_VERSION:
+        raise HipBackendError("load", TH_ERR_INVALID, f"ABI version {lib.th_abi_version()} != {ABI_VERSION}")
+    if path is None:
+        _LIB = lib
+    return lib
+
+
+def last_error(lib: C.CDLL | None = None) -> str:
+    lib = lib or load()
+    return (lib.th_last_error() or b"").decode(errors="replace")
+
+
+def check(status: int, entry: str, kernel: str | None = None) -> None:
+    if status != TH_OK:
+        raise HipBackendError(entry, status, last_error(), kernel)
+
+
+_INIT: set[int] = set()
+
+
+def init_device(device: int) -> C.CDLL:
+    lib = load()
+    if device not in _INIT:
+        check(lib.th_init(device), "th_init")
+        _INIT.add(device)
+    return lib

@@ -1,0 +1,197 @@
+"""Python entry points over the C ABI, taking torch device tensors.
+
+Each function fills one descriptor of ``include/th_hip.h`` and launches on the
+current torch stream. No function here computes anything on the host: if the
+library is missing or the device is not gfx950 they raise
+:class:`~torch_helion.hip.abi.HipBackendError`.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass, field
+from typing import Sequence
+
+import torch
+
+from . import abi
+
+_DT = {torch.float32: abi.TH_F32, torch.bfloat16: abi.TH_BF16, torch.float16: abi.TH_F16}
+
+
+def th_dtype(t: torch.Tensor | torch.dtype) -> int:
+    dt = t if isinstance(t, torch.dtype) else t.dtype
+    if dt not in _DT:
+        raise abi.HipBackendError("dtype", abi.TH_ERR_UNSUPPORTED, f"{dt} has no kernel")
+    return _DT[dt]
+
+
+def _lib(t: torch.Tensor) -> C.CDLL:
+    if t.device.type != "cuda":
+        raise abi.HipBackendError("device", abi.TH_ERR_INVALID, f"tensor on {t.device}, expected a HIP device")
+    return abi.init_device(t.device.index or 0)
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _row_major(t: torch.Tensor, name: str) -> int:
+    """Row stride of a 2-D tensor whose last dim is contiguous."""
+    if t.dim() != 2 or t.stride(1) != 1:
+        raise abi.HipBackendError(name, abi.TH_ERR_INVALID, f"expected a 2-D row-major tensor, got {tuple(t.shape)} strides {t.stride()}")
+    return t.stride(0)
+
+
+# ------------------------------------------------------------------ gemm
+def acc_tile(n: int, n_acc: int, dtype: torch.dtype) -> int:
+    return int(abi.load().th_gemm_acc_tile(n, n_acc, th_dtype(dtype)))
+
+
+def pack_rhs(ws: Sequence[torch.Tensor], dtype: torch.dtype, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Pack [K, N] operands into th_gemm's K-contiguous interleaved layout."""
+    lib = _lib(ws[0])
+    k, n = ws[0].shape
+    for w in ws:
+        if tuple(w.shape) != (k, n) or w.dtype != ws[0].dtype:
+            raise abi.HipBackendError("th_gemm_pack_rhs", abi.TH_ERR_INVALID, "operands differ in shape/dtype")
+    nbytes = lib.th_gemm_packed_bytes(n, k, len(ws), th_dtype(dtype))
+    if nbytes <= 0:
+        raise abi.HipBackendError("th_gemm_packed_bytes", abi.TH_ERR_INVALID, f"N={n} K={k} n_acc={len(ws)}")
+    if out is None:
+        out = torch.empty(nbytes, dtype=torch.uint8, device=ws[0].device)
+    elif out.numel() * out.element_size() < nbytes:
+        raise abi.HipBackendError("th_gemm_pack_rhs", abi.TH_ERR_INVALID, "packed buffer too small")
+    ptrs = (C.c_void_p * len(ws))(*[w.data_ptr() for w in ws])
+    lds = (C.c_int64 * len(ws))(*[_row_major(w, "pack_rhs") for w in ws])
+    abi.check(lib.th_gemm_pack_rhs(ptrs, lds, th_dtype(ws[0]), n, k, len(ws), th_dtype(dtype), out.data_ptr(),
+                                   _stream(ws[0])), "th_gemm_pack_rhs")
+    return out
+
+
+@dataclass
+class EpiSpec:
+    """One fused output of th_gemm (see th_epi_op in include/th_hip.h)."""
+
+    op: int
+    out: torch.Tensor
+    a: int = 0
+    b: int = -1
+    e: int = -1
+
+
+@dataclass
+class GemmCall:
+    M: int
+    N: int
+    K: int
+    n_acc: int
+    lhs: torch.Tensor
+    packed: torch.Tensor
+    outs: list[EpiSpec]
+    sumsq: bool = False
+    rscale_mask: int = 0
+    inv_k: float = 0.0
+    eps: float = 0.0
+    extras: list[torch.Tensor] = field(default_factory=list)
+    rope_cos: torch.Tensor | None = None
+    rope_sin: torch.Tensor | None = None
+    rope_head_dim: int = 0
+    rope_period: int = 0
+    sumsq_out: torch.Tensor | None = None
+
+    def descriptor(self) -> abi.GemmDesc:
+        d = abi.GemmDesc()
+        d.M, d.N, d.K, d.n_acc = self.M, self.N, self.K, self.n_acc
+        d.in_dtype = th_dtype(self.lhs)
+        d.lhs = self.lhs.data_ptr()
+        d.ld_lhs = _row_major(self.lhs, "th_gemm lhs")
+        d.rhs_packed = self.packed.data_ptr()
+        d.sumsq = 1 if self.sumsq else 0
+        d.rscale_mask = self.rscale_mask
+        d.inv_k, d.eps = self.inv_k, self.eps
+        d.n_extra = len(self.extras)
+        for i, x in enumerate(self.extras):
+            d.extra[i] = x.data_ptr()
+            d.ld_extra[i] = _row_major(x, "th_gemm extra")
+            d.extra_dtype[i] = th_dtype(x)
+        if self.rope_cos is not None:
+            d.rope_cos, d.rope_sin = self.rope_cos.data_ptr(), self.rope_sin.data_ptr()
+            d.rope_head_dim, d.rope_period = self.rope_head_dim, self.rope_period
+        d.n_out = len(self.outs)
+        for i, o in enumerate(self.outs):
+            e = d.out[i]
+            e.op, e.a, e.b, e.e = o.op, o.a, o.b, o.e
+            e.ptr = o.out.data_ptr()
+            e.ld = _row_major(o.out, "th_gemm out")
+            e.dtype = th_dtype(o.out)
+        if self.sumsq_out is not None:
+            d.sumsq_out = self.sumsq_out.data_ptr()
+        return d
+
+
+def gemm(call: GemmCall, kernel: str | None = None) -> None:
+    lib = _lib(call.lhs)
+    d = call.descriptor()
+    abi.check(lib.th_gemm(C.byref(d), _stream(call.lhs)), "th_gemm", kernel)
+
+
+# --------------------------------------------------------------- RMSNorm
+def rmsnorm(x: torch.Tensor, gain: torch.Tensor, eps: float, out: torch.Tensor, inv_k: float | None = None,
+            kernel: str | None = None) -> torch.Tensor:
+    lib = _lib(x)
+    d = abi.RmsNormDesc()
+    d.M, d.K = x.shape
+    d.x, d.ld_x, d.x_dtype = x.data_ptr(), _row_major(x, "th_rmsnorm x"), th_dtype(x)
+    d.out, d.ld_out, d.out_dtype = out.data_ptr(), _row_major(out, "th_rmsnorm out"), th_dtype(out)
+    if gain.dtype != torch.float32 or not gain.is_contiguous() or gain.numel() != x.shape[1]:
+        raise abi.HipBackendError("th_rmsnorm", abi.TH_ERR_INVALID, "gain must be a contiguous fp32 [K] tensor")
+    d.gain = gain.data_ptr()
+    d.inv_k = 1.0 / x.shape[1] if inv_k is None else inv_k
+    d.eps = eps
+    abi.check(lib.th_rmsnorm(C.byref(d), _stream(x)), "th_rmsnorm", kernel)
+    return out
+
+
+# ------------------------------------------------------------- attention
+def attention_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: torch.Tensor, *, batch: int,
+                      seq_q: int, seq_kv: int, heads_q: int, heads_kv: int, head_dim: int, scale: float,
+                      causal: bool, kernel: str | None = None) -> torch.Tensor:
+    lib = _lib(q)
+    d = abi.AttnDesc()
+    d.batch, d.seq_q, d.seq_kv, d.heads_q, d.heads_kv, d.head_dim = batch, seq_q, seq_kv, heads_q, heads_kv, head_dim
+    d.scale, d.causal, d.dtype = scale, 1 if causal else 0, th_dtype(q)
+    for t in (k, v, out):
+        if t.dtype != q.dtype:
+            raise abi.HipBackendError("th_attention_prefill", abi.TH_ERR_INVALID, "q/k/v/o dtypes differ")
+    d.q, d.ld_q = q.data_ptr(), _row_major(q, "attention q")
+    d.k, d.ld_k = k.data_ptr(), _row_major(k, "attention k")
+    d.v, d.ld_v = v.data_ptr(), _row_major(v, "attention v")
+    d.o, d.ld_o = out.data_ptr(), _row_major(out, "attention o")
+    abi.check(lib.th_attention_prefill(C.byref(d), _stream(q)), "th_attention_prefill", kernel)
+    return out
+
+
+# ----------------------------------------------------------- epilogue VM
+def epilogue_vm(M: int, N: int, operands: list[tuple[torch.Tensor, bool]], ops: list[tuple], outs: list[tuple[torch.Tensor, int]],
+                n_slots: int, workspace: torch.Tensor, kernel: str | None = None) -> None:
+    """``operands``: (tensor, is_column); ``ops``: (code, dst, a, b, scalar, mode);
+    ``outs``: (tensor, slot)."""
+    ref = workspace
+    lib = _lib(ref)
+    if len(operands) > abi.VM_MAX_IN or len(ops) > abi.VM_MAX_OPS or len(outs) > abi.VM_MAX_OUT:
+        raise abi.HipBackendError("th_epilogue_vm", abi.TH_ERR_UNSUPPORTED, "epilogue program too large")
+    if workspace.dtype != torch.float32 or workspace.numel() < n_slots * M * N:
+        raise abi.HipBackendError("th_epilogue_vm", abi.TH_ERR_INVALID, "workspace too small")
+    d = abi.VmDesc()
+    d.M, d.N = M, N
+    d.n_in, d.n_ops, d.n_out, d.n_slots = len(operands), len(ops), len(outs), n_slots
+    for i, (t, col) in enumerate(operands):
+        d.in_[i].ptr, d.in_[i].ld, d.in_[i].dtype, d.in_[i].column = t.data_ptr(), t.stride(0), th_dtype(t), 1 if col else 0
+    for i, (code, dst, a, b, scalar, mode) in enumerate(ops):
+        o = d.ops[i]
+        o.code, o.dst, o.a, o.b, o.scalar, o.mode = code, dst, a, b, scalar, mode
+    for i, (t, slot) in enumerate(outs):
+        d.out[i].ptr, d.out[i].ld, d.out[i].dtype, d.out[i].slot = t.data_ptr(), _row_major(t, "vm out"), th_dtype(t), slot
+    d.workspace = workspace.data_ptr()
+    abi.check(lib.th_epilogue_vm(C.byref(d), _stream(ref)), "th_epilogue_vm", kernel)
