@@ -1,0 +1,137 @@
+"""Benchmark: one Llama-3-8B-shaped decoder block forward (bf16, B=8, S=2048) on one MI355X.
+
+Prints ONE JSON line (the driver's contract). A step is one forward of the
+block compiled by ``compile_model`` and run through libth_hip.so, with the
+input already resident in HBM. ``value`` is microseconds per block forward
+(BASELINE.json's metric), ``tokens_per_s`` the matching throughput.
+
+Extra objects on the line:
+* ``roofline``: the dominant kernel (largest share of the step) with its
+  algorithmic FLOPs (or bytes) per launch divided by its average launch
+  duration measured with HIP events on the launch stream;
+* ``cpu_baseline``: the oracle's fp32 CPU forward of the same block on a
+  bounded sample (one of the 8 sequences), scaled to the whole batch;
+* ``parity``: max-abs error of the GPU output's first sequence against that
+  fp32 CPU forward (north-star tolerance 2e-2).
+
+``--gpus N`` with N > 1 exits: this build measures one GPU.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO / "torch-helion_amd"))
+sys.path.insert(0, str(REPO))
+
+METRIC = "µs per block fwd (Llama-8B block, Mamba-2 layer); % of MFMA/HBM roofline"
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def build_c3():
+    import torch
+    from targets.llama_block import build_llama_block, config_c3
+
+    cfg = config_c3()
+    model = build_llama_block(cfg, seed=0)
+    x = model.example_inputs(seed=0)
+    return cfg, model, x
+
+
+def cpu_baseline(model, cfg, x, out_gpu, sample_seqs: int = 1) -> tuple[dict, dict]:
+    """Oracle fp32 forward of ``sample_seqs`` sequence(s) on the host cores."""
+    import torch
+    from oracle.llama import block_forward
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    w = {k: v.detach().float() for k, v in model.state_dict().items() if not k.startswith(("rope", "attn_bias"))}
+    rope = (model.rope_cos.float(), model.rope_sin.float())
+    xs = x[0][:sample_seqs].float()
+    kw = dict(heads=cfg.heads, kv_heads=cfg.n_kv, eps=cfg.eps, theta=cfg.rope_theta, causal=cfg.causal, rope=rope,
+              dtype=torch.float32)
+    with torch.inference_mode():
+        t0 = time.perf_counter()
+        ref = block_forward(xs, w, **kw)
+        dt = time.perf_counter() - t0
+    scale = cfg.batch / sample_seqs
+    base = {"value": dt * scale * 1e6, "unit": "us", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"oracle.llama.block_forward fp32 on {sample_seqs} of {cfg.batch} sequences "
+                      f"(S={cfg.seq}), one timed rep of {dt:.1f} s, scaled x{scale:g} to the full batch"}
+    err = (out_gpu[:sample_seqs].float().cpu() - ref).abs().max().item()
+    parity = {"max_abs_err": err, "tolerance": 2e-2, "ok": err <= 2e-2, "against": "oracle fp32, first sequence"}
+    return base, parity
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU; --gpus must be 1 (see DESIGN.md for how the block would shard)"}))
+        return 2
+
+    import torch
+    from torch_helion import CompileConfig, compile_model
+    from torch_helion.hip.bench import bench_program
+
+    log("building the Llama-3-8B-shaped block (random init, seed 0)")
+    cfg, model, x = build_c3()
+    t0 = time.time()
+    res = compile_model(model, x, CompileConfig(run_name="bench_llama_c3", results_dir=REPO / "gpurun_out" / "results",
+                                                backend="hip", device_check=False, reference_check=False,
+                                                verify_passes=False, planner_mode="exhaustive"))
+    log(f"compiled in {time.time() - t0:.1f} s: {len(res.program.kernels)} kernels")
+    dp = res.device_program
+    b = bench_program(dp, x, res.hw, warmup=args.warmup, reps=args.steps)
+    us = b["us_median"]
+    out_gpu = dp.outputs()[0]
+    torch.cuda.synchronize()
+    tokens = cfg.batch * cfg.seq
+    dom_name, dom = max(b["kernels"].items(), key=lambda kv: kv[1]["us"])
+    if dom["bound"] == "mfma":
+        roof = {"bound": "mfma", "achieved": dom["achieved_tflops"], "peak": dom["peak_tflops"], "unit": "TFLOP/s",
+                "frac": dom["frac"], "traffic": None, "kernel": dom_name, "kernel_us": dom["us"],
+                "algorithmic_flops": dom["flops"]}
+    else:
+        roof = {"bound": "hbm", "achieved": dom["achieved_gbs"], "peak": dom["peak_gbs"], "unit": "GB/s",
+                "frac": dom["frac"], "traffic": None, "kernel": dom_name, "kernel_us": dom["us"],
+                "algorithmic_bytes": dom["bytes"]}
+    block_frac = b["total_flops"] / (us * 1e-6) / (res.hw.peak_tflops["bfloat16"] * 1e12)
+    line = {
+        "metric": METRIC, "value": us, "unit": "us", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": us / 1e3, "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic (N(0,1) input, N(0,0.02) weights, seed 0)",
+        "tokens_per_s": tokens / (us * 1e-6),
+        "block_mfma_frac": block_frac,
+        "config": {"workload": "llama3-8b-block-prefill", "batch": cfg.batch, "seq_len": cfg.seq,
+                   "d_model": cfg.hidden, "heads": cfg.heads, "kv_heads": cfg.n_kv, "ffn": cfg.intermediate,
+                   "causal": cfg.causal, "parallelism": "none (1 GPU)"},
+        "roofline": roof,
+        "kernels_us": {k: round(v["us"], 2) for k, v in b["kernels"].items()},
+        "kernels_frac": {k: round(v["frac"], 4) for k, v in b["kernels"].items()},
+        "us_p10": b["us_p10"], "us_p90": b["us_p90"],
+    }
+    if not args.no_cpu_baseline:
+        log("cpu baseline: oracle fp32 forward of one sequence on the host")
+        base, parity = cpu_baseline(model, cfg, x, out_gpu)
+        line["cpu_baseline"] = base
+        line["parity"] = parity
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

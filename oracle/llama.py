@@ -1,0 +1,79 @@
+"""Functional Llama decoder block (oracle; test infrastructure only).
+
+Restates reference models/llama_block.py:28-159: pre-norm RMSNorm
+(``x * rsqrt(mean(x^2) + eps) * g``, :55-63), q/k/v projections, RoPE with
+``rotate_half`` (:66-79, :99-100), softmax(q k^T / sqrt(d)) v (:101-103),
+o-projection + residual, RMSNorm, SwiGLU MLP + residual (:108-117, :137-139).
+Extensions used by the BASELINE configs: a causal mask (key j visible to
+query i iff j <= i) and grouped KV heads (query head h reads kv head
+h // (H / H_kv)).
+
+``weights`` uses the nn.Linear convention [out, in] and the state-dict names
+of ``targets.llama_block.LlamaBlock``.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+
+def rms_norm(x: torch.Tensor, g: torch.Tensor, eps: float) -> torch.Tensor:
+    return x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps) * g
+
+
+def rope_tables(seq: int, head_dim: int, theta: float, dtype=torch.float64):
+    """cos/sin [seq, head_dim]: angle(pos, i) = pos * theta^(-2(i mod d/2)/d)."""
+    half = head_dim // 2
+    inv = theta ** (-torch.arange(half, dtype=torch.float64) * 2.0 / head_dim)
+    ang = torch.arange(seq, dtype=torch.float64)[:, None] * inv[None, :]
+    ang = torch.cat([ang, ang], dim=1)
+    return torch.cos(ang).to(dtype), torch.sin(ang).to(dtype)
+
+
+def rotate_half(x: torch.Tensor) -> torch.Tensor:
+    half = x.shape[-1] // 2
+    return torch.cat([-x[..., half:], x[..., :half]], dim=-1)
+
+
+def attention(q, k, v, causal: bool) -> torch.Tensor:
+    """q [b, h, s, d]; k, v [b, hk, s, d] with h a multiple of hk."""
+    h, hk = q.shape[1], k.shape[1]
+    if hk != h:
+        k = k.repeat_interleave(h // hk, dim=1)
+        v = v.repeat_interleave(h // hk, dim=1)
+    d = q.shape[-1]
+    scores = q @ k.transpose(-1, -2) / math.sqrt(d)
+    if causal:
+        s = q.shape[2]
+        scores = scores.masked_fill(torch.ones(s, s, dtype=torch.bool).triu(1), float("-inf"))
+    return torch.softmax(scores, dim=-1) @ v
+
+
+def block_forward(x: torch.Tensor, w: dict[str, torch.Tensor], *, heads: int, kv_heads: int, eps: float,
+                  theta: float, causal: bool, rope: tuple[torch.Tensor, torch.Tensor] | None = None,
+                  dtype=torch.float64) -> torch.Tensor:
+    """x [b, s, D] -> [b, s, D], computed in ``dtype``.
+
+    ``rope`` overrides the cos/sin tables (e.g. with the model's own buffers,
+    which the reference rounds to the model dtype, models/llama_block.py:79)."""
+    w = {k: v.to(dtype) for k, v in w.items()}
+    x = x.to(dtype)
+    b, s, dm = x.shape
+    hd = dm // heads
+    cos, sin = rope if rope is not None else rope_tables(s, hd, theta, dtype)
+    cos, sin = cos.to(dtype)[:s], sin.to(dtype)[:s]
+    h = rms_norm(x, w["input_norm.weight"], eps)
+    q = (h @ w["attn.q_proj.weight"].T).view(b, s, heads, hd).transpose(1, 2)
+    k = (h @ w["attn.k_proj.weight"].T).view(b, s, kv_heads, hd).transpose(1, 2)
+    v = (h @ w["attn.v_proj.weight"].T).view(b, s, kv_heads, hd).transpose(1, 2)
+    q = q * cos + rotate_half(q) * sin
+    k = k * cos + rotate_half(k) * sin
+    a = attention(q, k, v, causal).transpose(1, 2).reshape(b, s, heads * hd)
+    x = x + a @ w["attn.o_proj.weight"].T
+    h2 = rms_norm(x, w["post_norm.weight"], eps)
+    gate = h2 @ w["mlp.gate_proj.weight"].T
+    up = h2 @ w["mlp.up_proj.weight"].T
+    mlp = (gate * torch.sigmoid(gate) * up) @ w["mlp.down_proj.weight"].T
+    return x + mlp

@@ -1,0 +1,89 @@
+"""End to end on the GPU: compile_model(backend="hip") vs the CPU oracle.
+
+fp32 programs: max relative error (max|a-b| / max|b|) <= 1e-4 against the
+oracle in float64. bf16 programs: max-abs error <= 2e-2 against the oracle in
+float32 on the same (bf16) weights and inputs.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from conftest import announce
+
+pytestmark = pytest.mark.gpu
+
+
+def _oracle(model, cfg, x, dtype):
+    from oracle.llama import block_forward
+
+    w = {k: v.detach().to(dtype) for k, v in model.state_dict().items() if not k.startswith(("rope", "attn_bias"))}
+    return block_forward(x.to(dtype), w, heads=cfg.heads, kv_heads=cfg.n_kv, eps=cfg.eps, theta=cfg.rope_theta,
+                         causal=cfg.causal, rope=(model.rope_cos.to(dtype), model.rope_sin.to(dtype)), dtype=dtype)
+
+
+def _compile(model, x, tmp_path, name):
+    from torch_helion import CompileConfig, compile_model
+
+    return compile_model(model, x, CompileConfig(run_name=name, results_dir=tmp_path, backend="hip",
+                                                 planner_mode="greedy"))
+
+
+CASES = {
+    "mha_bf16": dict(batch=2, seq=128, hidden=256, heads=4, intermediate=512, dtype=torch.bfloat16),
+    "gqa_causal_bf16": dict(batch=2, seq=256, hidden=512, heads=8, kv_heads=2, intermediate=1024, causal=True,
+                            dtype=torch.bfloat16, rope_theta=500000.0),
+    "gqa_causal_bf16_hd128": dict(batch=1, seq=384, hidden=1024, heads=8, kv_heads=4, intermediate=2048, causal=True,
+                                  dtype=torch.bfloat16),
+}
+
+
+@pytest.mark.parametrize("case", list(CASES))
+def test_llama_block_bf16(gpu, tmp_path, case):
+    from targets.llama_block import LlamaBlockConfig, build_llama_block
+
+    announce(f"e2e llama {case}")
+    cfg = LlamaBlockConfig(**CASES[case])
+    model = build_llama_block(cfg, seed=0)
+    x = model.example_inputs(seed=0)
+    res = _compile(model, x, tmp_path, case)
+    assert res.validation["ok"], res.validation
+    # the pre-rotated RoPE siblings are re-fused: q alone and (k, v) as 2 accumulators
+    fused = [p for p in res.device_program.plans.values() if p.get("rope_fused")]
+    assert fused and all(p["n_acc"] <= 3 for p in fused), res.device_program.plans
+    out = res.run(*x)[0].float().cpu()
+    ref = _oracle(model, cfg, x[0], torch.float32)
+    assert torch.isfinite(out).all()
+    assert (out - ref).abs().max().item() < 2e-2
+
+
+def test_llama_block_c1_fp32(gpu, tmp_path):
+    """BASELINE config 0 (C1): fp32, B=1, S=128, d=512, 8x64 MHA, FFN 1376, causal."""
+    from targets.llama_block import build_llama_block, config_c1
+
+    announce("e2e llama C1 fp32")
+    cfg = config_c1()
+    model = build_llama_block(cfg, seed=0)
+    x = model.example_inputs(seed=0)
+    res = _compile(model, x, tmp_path, "c1")
+    out = res.run(*x)[0].double().cpu()
+    ref = _oracle(model, cfg, x[0], torch.float64)
+    rel = ((out - ref).abs().max() / ref.abs().max()).item()
+    assert rel < 1e-4, rel
+    kinds = [k.kind for k in res.program.kernels]
+    assert kinds == ["gemm", "attention", "gemm", "gemm", "gemm"], kinds
+
+
+def test_device_program_reruns_are_identical(gpu, tmp_path):
+    """Two runs on the same inputs give bit-identical outputs (no atomics in reductions)."""
+    from targets.llama_block import LlamaBlockConfig, build_llama_block
+
+    announce("e2e determinism")
+    cfg = LlamaBlockConfig(**CASES["gqa_causal_bf16"])
+    model = build_llama_block(cfg, seed=1)
+    x = model.example_inputs(seed=1)
+    res = _compile(model, x, tmp_path, "det")
+    a = res.run(*x)[0].clone()
+    b = res.run(*x)[0].clone()
+    assert torch.equal(a, b)

@@ -1,0 +1,162 @@
+"""Roofline cost model for OpIR kernels on MI355X.
+
+Replaces the reference's mesh-cycle model (cost_models/analytic.py:109-266)
+with what bounds a gfx950 kernel: ``max(MFMA time, HBM time)`` where
+
+* MFMA time counts the work of whole block tiles (tile quantisation: a
+  ragged edge tile costs a full tile) spread over 256 CUs in waves (wave
+  quantisation: a partial last wave costs a full wave), at the dtype's dense
+  peak times an achievable efficiency from ``hwspec``;
+* HBM time is the kernel's algorithmic bytes at peak bandwidth times an
+  efficiency;
+
+plus a fixed launch overhead in microseconds. ``algorithmic`` FLOPs/bytes are
+also reported; they are what bench.py's roofline fraction divides by.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import asdict, dataclass, field
+from typing import Any
+
+from ..capture.opgraph import DTYPE_BYTES, TensorType
+from ..optimizer.opir import KernelSpec
+from .hw_spec import HardwareSpec
+
+
+class CostModelError(RuntimeError):
+    pass
+
+
+@dataclass
+class CostBreakdown:
+    us: float
+    flops: float
+    bytes: float
+    bound: str
+    tiles: dict[str, int] = field(default_factory=dict)
+    blocks: int = 0
+    waves: int = 0
+    t_mfma_us: float = 0.0
+    t_hbm_us: float = 0.0
+    detail: dict[str, Any] = field(default_factory=dict)
+
+    @property
+    def cycles(self) -> float:
+        """Kept for reports that expect the reference's ``cycles`` key: µs here."""
+        return self.us
+
+    def to_dict(self) -> dict[str, Any]:
+        d = asdict(self)
+        d["cycles"] = self.us
+        return d
+
+
+def _dtype(spec: KernelSpec, tensors: dict[str, TensorType]) -> str:
+    for a in spec.args:
+        t = tensors.get(a.tensor)
+        if t is not None and a.role in ("lhs", "q", "x") and t.dtype.startswith(("bfloat", "float")):
+            return t.dtype
+    return "float32"
+
+
+def _bytes(t: TensorType) -> int:
+    return t.numel * DTYPE_BYTES.get(t.dtype, 4)
+
+
+def gemm_tiles(N: int, n_acc: int, M: int, dtype: str) -> tuple[int, int]:
+    """(BM, per-accumulator column tile) the HIP GEMM picks (mirrors csrc/gemm.hip)."""
+    if dtype == "float32":
+        bn = {1: 128 if N > 64 else 64, 2: 64 if N > 32 else 32, 3: 64}.get(n_acc, 64 if N > 32 else 32)
+        return 64, bn
+    bn = {1: 256 if N >= 192 else (128 if N > 64 else 64), 2: 128 if N >= 128 else (64 if N > 32 else 32),
+          3: 64}.get(n_acc, 64 if N > 32 else 32)
+    big = math.ceil(M / 256) * math.ceil(N / bn) >= 512
+    return (256 if big else 128), bn
+
+
+def _compose(hw: HardwareSpec, flops: float, nbytes: float, mfma_flops: float, blocks: int, dtype: str,
+             tiles: dict[str, int], detail: dict[str, Any]) -> CostBreakdown:
+    eff_m = hw.efficiency.get("mfma", 0.6)
+    eff_h = hw.efficiency.get("hbm", 0.7)
+    waves = max(1, math.ceil(blocks / hw.compute_units)) if blocks else 1
+    per_block = mfma_flops / max(blocks, 1)
+    t_mfma = waves * per_block / (hw.peak_flops(dtype) / hw.compute_units * eff_m) * 1e6 if mfma_flops else 0.0
+    t_hbm = nbytes / (hw.hbm_bytes_per_s() * eff_h) * 1e6
+    us = max(t_mfma, t_hbm) + hw.launch_overhead_us
+    bound = "mfma" if t_mfma >= t_hbm else "hbm"
+    return CostBreakdown(us, flops, nbytes, bound, tiles, blocks, waves, t_mfma, t_hbm, detail)
+
+
+def gemm_cost(spec: KernelSpec, tensors: dict[str, TensorType], hw: HardwareSpec) -> CostBreakdown:
+    from ..hip.epilogue import fused_acc_count  # structural, no parameter values needed
+
+    T, N, K = spec.grid["rows"], spec.grid["cols"], spec.k_extent
+    dtype = _dtype(spec, tensors)
+    eb = DTYPE_BYTES.get(dtype, 4)
+    n_acc = fused_acc_count(spec) if spec.gemms else 0
+    extras = [a for a in spec.args if a.role == "extra"]
+    nbytes = T * K * eb + n_acc * K * N * eb + sum(_bytes(tensors[a.tensor]) for a in extras) + len(spec.outputs) * T * N * eb
+    if n_acc == 0:  # stand-alone normalisation: HBM bound
+        return _compose(hw, 3.0 * T * K, nbytes, 0.0, 0, dtype, {"tile_t": 4}, {"n_acc": 0})
+    flops = 2.0 * T * N * K * n_acc
+    bm, bn = gemm_tiles(N, n_acc, T, dtype)
+    tiles_m, tiles_n = math.ceil(T / bm), math.ceil(N / bn)
+    kq = math.ceil(K / (16 if dtype == "float32" else 64)) * (16 if dtype == "float32" else 64)
+    mfma = 2.0 * tiles_m * bm * tiles_n * bn * n_acc * kq
+    return _compose(hw, flops, nbytes, mfma, tiles_m * tiles_n, dtype,
+                    {"tile_t": bm, "tile_n": bn, "tile_k": 16 if dtype == "float32" else 64},
+                    {"n_acc": n_acc, "sumsq": spec.sumsq, "extras": len(extras), "outputs": len(spec.outputs)})
+
+
+def attention_cost(spec: KernelSpec, tensors: dict[str, TensorType], hw: HardwareSpec) -> CostBreakdown:
+    a = spec.attrs
+    b, s, h, d = a["batch"], a["seq"], a["heads"], a["head_dim"]
+    hk = a.get("kv_heads", h)
+    skv = a.get("seq_kv", s)
+    dtype = _dtype(spec, tensors)
+    eb = DTYPE_BYTES.get(dtype, 4)
+    pairs = s * skv
+    if a.get("causal"):
+        pairs = sum(min(skv, i + 1 + skv - s) for i in range(s))
+    flops = 4.0 * b * h * pairs * d
+    nbytes = (2 * b * s * h * d + 2 * b * skv * hk * d) * eb
+    qb = math.ceil(s / 128)
+    blocks = b * h * qb
+    kv_tiles = sum(math.ceil(min(skv, (i + 1) * 128 + skv - s) / 64) for i in range(qb)) if a.get("causal") else qb * math.ceil(skv / 64)
+    mfma = 4.0 * b * h * 128 * 64 * d * kv_tiles
+    return _compose(hw, flops, nbytes, mfma, blocks, dtype, {"tile_m": 128, "tile_n": 64}, {"kv_heads": hk})
+
+
+def ssd_cost(spec: KernelSpec, tensors: dict[str, TensorType], hw: HardwareSpec) -> CostBreakdown:
+    a = spec.attrs
+    b, s, h, p, n = a["batch"], a["seq"], a["heads"], a["head_dim"], a["state_dim"]
+    q = a.get("chunk", 64)
+    dtype = _dtype(spec, tensors)
+    eb = DTYPE_BYTES.get(dtype, 4)
+    # intra-chunk C B^T and M X, chunk states, carried-state output
+    flops = 2.0 * b * h * s * (q * n + q * p + 2 * n * p)
+    nbytes = sum(_bytes(tensors[x.tensor]) for x in spec.args) + len(spec.outputs) * b * s * h * p * eb
+    blocks = b * h * max(1, math.ceil(s / q))
+    return _compose(hw, flops, nbytes, flops, blocks, dtype, {"chunk": q}, {})
+
+
+def elementwise_cost(spec: KernelSpec, tensors: dict[str, TensorType], hw: HardwareSpec) -> CostBreakdown:
+    dtype = _dtype(spec, tensors)
+    nbytes = sum(_bytes(tensors[x.tensor]) for x in spec.args) + sum(_bytes(tensors[o.tensor]) for o in spec.outputs)
+    a = spec.attrs
+    flops = 2.0 * a.get("batch", 1) * a.get("seq", 1) * a.get("width", 1) * a.get("kernel", 1)
+    return _compose(hw, flops, nbytes, 0.0, 0, dtype, {}, {})
+
+
+def kernel_cost(spec: KernelSpec, tensors: dict[str, TensorType], hw: HardwareSpec, tiles: dict[str, int] | None = None) -> CostBreakdown:
+    if spec.kind == "gemm":
+        return gemm_cost(spec, tensors, hw)
+    if spec.kind == "attention":
+        return attention_cost(spec, tensors, hw)
+    if spec.kind in ("ssd", "ssd_chunked"):
+        return ssd_cost(spec, tensors, hw)
+    if spec.kind in ("conv1d", "embedding"):
+        return elementwise_cost(spec, tensors, hw)
+    raise CostModelError(f"unknown kernel kind {spec.kind}")

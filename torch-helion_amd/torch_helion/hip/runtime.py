@@ -1,0 +1,367 @@
+"""Execute an OpIR Program on one MI355X through libth_hip.so.
+
+The device twin of the reference's interpreter loop (codegen/interpret.py:54-77):
+parameters are uploaded once (GEMM weights pre-packed into th_gemm's layout,
+RoPE tables compressed back to [S, head_dim] after checking their structure),
+every intermediate is allocated once from ``Program.tensors``, and each
+KernelSpec becomes one or two C-ABI launches on the current stream, in
+program order. There is no host fallback: a kernel the library cannot run
+raises :class:`HipBackendError` naming it.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+from typing import Any, Callable
+
+import torch
+
+from ..optimizer.opir import KernelSpec, Program
+from . import abi, ops
+from .epilogue import (EpiloguePlan, build_trees, is_rotated_copy, match_epilogue, match_rscale, periodic_table,
+                       rope_geometry)
+
+_TORCH_DT = {"float32": torch.float32, "bfloat16": torch.bfloat16, "float16": torch.float16,
+             "int64": torch.int64, "int32": torch.int32, "float8_e4m3fn": torch.float8_e4m3fn}
+
+
+def _err(kernel: str, msg: str) -> abi.HipBackendError:
+    return abi.HipBackendError("lower", abi.TH_ERR_UNSUPPORTED, msg, kernel)
+
+
+@dataclass
+class Launch:
+    """One kernel of the program, bound to device buffers."""
+
+    kernel: str
+    kind: str
+    run: Callable[[], None]
+    entry: str
+    info: dict[str, Any] = field(default_factory=dict)
+
+
+class DeviceProgram:
+    """A Program lowered and bound for execution on ``device``."""
+
+    def __init__(self, program: Program, params: dict[str, torch.Tensor], device: int | torch.device = 0,
+                 fuse_rope: bool = True) -> None:
+        self.program = program
+        self.device = torch.device("cuda", device) if isinstance(device, int) else torch.device(device)
+        if self.device.type != "cuda":
+            raise abi.HipBackendError("DeviceProgram", abi.TH_ERR_INVALID, f"device {device} is not a HIP device")
+        abi.init_device(self.device.index or 0)
+        self.fuse_rope = fuse_rope
+        self.buffers: dict[str, torch.Tensor] = {}
+        self.workspaces: list[torch.Tensor] = []
+        self.launches: list[Launch] = []
+        self.plans: dict[str, Any] = {}
+        self._host_params = params
+        for name in program.params:
+            self.buffers[name] = params[name].to(self.device)
+        for name in program.inputs:
+            t = program.tensors[name]
+            self.buffers[name] = torch.empty(t.shape, dtype=_TORCH_DT[t.dtype], device=self.device)
+        for k in program.kernels:
+            for o in k.outputs:
+                if o.tensor not in self.buffers:
+                    t = program.tensors[o.tensor]
+                    self.buffers[o.tensor] = torch.empty(t.shape, dtype=_TORCH_DT[t.dtype], device=self.device)
+        # Residual operands produced inside the program get an fp32 shadow:
+        # the producer also writes fp32 and every kernel that adds it as an
+        # epilogue operand reads the shadow, so the residual stream is rounded
+        # to the activation dtype only where a GEMM consumes it as its LHS.
+        self.shadow: dict[str, torch.Tensor] = {}
+        produced = {o.tensor for k in program.kernels for o in k.outputs}
+        for k in program.kernels:
+            for a in k.args:
+                if (a.role == "extra" and a.tensor in produced and a.tensor not in self.shadow
+                        and self.buffers[a.tensor].dtype in (torch.bfloat16, torch.float16)):
+                    self.shadow[a.tensor] = torch.empty(self.buffers[a.tensor].shape, dtype=torch.float32,
+                                                        device=self.device)
+        for k in program.kernels:
+            self.launches.extend(self._lower(k))
+
+    # -------------------------------------------------------------- running
+    def set_inputs(self, inputs: dict[str, torch.Tensor] | list[torch.Tensor] | tuple) -> None:
+        if isinstance(inputs, (list, tuple)):
+            inputs = dict(zip(self.program.inputs, inputs))
+        for name in self.program.inputs:
+            dst = self.buffers[name]
+            src = inputs[name]
+            dst.copy_(src.reshape(dst.shape).to(dst.dtype), non_blocking=True)
+
+    def launch_all(self) -> None:
+        for l in self.launches:
+            l.run()
+
+    def run(self, inputs=None) -> list[torch.Tensor]:
+        """Run the program; returns the program outputs (device tensors)."""
+        if inputs is not None:
+            self.set_inputs(inputs)
+        self.launch_all()
+        return self.outputs()
+
+    def outputs(self) -> list[torch.Tensor]:
+        shapes = self.program.metadata.get("output_shapes", {})
+        return [self.buffers[o].reshape(shapes[o]) if o in shapes else self.buffers[o] for o in self.program.outputs]
+
+    def tensor(self, name: str) -> torch.Tensor:
+        return self.buffers[name]
+
+    def operand(self, name: str) -> torch.Tensor:
+        """Buffer an epilogue reads for ``name`` (its fp32 shadow if it has one)."""
+        return self.shadow.get(name, self.buffers[name])
+
+    # ------------------------------------------------------------- lowering
+    def _dt(self, name: str) -> torch.dtype:
+        return _TORCH_DT[self.program.tensors[name].dtype]
+
+    def _host(self, name: str) -> torch.Tensor | None:
+        return self._host_params.get(name) if name in self.program.params else None
+
+    def _workspace(self, numel: int, dtype=torch.float32) -> torch.Tensor:
+        w = torch.empty(numel, dtype=dtype, device=self.device)
+        self.workspaces.append(w)
+        return w
+
+    def _lower(self, spec: KernelSpec) -> list[Launch]:
+        if spec.kind == "gemm":
+            return self._lower_gemm(spec)
+        if spec.kind == "attention":
+            return [self._lower_attention(spec)]
+        if spec.kind in ("ssd", "ssd_chunked"):
+            from .ssd import lower_ssd
+            return lower_ssd(self, spec)
+        if spec.kind == "conv1d":
+            from .ssd import lower_conv1d
+            return lower_conv1d(self, spec)
+        raise _err(spec.name, f"kernel kind {spec.kind!r} has no HIP kernel")
+
+    # attention ------------------------------------------------------------
+    def _lower_attention(self, spec: KernelSpec) -> Launch:
+        a = spec.attrs
+        q, k, v = (self.buffers[spec.arg(r).tensor] for r in ("q", "k", "v"))
+        out = self.buffers[spec.outputs[0].tensor]
+        kw = dict(batch=a["batch"], seq_q=a["seq"], seq_kv=a.get("seq_kv", a["seq"]), heads_q=a["heads"],
+                  heads_kv=a.get("kv_heads", a["heads"]), head_dim=a["head_dim"], scale=float(a["scale"]),
+                  causal=bool(a.get("causal", False)))
+
+        def run() -> None:
+            ops.attention_prefill(q, k, v, out, kernel=spec.name, **kw)
+
+        return Launch(spec.name, "attention", run, "th_attention_prefill", kw)
+
+    # gemm -----------------------------------------------------------------
+    def _pack(self, spec: KernelSpec, rhs_args: list[str], in_dtype: torch.dtype) -> Callable[[], torch.Tensor]:
+        """Packed rhs for these weight arguments: packed once if all are params,
+        else re-packed into a workspace at every run."""
+        tens = [spec.arg(r).tensor for r in rhs_args]
+        srcs = [self.buffers[t] for t in tens]
+        if all(t in self.program.params for t in tens):
+            srcs = [s if s.dtype in (torch.float32, torch.bfloat16) else s.float() for s in srcs]
+            if in_dtype == torch.float32:
+                srcs = [s.float() for s in srcs]
+            packed = ops.pack_rhs(srcs, in_dtype)
+            return lambda: packed
+        k_, n_ = srcs[0].shape
+        nbytes = abi.load().th_gemm_packed_bytes(n_, k_, len(srcs), ops.th_dtype(in_dtype))
+        ws = self._workspace(int(nbytes), torch.uint8)
+        return lambda: ops.pack_rhs(srcs, in_dtype, out=ws)
+
+    def _lower_gemm(self, spec: KernelSpec) -> list[Launch]:
+        lhs = self.buffers[spec.arg("lhs").tensor]
+        T, N, K = spec.grid["rows"], spec.grid["cols"], spec.k_extent
+        if lhs.dtype not in (torch.bfloat16, torch.float32):
+            raise _err(spec.name, f"lhs dtype {lhs.dtype} has no MFMA GEMM in this build")
+        if not spec.gemms:
+            norm = self._lower_norm(spec)
+            if norm is not None:
+                return [norm]
+            return self._lower_gemm_vm(spec)
+        plan = match_epilogue(spec)
+        if plan.fused:
+            launches = self._lower_gemm_fused(spec, plan)
+            if launches is not None:
+                return launches
+        return self._lower_gemm_vm(spec)
+
+    def _lower_norm(self, spec: KernelSpec) -> Launch | None:
+        """gemms=[] + sumsq kernels of the form (x * r) * gain_full -> th_rmsnorm."""
+        trees = build_trees(spec)
+        if len(spec.outputs) != 1:
+            return None
+        e = trees[spec.outputs[0].value]
+        lhs_tensor = spec.arg("lhs").tensor
+        if not (len(e) == 4 and e[0] == "mul" and not dict(e[1])):
+            return None
+        for inner, gain in ((e[2], e[3]), (e[3], e[2])):
+            if gain[0] != "extra" or not (len(inner) == 4 and inner[0] == "mul"):
+                continue
+            for x, r in ((inner[2], inner[3]), (inner[3], inner[2])):
+                rs = match_rscale(r)
+                if rs is None or x[0] != "extra" or spec.arg(x[1]).tensor != lhs_tensor:
+                    continue
+                gt = spec.arg(gain[1]).tensor
+                host = self._host(gt)
+                if host is None:
+                    continue
+                row = periodic_table(host.float(), 1, host.shape[1])
+                if row is None:
+                    continue
+                gvec = row.reshape(-1).to(self.device).contiguous()
+                xbuf = self.buffers[lhs_tensor]
+                out = self.buffers[spec.outputs[0].tensor]
+                inv_k, eps = rs
+
+                def run() -> None:
+                    ops.rmsnorm(xbuf, gvec, eps, out, inv_k=inv_k, kernel=spec.name)
+
+                return Launch(spec.name, "rmsnorm", run, "th_rmsnorm", {"inv_k": inv_k, "eps": eps})
+        return None
+
+    def _lower_gemm_fused(self, spec: KernelSpec, plan: EpiloguePlan) -> list[Launch] | None:
+        T, N, K = spec.grid["rows"], spec.grid["cols"], spec.k_extent
+        lhs_t = spec.arg("lhs").tensor
+        lhs = self.buffers[lhs_t]
+        in_dtype = lhs.dtype
+        rhs_of = {i: g.rhs for i, g in enumerate(spec.gemms)}
+        outs = []
+        rope_tables: dict[tuple[str, str], tuple[torch.Tensor, torch.Tensor, int, int]] = {}
+        for o in plan.outs:
+            op, a, b = o.op, o.a, o.b
+            if op == abi.EPI_ROPE_PAIR:
+                cos_t, sin_t = (spec.arg(x).tensor for x in o.rope)
+                hc, hs = self._host(cos_t), self._host(sin_t)
+                if hc is None or hs is None:
+                    return None
+                key = (cos_t, sin_t)
+                geo = rope_geometry(hc.float(), hs.float())
+                if geo is None:
+                    return None
+                rp, period = geo
+                wa, wb = self._host(spec.arg(rhs_of[a]).tensor), self._host(spec.arg(rhs_of[b]).tensor)
+                # the tables repeat every half head (cos = cat(f, f)), so the head
+                # dim is the multiple of their period for which w_b is w_a rotated
+                hd, fused = period, False
+                if self.fuse_rope and wa is not None and wb is not None:
+                    cand = period
+                    while cand <= N and N % cand == 0:
+                        if is_rotated_copy(wa, wb, cand):
+                            hd, fused = cand, True
+                            break
+                        cand *= 2
+                if key in rope_tables and rope_tables[key][3] != hd:
+                    return None
+                if key not in rope_tables:
+                    ct = periodic_table(hc.float(), rp, hd).to(self.device)
+                    st = periodic_table(hs.float(), rp, hd).to(self.device)
+                    rope_tables[key] = (ct, st, rp, hd)
+                outs.append((o, abi.EPI_ROPE, a, -1, key) if fused else (o, abi.EPI_ROPE_PAIR, a, b, key))
+            else:
+                outs.append((o, op, a, b, None))
+        if len(rope_tables) > 1:
+            return None
+        used: list[int] = []
+        for _, op, a, b, _ in outs:
+            for i in (a, b):
+                if i >= 0 and i not in used:
+                    used.append(i)
+        used.sort()
+        if any(op == abi.EPI_ROPE for _, op, *_ in outs):
+            bn = abi.load().th_gemm_acc_tile(N, min(len(used), abi.MAX_ACC), ops.th_dtype(in_dtype))
+            hd = next(iter(rope_tables.values()))[3]
+            if bn % hd:
+                # the column tile cannot hold whole heads: keep the rotated accumulators
+                outs = [(o, abi.EPI_ROPE_PAIR if op == abi.EPI_ROPE else op, a, o.b if op == abi.EPI_ROPE else b, key)
+                        for (o, op, a, b, key) in outs]
+                used = sorted({i for _, _, a, b, _ in outs for i in (a, b) if i >= 0})
+        if len(used) > abi.MAX_ACC:
+            return None
+        slot = {i: s for s, i in enumerate(used)}
+        extras: list[str] = []
+        for o, *_ in outs:
+            if o.extra is not None and o.extra not in extras:
+                extras.append(o.extra)
+        if len(extras) > abi.MAX_EXTRA:
+            return None
+        get_packed = self._pack(spec, [rhs_of[i] for i in used], in_dtype)
+        extra_bufs = [self.operand(spec.arg(x).tensor) for x in extras]
+        epi = []
+        for o, op, a, b, key in outs:
+            dsts = [self.buffers[o.tensor]] + ([self.shadow[o.tensor]] if o.tensor in self.shadow else [])
+            for out_buf in dsts:
+                epi.append(ops.EpiSpec(op, out_buf, a=slot[a], b=slot[b] if b >= 0 else -1,
+                                       e=extras.index(o.extra) if o.extra is not None else -1))
+        if len(epi) > abi.MAX_OUT:
+            return None
+        mask = 0
+        for i in used:
+            if plan.scaled.get(i, False):
+                mask |= 1 << slot[i]
+        inv_k, eps = plan.rscale if plan.rscale else (0.0, 0.0)
+        rope = next(iter(rope_tables.values())) if rope_tables else None
+        info = {"n_acc": len(used), "ops": [op for _, op, *_ in outs], "rscale": plan.rscale is not None,
+                "rope_fused": any(op == abi.EPI_ROPE for _, op, *_ in outs)}
+
+        def run() -> None:
+            call = ops.GemmCall(T, N, K, len(used), lhs, get_packed(), epi, sumsq=plan.rscale is not None,
+                                rscale_mask=mask, inv_k=inv_k, eps=eps, extras=extra_bufs)
+            if rope is not None:
+                call.rope_cos, call.rope_sin, call.rope_period, call.rope_head_dim = rope[0], rope[1], rope[2], rope[3]
+            ops.gemm(call, kernel=spec.name)
+
+        self.plans[spec.name] = info
+        return [Launch(spec.name, "gemm", run, "th_gemm", info)]
+
+    # generic path ---------------------------------------------------------
+    def _lower_gemm_vm(self, spec: KernelSpec) -> list[Launch]:
+        """Raw fp32 accumulators (+ sum of squares) then th_epilogue_vm."""
+        T, N, K = spec.grid["rows"], spec.grid["cols"], spec.k_extent
+        lhs = self.buffers[spec.arg("lhs").tensor]
+        launches: list[Launch] = []
+        acc_bufs: dict[str, torch.Tensor] = {}
+        sumsq = self._workspace(T) if spec.sumsq else None
+        if spec.gemms:
+            for start in range(0, len(spec.gemms), abi.MAX_ACC):
+                group = list(range(start, min(start + abi.MAX_ACC, len(spec.gemms))))
+                get_packed = self._pack(spec, [spec.gemms[i].rhs for i in group], lhs.dtype)
+                bufs = [self._workspace(T * N).view(T, N) for _ in group]
+                for i, b in zip(group, bufs):
+                    acc_bufs[spec.gemms[i].acc] = b
+                epi = [ops.EpiSpec(abi.EPI_ACC, b, a=s) for s, b in enumerate(bufs)]
+                first = start == 0
+
+                def run(group=group, get_packed=get_packed, epi=epi, first=first) -> None:
+                    ops.gemm(ops.GemmCall(T, N, K, len(group), lhs, get_packed(), epi, sumsq=bool(first and sumsq is not None),
+                                          sumsq_out=sumsq if first else None), kernel=spec.name)
+
+                launches.append(Launch(spec.name, "gemm", run, "th_gemm", {"n_acc": len(group), "vm": True}))
+        launches.append(self._vm_launch(spec, acc_bufs, sumsq, lhs))
+        return launches
+
+    def _vm_launch(self, spec: KernelSpec, acc_bufs: dict[str, torch.Tensor], sumsq: torch.Tensor | None,
+                   lhs: torch.Tensor | None) -> Launch:
+        from .vm import compile_vm
+
+        M, N = (spec.grid["rows"], spec.grid["cols"]) if spec.kind == "gemm" else next(
+            iter(acc_bufs.values())).shape
+        prog = compile_vm(self, spec, acc_bufs, sumsq, lhs, M, N)
+        ws = self._workspace(prog.n_slots * M * N)
+
+        def run() -> None:
+            ops.epilogue_vm(M, N, prog.operands, prog.ops, prog.outs, prog.n_slots, ws, kernel=spec.name)
+
+        return Launch(spec.name, "epilogue_vm", run, "th_epilogue_vm", {"slots": prog.n_slots, "ops": len(prog.ops)})
+
+
+def run_program(program: Program, params: dict[str, torch.Tensor], inputs, device: int = 0) -> dict[str, torch.Tensor]:
+    """Device twin of the reference's interpreter ``run_program``: every produced
+    tensor, on the device."""
+    dp = DeviceProgram(program, params, device)
+    dp.run(inputs)
+    return dict(dp.buffers)
+
+
+def program_outputs(program: Program, params: dict[str, torch.Tensor], inputs, device: int = 0) -> list[torch.Tensor]:
+    return DeviceProgram(program, params, device).run(inputs)

@@ -1,0 +1,148 @@
+"""Planner: choose the sibling-GEMM grouping with the cost model
+(reference: optimizer/planner.py:83-164).
+
+The freedom left after canonicalisation is which sibling GEMMs share a
+kernel. ``exhaustive`` enumerates every set partition of each sibling set
+(Bell-number many, sets up to 6), ``greedy`` only all-merged vs all-split.
+Each candidate is partitioned, checked for MI355X legality and costed with
+the roofline model (``us`` per kernel plus launch overhead); the cheapest
+legal candidate wins, ties broken by fewer kernels.
+"""
+
+from __future__ import annotations
+
+import json
+from dataclasses import dataclass, field
+from itertools import product
+from typing import Any
+
+from ..capture.opgraph import OpGraph
+from ..cost_models.hw_spec import HardwareSpec
+from ..cost_models.roofline import CostModelError, kernel_cost
+from .legality import check_program
+from .opir import Program
+from .partition import Grouping, PartitionError, build_program, sibling_sets
+
+
+@dataclass
+class Candidate:
+    index: int
+    grouping: Grouping
+    program: Program | None
+    legal: bool
+    total_cycles: float          # microseconds on MI355X (key kept from the reference)
+    kernel_cycles: dict[str, float] = field(default_factory=dict)
+    violations: list[str] = field(default_factory=list)
+    error: str | None = None
+
+    @property
+    def total_us(self) -> float:
+        return self.total_cycles
+
+    def to_dict(self) -> dict[str, Any]:
+        return {"index": self.index, "grouping": self.grouping, "legal": self.legal, "total_us": self.total_cycles,
+                "kernel_us": self.kernel_cycles, "kernels": [k.name for k in self.program.kernels] if self.program else [],
+                "violations": self.violations, "error": self.error}
+
+
+@dataclass
+class PlanResult:
+    best: Candidate
+    candidates: list[Candidate]
+
+    @property
+    def program(self) -> Program:
+        assert self.best.program is not None
+        return self.best.program
+
+
+def set_partitions(items: list[str]) -> list[list[list[str]]]:
+    if not items:
+        return [[]]
+    first, rest = items[0], items[1:]
+    out = []
+    for part in set_partitions(rest):
+        out.append([[first]] + part)
+        for i in range(len(part)):
+            out.append(part[:i] + [[first] + part[i]] + part[i + 1:])
+    return out
+
+
+def enumerate_groupings(g: OpGraph, mode: str = "exhaustive", max_candidates: int = 512) -> list[Grouping]:
+    per_set = []
+    for s in sibling_sets(g):
+        if mode == "exhaustive" and len(s) <= 6:
+            per_set.append(set_partitions(s))
+        else:
+            per_set.append([[list(s)], [[m] for m in s]] if len(s) > 1 else [[list(s)]])
+    groupings: list[Grouping] = []
+    for combo in product(*per_set):
+        grouping: Grouping = {}
+        gid = 0
+        for part in combo:
+            for block in part:
+                for m in block:
+                    grouping[m] = gid
+                gid += 1
+        groupings.append(grouping)
+        if len(groupings) >= max_candidates:
+            break
+    return groupings
+
+
+def kernel_signature(spec, tensors) -> str:
+    d = spec.to_dict()
+    for key in ("name", "tiles", "cost"):
+        d.pop(key, None)
+    d["shapes"] = {a.name: list(tensors[a.tensor].shape) for a in spec.args}
+    d["dtypes"] = {a.name: tensors[a.tensor].dtype for a in spec.args}
+    d["args"] = [[a.name, a.role, a.view] for a in spec.args]
+    d["outputs"] = [o.value for o in spec.outputs]
+    return json.dumps(d, sort_keys=True, default=str)
+
+
+def cost_program(program: Program, hw: HardwareSpec, config=None, memo: dict[str, Any] | None = None) -> tuple[float, dict[str, float]]:
+    total, per = 0.0, {}
+    memo = {} if memo is None else memo
+    for spec in program.kernels:
+        key = kernel_signature(spec, program.tensors)
+        cb = memo.get(key)
+        if cb is None:
+            cb = memo[key] = kernel_cost(spec, program.tensors, hw)
+        spec.tiles = dict(cb.tiles)
+        spec.cost = {"us": cb.us, "cycles": cb.us, "bound": cb.bound, "flops": cb.flops, "bytes": cb.bytes,
+                     "breakdown": cb.to_dict()}
+        per[spec.name] = cb.us
+        total += cb.us
+    return total, per
+
+
+def plan(g: OpGraph, hw: HardwareSpec, config, name: str = "program") -> PlanResult:
+    mode = getattr(config, "planner_mode", "exhaustive")
+    candidates: list[Candidate] = []
+    memo: dict[str, Any] = {}
+    for i, grouping in enumerate(enumerate_groupings(g, mode)):
+        try:
+            program = build_program(g, grouping, name=name)
+        except PartitionError as e:
+            candidates.append(Candidate(i, grouping, None, False, float("inf"), error=str(e)))
+            continue
+        rep = check_program(program)
+        if not rep.ok:
+            candidates.append(Candidate(i, grouping, program, False, float("inf"), violations=[str(v) for v in rep.violations]))
+            continue
+        try:
+            total, per = cost_program(program, hw, config, memo)
+        except CostModelError as e:
+            candidates.append(Candidate(i, grouping, program, False, float("inf"), error=str(e)))
+            continue
+        candidates.append(Candidate(i, grouping, program, True, total, per))
+    legal = [c for c in candidates if c.legal]
+    if not legal:
+        details = "\n".join(f"  candidate {c.index}: {c.error or c.violations}" for c in candidates[:10])
+        raise PartitionError(f"no legal partition among {len(candidates)} candidates:\n{details}")
+    best = min(legal, key=lambda c: (c.total_cycles, len(c.program.kernels)))
+    best.program.metadata["plan"] = {"candidates": len(candidates), "legal": len(legal), "total_us": best.total_cycles,
+                                     "total_cycles": best.total_cycles, "kernel_us": best.kernel_cycles,
+                                     "launch_overhead_us": hw.launch_overhead_us}
+    return PlanResult(best, candidates)

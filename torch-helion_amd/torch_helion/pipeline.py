@@ -1,0 +1,252 @@
+"""compile_model: PyTorch model -> OpGraph -> OpIR -> MI355X HIP kernels.
+
+::
+
+    from torch_helion import compile_model, CompileConfig
+    res = compile_model(model, example_args, CompileConfig(run_name="llama_block"))
+    print(res.program.summary())
+    out = res.run(*example_args)            # on the GPU, through libth_hip.so
+
+Stages as in the reference (reference: pipeline.py:60-145): capture,
+canonicalize, plan, codegen (here: HIP launch plans + device binding),
+reference_check (CPU interpreter vs eager), then the MI355X additions:
+device_check (HIP run vs the eager model in fp32) and an optional bench.
+"""
+
+from __future__ import annotations
+
+import copy
+import logging
+import math
+import time
+from dataclasses import dataclass, field
+from pathlib import Path
+from typing import Any, Sequence
+
+import torch
+
+from .capture import CapturedFx, OpGraph, capture
+from .codegen.emit import emit_program
+from .codegen.interpret import program_outputs
+from .config import CompileConfig
+from .cost_models.hw_spec import HardwareSpec
+from .optimizer.evaluate import max_rel_err
+from .optimizer.opir import Program
+from .optimizer.passes import canonicalize
+from .optimizer.planner import PlanResult, plan
+from .results import ResultsWriter
+
+log = logging.getLogger("torch_helion")
+
+
+@dataclass
+class CompileResult:
+    config: CompileConfig
+    run_dir: Path
+    fx: CapturedFx
+    raw_graph: OpGraph
+    graph: OpGraph
+    hw: HardwareSpec
+    plan: PlanResult
+    program: Program
+    kernel_files: dict[str, Path]
+    validation: dict[str, Any] = field(default_factory=dict)
+    reference_check: dict[str, Any] = field(default_factory=dict)
+    loom_results: dict[str, Any] = field(default_factory=dict)
+    timings: dict[str, float] = field(default_factory=dict)
+    device_program: Any = None
+    bench: dict[str, Any] = field(default_factory=dict)
+
+    @property
+    def estimated_cycles(self) -> float:
+        """Estimated program time (µs on MI355X; key name kept from the reference)."""
+        return self.program.metadata.get("plan", {}).get("total_us", float("nan"))
+
+    def run(self, *args) -> list[torch.Tensor]:
+        if self.device_program is None:
+            raise RuntimeError("no device program: compile with backend='hip' on a machine with an MI355X")
+        return self.device_program.run(list(args))
+
+
+def _graph_flops(g: OpGraph) -> float:
+    total = 0.0
+    for n in g:
+        if n.op in ("matmul", "batch_matmul") and len(n.inputs) == 2:
+            total += 2.0 * math.prod(n.type.shape) * g[n.inputs[0]].type.shape[-1]
+    return total
+
+
+def eager_reference(model: torch.nn.Module, args: Sequence[Any], batch_slice: int | None = None) -> list[torch.Tensor]:
+    """The model in fp32 on the CPU (optionally on the first ``batch_slice``
+    sequences only: every config here is independent across the batch)."""
+    m = copy.deepcopy(model).float().cpu().eval()
+    xs = []
+    for a in args:
+        if isinstance(a, torch.Tensor):
+            a = a.detach().cpu()
+            if batch_slice is not None:
+                a = a[:batch_slice]
+            xs.append(a.float() if a.is_floating_point() else a)
+        else:
+            xs.append(a)
+    with torch.inference_mode():
+        out = m(*xs)
+    return list(out) if isinstance(out, (list, tuple)) else [out]
+
+
+def compile_model(model: torch.nn.Module, example_args: Sequence[Any], config: CompileConfig | None = None) -> CompileResult:
+    config = config or CompileConfig()
+    rw = ResultsWriter(config.run_dir)
+    timings: dict[str, float] = {}
+
+    class stage:
+        def __init__(self, name: str) -> None:
+            self.name = name
+
+        def __enter__(self):
+            self.t = time.time()
+            log.info("stage %s", self.name)
+
+        def __exit__(self, *exc):
+            timings[self.name] = time.time() - self.t
+
+    with stage("capture"):
+        fx, raw = capture(model, example_args)
+        rw.write_text("00_model.txt", f"{model!r}\n\nconfig: {config!r}\n")
+        rw.write_text("01_fx_graph.txt", fx.text())
+        rw.write_json("01_fx_op_histogram.json", fx.op_histogram())
+        raw.to_json(rw.path("02_opgraph_raw.json"))
+        rw.write_text("02_opgraph_raw.txt", raw.summary())
+
+    small = _graph_flops(raw) <= config.cpu_flop_budget
+    verify = small if config.verify_passes is None else config.verify_passes
+    with stage("canonicalize"):
+        graph, pass_log = canonicalize(raw, verify_inputs=list(example_args) if verify else None,
+                                       tolerance=config.tolerance, ssd_chunk=config.ssd_chunk)
+        graph.to_json(rw.path("03_opgraph_canonical.json"))
+        rw.write_text("03_opgraph_canonical.txt", graph.summary())
+        rw.write_json("03_pass_log.json", pass_log)
+
+    with stage("plan"):
+        hw = HardwareSpec.load(config.hw_spec)
+        rw.write_json("04_hw_spec.json", hw.summary())
+        result = plan(graph, hw, config, name=config.run_name)
+        program = result.program
+        rw.write_json("05_plan/candidates.json", [c.to_dict() for c in result.candidates])
+        rw.write_text("05_plan/plan.md", plan_report(result, hw, config))
+        program.to_json(rw.path("06_opir.json"))
+        rw.write_text("06_opir.txt", program.summary())
+
+    device_program = None
+    with stage("codegen"):
+        kernel_files = emit_program(program, config, rw.path("kernels"))
+        if config.save_params:
+            torch.save({n: graph.params[n] for n in program.params}, rw.path("params.pt"))
+        if config.backend == "hip":
+            from .hip.runtime import DeviceProgram
+
+            device_program = DeviceProgram(program, graph.params, config.device, fuse_rope=config.fuse_rope)
+            rw.write_json("kernels/launches.json", [{"kernel": l.kernel, "entry": l.entry, "info": l.info}
+                                                    for l in device_program.launches])
+
+    reference_check: dict[str, Any] = {}
+    do_ref = small if config.reference_check is None else config.reference_check
+    if do_ref:
+        with stage("reference_check"):
+            with torch.no_grad():
+                ref = model(*example_args)
+            outs = program_outputs(program, graph.params, list(example_args))
+            refs = ref if isinstance(ref, (list, tuple)) else [ref]
+            errs = [max_rel_err(o.reshape(-1), r.reshape(-1)) for o, r in zip(outs, refs)]
+            reference_check = {"max_rel_err": max(errs), "per_output": errs, "tolerance": config.tolerance,
+                               "ok": max(errs) <= config.tolerance}
+            rw.write_json("08_reference_check.json", reference_check)
+
+    validation: dict[str, Any] = {}
+    if device_program is not None and config.device_check:
+        with stage("device_check"):
+            validation = device_check(model, example_args, device_program, config, small)
+            rw.write_json("07_validation.json", validation)
+
+    rw.write_json("09_cost_report.json", cost_report_json(program, hw, config))
+    rw.write_text("09_cost_report.md", cost_report_md(program, hw, config))
+
+    res = CompileResult(config, rw.run_dir, fx, raw, graph, hw, result, program, kernel_files, validation,
+                        reference_check, {}, timings, device_program)
+    if config.bench and device_program is not None:
+        from .hip.bench import bench_program
+
+        with stage("bench"):
+            res.bench = bench_program(device_program, example_args, hw, warmup=config.bench_warmup,
+                                      reps=config.bench_reps)
+            rw.write_json("11_bench.json", res.bench)
+    rw.write_json("timings.json", timings)
+    return res
+
+
+def device_check(model, example_args, dp, config: CompileConfig, small: bool) -> dict[str, Any]:
+    """HIP run vs the eager model in fp32 (first sequence only for large graphs)."""
+    outs = dp.run(list(example_args))
+    torch.cuda.synchronize()
+    batch_slice = None if small else 1
+    refs = eager_reference(model, example_args, batch_slice)
+    res: dict[str, Any] = {"batch_slice": batch_slice, "outputs": []}
+    ok = True
+    for o, r in zip(outs, refs):
+        o = o.float().cpu()
+        if batch_slice is not None:
+            o = o[:batch_slice]
+        o = o.reshape(r.shape)
+        rel = max_rel_err(o.reshape(-1), r.reshape(-1))
+        mab = float((o - r).abs().max())
+        dtype = str(dp.program.tensors[dp.program.outputs[0]].dtype)
+        passed = (rel <= 1e-4) if dtype == "float32" else (mab <= config.tolerance)
+        ok &= passed
+        res["outputs"].append({"max_rel_err": rel, "max_abs_err": mab, "dtype": dtype, "ok": passed,
+                               "finite": bool(torch.isfinite(o).all())})
+    res["ok"] = ok
+    return res
+
+
+# ------------------------------------------------------------------ reports
+def plan_report(result: PlanResult, hw: HardwareSpec, config: CompileConfig) -> str:
+    lines = [f"# Partition plan ({config.run_name})", "",
+             f"Hardware: {hw.name} ({hw.compute_units} CUs, {hw.hbm_bandwidth_gbs:.0f} GB/s HBM)",
+             f"Candidates: {len(result.candidates)} (legal: {sum(c.legal for c in result.candidates)}), "
+             f"planner mode: {config.planner_mode}", "",
+             "| # | kernels | est. us | legal | note |", "|---|---|---|---|---|"]
+    for c in sorted(result.candidates, key=lambda c: (not c.legal, c.total_cycles)):
+        note = c.error or "; ".join(c.violations[:2]) or ("best" if c is result.best else "")
+        est = f"{c.total_cycles:,.1f}" if c.legal else "-"
+        lines.append(f"| {c.index} | {len(c.program.kernels) if c.program else '-'} | {est} | {'yes' if c.legal else 'no'} | {note} |")
+    lines += ["", "## Chosen program", "", "```", result.program.summary(), "```"]
+    return "\n".join(lines)
+
+
+def cost_report_json(program: Program, hw: HardwareSpec, config: CompileConfig) -> dict[str, Any]:
+    kernels = [{"name": k.name, "kind": k.kind, "tiles": k.tiles, "us": k.cost.get("us"), "bound": k.cost.get("bound"),
+                "flops": k.cost.get("flops"), "bytes": k.cost.get("bytes")} for k in program.kernels]
+    inter = program.intermediates()
+    link = {t: program.tensors[t].nbytes for t in inter}
+    return {"hw": hw.summary(), "kernels": kernels, "total_us": program.metadata.get("plan", {}).get("total_us"),
+            "intermediate_tensors": link, "intermediate_bytes": sum(link.values())}
+
+
+def cost_report_md(program: Program, hw: HardwareSpec, config: CompileConfig) -> str:
+    total = program.metadata.get("plan", {}).get("total_us", 0.0)
+    lines = [f"# Cost report ({program.name})", "",
+             f"Hardware `{hw.name}`: {hw.compute_units} CUs, {hw.hbm_bandwidth_gbs:.0f} GB/s.",
+             f"Estimated time: **{total:,.1f} us** (roofline, incl. {hw.launch_overhead_us} us per kernel).", "",
+             "| kernel | kind | tiles | est. us | bound | GFLOP | MB |", "|---|---|---|---|---|---|---|"]
+    for k in program.kernels:
+        c = k.cost
+        lines.append(f"| {k.name} | {k.kind} | {k.tiles} | {c.get('us', 0):,.1f} | {c.get('bound', '-')} | "
+                     f"{c.get('flops', 0) / 1e9:,.2f} | {c.get('bytes', 0) / 1e6:,.1f} |")
+    inter = program.intermediates()
+    lines += ["", f"Kernel-to-kernel links: {len(inter)} intermediate tensors, "
+              f"{sum(program.tensors[t].nbytes for t in inter):,} bytes through HBM.", ""]
+    for t in inter:
+        p = program.producer(t)
+        lines.append(f"- `{t}` {program.tensors[t]}: {p.name if p else '?'} -> "
+                     f"{', '.join(c.name for c in program.consumers(t)) or 'output'}")
+    return "\n".join(lines) + "\n"
