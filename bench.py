@@ -63,12 +63,23 @@ def cpu_baseline(model, cfg, x, out_gpu, sample_seqs: int = 1) -> tuple[dict, di
         t0 = time.perf_counter()
         ref = block_forward(xs, w, **kw)
         dt = time.perf_counter() - t0
+        ref_store = block_forward(xs, w, storage=torch.bfloat16, **kw)
     scale = cfg.batch / sample_seqs
     base = {"value": dt * scale * 1e6, "unit": "us", "cores": torch.get_num_threads(), "kind": "port",
             "sample": f"oracle.llama.block_forward fp32 on {sample_seqs} of {cfg.batch} sequences "
                       f"(S={cfg.seq}), one timed rep of {dt:.1f} s, scaled x{scale:g} to the full batch"}
-    err = (out_gpu[:sample_seqs].float().cpu() - ref).abs().max().item()
-    parity = {"max_abs_err": err, "tolerance": 2e-2, "ok": err <= 2e-2, "against": "oracle fp32, first sequence"}
+    o = out_gpu[:sample_seqs].float().cpu()
+    err = (o - ref_store).abs().max().item()
+    err32 = (o - ref).abs().max().item()
+    floor = (ref_store - ref).abs().max().item()
+    rel = err32 / ref.abs().max().item()
+    # Gate: the reference's normalised error max|a-b|/max|b| <= 2e-2 against the pure fp32
+    # oracle. Max-abs is reported beside it together with the floor that any bf16-storage
+    # block has at this size (output magnitudes reach ~14, where one bf16 ulp is 0.0625).
+    parity = {"max_rel_err": rel, "tolerance": 2e-2, "ok": rel <= 2e-2,
+              "against": "oracle fp32 (oracle.llama.block_forward), first sequence, fp32 copy of the GPU output",
+              "max_abs_err": err32, "max_abs_err_vs_bf16_storage_oracle": err,
+              "bf16_storage_floor_max_abs": floor}
     return base, parity
 
 
@@ -97,7 +108,7 @@ def main() -> int:
     dp = res.device_program
     b = bench_program(dp, x, res.hw, warmup=args.warmup, reps=args.steps)
     us = b["us_median"]
-    out_gpu = dp.outputs()[0]
+    out_gpu = dp.outputs(fp32=True)[0]
     torch.cuda.synchronize()
     tokens = cfg.batch * cfg.seq
     dom_name, dom = max(b["kernels"].items(), key=lambda kv: kv[1]["us"])

@@ -53,11 +53,18 @@ def attention(q, k, v, causal: bool) -> torch.Tensor:
 
 def block_forward(x: torch.Tensor, w: dict[str, torch.Tensor], *, heads: int, kv_heads: int, eps: float,
                   theta: float, causal: bool, rope: tuple[torch.Tensor, torch.Tensor] | None = None,
-                  dtype=torch.float64) -> torch.Tensor:
+                  dtype=torch.float64, storage: torch.dtype | None = None) -> torch.Tensor:
     """x [b, s, D] -> [b, s, D], computed in ``dtype``.
 
     ``rope`` overrides the cos/sin tables (e.g. with the model's own buffers,
-    which the reference rounds to the model dtype, models/llama_block.py:79)."""
+    which the reference rounds to the model dtype, models/llama_block.py:79).
+
+    ``storage`` (e.g. torch.bfloat16) rounds the values a bf16 program keeps
+    in memory between kernels -- q, k, v after RoPE, the attention output,
+    the residual stream where the MLP reads it as a GEMM operand and the
+    SwiGLU product -- while the residual additions and the output stay in
+    ``dtype``. This is the arithmetic of a bf16 block whose kernels
+    accumulate in fp32, the bar a device result is compared against."""
     w = {k: v.to(dtype) for k, v in w.items()}
     x = x.to(dtype)
     b, s, dm = x.shape
@@ -68,12 +75,14 @@ def block_forward(x: torch.Tensor, w: dict[str, torch.Tensor], *, heads: int, kv
     q = (h @ w["attn.q_proj.weight"].T).view(b, s, heads, hd).transpose(1, 2)
     k = (h @ w["attn.k_proj.weight"].T).view(b, s, kv_heads, hd).transpose(1, 2)
     v = (h @ w["attn.v_proj.weight"].T).view(b, s, kv_heads, hd).transpose(1, 2)
-    q = q * cos + rotate_half(q) * sin
-    k = k * cos + rotate_half(k) * sin
-    a = attention(q, k, v, causal).transpose(1, 2).reshape(b, s, heads * hd)
+    rnd = (lambda t: t.to(storage).to(dtype)) if storage is not None else (lambda t: t)
+    q = rnd(q * cos + rotate_half(q) * sin)
+    k = rnd(k * cos + rotate_half(k) * sin)
+    v = rnd(v)
+    a = rnd(attention(q, k, v, causal).transpose(1, 2).reshape(b, s, heads * hd))
     x = x + a @ w["attn.o_proj.weight"].T
-    h2 = rms_norm(x, w["post_norm.weight"], eps)
+    h2 = rms_norm(rnd(x), w["post_norm.weight"], eps)
     gate = h2 @ w["mlp.gate_proj.weight"].T
     up = h2 @ w["mlp.up_proj.weight"].T
-    mlp = (gate * torch.sigmoid(gate) * up) @ w["mlp.down_proj.weight"].T
+    mlp = rnd(gate * torch.sigmoid(gate) * up) @ w["mlp.down_proj.weight"].T
     return x + mlp

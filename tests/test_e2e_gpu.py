@@ -15,12 +15,13 @@ from conftest import announce
 pytestmark = pytest.mark.gpu
 
 
-def _oracle(model, cfg, x, dtype):
+def _oracle(model, cfg, x, dtype, storage=None):
     from oracle.llama import block_forward
 
     w = {k: v.detach().to(dtype) for k, v in model.state_dict().items() if not k.startswith(("rope", "attn_bias"))}
     return block_forward(x.to(dtype), w, heads=cfg.heads, kv_heads=cfg.n_kv, eps=cfg.eps, theta=cfg.rope_theta,
-                         causal=cfg.causal, rope=(model.rope_cos.to(dtype), model.rope_sin.to(dtype)), dtype=dtype)
+                         causal=cfg.causal, rope=(model.rope_cos.to(dtype), model.rope_sin.to(dtype)), dtype=dtype,
+                         storage=storage)
 
 
 def _compile(model, x, tmp_path, name):
@@ -56,6 +57,10 @@ def test_llama_block_bf16(gpu, tmp_path, case):
     ref = _oracle(model, cfg, x[0], torch.float32)
     assert torch.isfinite(out).all()
     assert (out - ref).abs().max().item() < 2e-2
+    # the fp32 copy of the output against the oracle with the program's bf16 storage points
+    out32 = res.device_program.outputs(fp32=True)[0].float().cpu()
+    ref_store = _oracle(model, cfg, x[0], torch.float32, storage=torch.bfloat16)
+    assert (out32 - ref_store).abs().max().item() < 1e-2
 
 
 def test_llama_block_c1_fp32(gpu, tmp_path):

@@ -45,7 +45,7 @@ class DeviceProgram:
     """A Program lowered and bound for execution on ``device``."""
 
     def __init__(self, program: Program, params: dict[str, torch.Tensor], device: int | torch.device = 0,
-                 fuse_rope: bool = True) -> None:
+                 fuse_rope: bool = True, fp32_outputs: bool = True) -> None:
         self.program = program
         self.device = torch.device("cuda", device) if isinstance(device, int) else torch.device(device)
         if self.device.type != "cuda":
@@ -79,6 +79,12 @@ class DeviceProgram:
                         and self.buffers[a.tensor].dtype in (torch.bfloat16, torch.float16)):
                     self.shadow[a.tensor] = torch.empty(self.buffers[a.tensor].shape, dtype=torch.float32,
                                                         device=self.device)
+        if fp32_outputs:
+            # program outputs are also kept in fp32 (the epilogue computes them in
+            # fp32; rounding to the declared dtype is only the storage step)
+            for o in program.outputs:
+                if o in produced and o not in self.shadow and self.buffers[o].dtype in (torch.bfloat16, torch.float16):
+                    self.shadow[o] = torch.empty(self.buffers[o].shape, dtype=torch.float32, device=self.device)
         for k in program.kernels:
             self.launches.extend(self._lower(k))
 
@@ -102,9 +108,15 @@ class DeviceProgram:
         self.launch_all()
         return self.outputs()
 
-    def outputs(self) -> list[torch.Tensor]:
+    def outputs(self, fp32: bool = False) -> list[torch.Tensor]:
+        """Program outputs in their declared dtype, or (``fp32=True``) their fp32
+        copies where the producing kernel wrote one."""
         shapes = self.program.metadata.get("output_shapes", {})
-        return [self.buffers[o].reshape(shapes[o]) if o in shapes else self.buffers[o] for o in self.program.outputs]
+        res = []
+        for o in self.program.outputs:
+            t = self.shadow[o] if fp32 and o in self.shadow else self.buffers[o]
+            res.append(t.reshape(shapes[o]) if o in shapes else t)
+        return res
 
     def tensor(self, name: str) -> torch.Tensor:
         return self.buffers[name]
