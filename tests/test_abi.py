@@ -1,0 +1,158 @@
+"""C ABI of libth_hip.so on the CPU: exports, struct layouts, host-side validation.
+
+No compute call is made here: every call either is a pure query or fails
+host-side validation before any HIP call (or, for a valid descriptor on a
+machine without a GPU, stops at the "th_init was not called" check).
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+REPO = Path(__file__).resolve().parents[1]
+HEADER = REPO / "include" / "th_hip.h"
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from torch_helion.hip import abi
+
+    if not abi.library_path().exists():
+        pytest.skip("libth_hip.so not built (run __graft_entry__.build())")
+    return abi.load()
+
+
+def declared_functions() -> list[str]:
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:int|int64_t|const char\*)\s+(th_\w+)\s*\(", text, re.M)))
+
+
+def test_every_declared_symbol_is_exported_and_bound(lib):
+    from torch_helion.hip import abi
+
+    names = declared_functions()
+    assert len(names) >= 10
+    for n in names:
+        assert hasattr(lib, n), n
+        assert n in abi.SIGNATURES, f"{n} has no ctypes signature"
+    assert lib.th_abi_version() == abi.ABI_VERSION
+
+
+_STRUCTS = {
+    "th_epi_out": "EpiOut", "th_gemm_desc": "GemmDesc", "th_rmsnorm_desc": "RmsNormDesc",
+    "th_attn_desc": "AttnDesc", "th_vm_operand": "VmOperand", "th_vm_op": "VmOp", "th_vm_out": "VmOut",
+    "th_vm_desc": "VmDesc",
+}
+
+
+def test_struct_layouts_match_the_header(tmp_path):
+    """Compile a C probe against include/th_hip.h and compare sizeof/offsetof with ctypes."""
+    from torch_helion.hip import abi
+
+    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "th_hip.h"', "int main(void){"]
+    for cname, pyname in _STRUCTS.items():
+        st = getattr(abi, pyname)
+        lines.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
+        for fname, _ in st._fields_:
+            cf = "in" if (cname == "th_vm_desc" and fname == "in_") else fname
+            lines.append(f'printf("{cname} {fname} %zu\\n", offsetof({cname}, {cf}));')
+    lines.append("return 0;}")
+    src = tmp_path / "probe.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "probe"
+    subprocess.run(["gcc", "-I", str(HEADER.parent), str(src), "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split("\n")
+    got = {tuple(l.split()[:2]): int(l.split()[2]) for l in out if l.strip()}
+    for cname, pyname in _STRUCTS.items():
+        st = getattr(abi, pyname)
+        assert got[(cname, "size")] == C.sizeof(st), cname
+        for fname, _ in st._fields_:
+            assert got[(cname, fname)] == getattr(st, fname).offset, (cname, fname)
+
+
+def test_pure_queries(lib):
+    from torch_helion.hip import abi
+
+    assert lib.th_gemm_acc_tile(4096, 1, abi.TH_BF16) == 256
+    assert lib.th_gemm_acc_tile(1024, 2, abi.TH_BF16) == 128
+    assert lib.th_gemm_acc_tile(512, 3, abi.TH_BF16) == 64
+    assert lib.th_gemm_acc_tile(0, 1, abi.TH_BF16) == 0
+    # rows = ceil(N / tile) * tile * n_acc, K padded to 8 bf16 elements
+    assert lib.th_gemm_packed_bytes(1000, 100, 2, abi.TH_BF16) == 8 * 128 * 2 * 104 * 2
+    assert lib.th_gemm_packed_bytes(10, 10, 9, abi.TH_BF16) == -1
+
+
+def _gemm_desc(**over):
+    from torch_helion.hip import abi
+
+    d = abi.GemmDesc()
+    d.M = d.N = d.K = 64
+    d.n_acc, d.in_dtype = 1, abi.TH_BF16
+    d.lhs, d.ld_lhs, d.rhs_packed = 4096, 64, 8192
+    d.n_out = 1
+    d.out[0].ptr, d.out[0].ld, d.out[0].dtype = 12288, 64, abi.TH_BF16
+    for k, v in over.items():
+        setattr(d, k, v)
+    return d
+
+
+@pytest.mark.parametrize("field,value,msg", [
+    ("n_acc", 7, "n_acc"), ("K", 60, "multiple of 8"), ("in_dtype", 3, "in_dtype"), ("n_out", 0, "n_out"),
+    ("rscale_mask", 1, "without sumsq"), ("lhs", 4100, "aligned"),
+])
+def test_gemm_rejects_bad_descriptors(lib, field, value, msg):
+    from torch_helion.hip import abi
+
+    d = _gemm_desc(**{field: value})
+    assert lib.th_gemm(C.byref(d), None) == abi.TH_ERR_INVALID
+    assert msg in abi.last_error(lib)
+
+
+def test_null_descriptors_are_rejected(lib):
+    from torch_helion.hip import abi
+
+    for fn in ("th_gemm", "th_rmsnorm", "th_attention_prefill", "th_epilogue_vm"):
+        assert getattr(lib, fn)(None, None) == abi.TH_ERR_INVALID, fn
+        assert "null descriptor" in abi.last_error(lib)
+
+
+def test_attention_rejects_bad_heads(lib):
+    from torch_helion.hip import abi
+
+    d = abi.AttnDesc()
+    d.batch, d.seq_q, d.seq_kv, d.heads_q, d.heads_kv, d.head_dim = 1, 16, 16, 6, 4, 64
+    d.dtype = abi.TH_BF16
+    d.q = d.k = d.v = d.o = 4096
+    d.ld_q = d.ld_k = d.ld_v = d.ld_o = 384
+    assert lib.th_attention_prefill(C.byref(d), None) == abi.TH_ERR_INVALID
+    assert "multiple of heads_kv" in abi.last_error(lib)
+    d.heads_q, d.head_dim = 4, 96
+    assert lib.th_attention_prefill(C.byref(d), None) == abi.TH_ERR_INVALID
+    assert "head_dim" in abi.last_error(lib)
+
+
+def test_valid_descriptor_without_init_stops_before_the_device(lib):
+    import torch
+    from torch_helion.hip import abi
+
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present; this checks the GPU-less error path")
+    d = _gemm_desc()
+    assert lib.th_gemm(C.byref(d), None) == abi.TH_ERR_NOT_INIT
+    assert "th_init" in abi.last_error(lib)
+
+
+def test_product_raises_without_a_device():
+    """The runtime refuses to bind a program to a non-HIP device (no host fallback)."""
+    from torch_helion.hip import abi
+    from torch_helion.hip.runtime import DeviceProgram
+    from torch_helion.optimizer.opir import Program
+
+    prog = Program("p", [], [], {}, [])
+    with pytest.raises(abi.HipBackendError):
+        DeviceProgram(prog, {}, device=__import__("torch").device("cpu"))

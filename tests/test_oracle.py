@@ -1,0 +1,172 @@
+"""Pinning the oracle: each oracle function against something independent of it.
+
+* oracle.mamba.ssd_recurrence is the reference's definition (tests/test_mamba.py:27-38);
+  it is pinned by a single-step closed form and by the two scan forms of the
+  eager model (quadratic and chunked) agreeing with it to 1e-10 in float64,
+  with a planted sign error that must be caught.
+* oracle.llama.block_forward is pinned against the nn.Module restatement in
+  targets/ (an independent implementation) and its attention against torch's
+  scaled_dot_product_attention (causal and grouped KV).
+* oracle.interpret is pinned against the reference's recorded Llama reference
+  check (bit-exact max_rel_err from tests/golden) through the product
+  interpreter agreeing with it to fp32 rounding, and per kind against the
+  closed forms above.
+"""
+
+from __future__ import annotations
+
+import json
+import math
+from pathlib import Path
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+GOLDEN = Path(__file__).parent / "golden" / "reference_results"
+
+
+def _ssd_inputs(b=2, h=3, s=24, p=4, n=5, seed=0, dtype=torch.float64):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(b, h, s, p, generator=g, dtype=dtype)
+    B = torch.randn(b, h, s, n, generator=g, dtype=dtype)
+    C = torch.randn(b, h, s, n, generator=g, dtype=dtype)
+    dt = torch.rand(b, h, s, generator=g, dtype=dtype) * 0.1 + 0.01
+    A = -(torch.rand(b, h, 1, generator=g, dtype=dtype) * 15 + 1)
+    return x, dt * A, dt, B, C
+
+
+def test_recurrence_single_step_closed_form():
+    from oracle.mamba import ssd_recurrence
+
+    x, dA, dt, B, C = _ssd_inputs(s=1)
+    y = ssd_recurrence(x, dA, dt, B, C)
+    expect = dt[..., None] * x * (B * C).sum(-1, keepdim=True)
+    assert torch.allclose(y, expect, atol=1e-14)
+
+
+def test_recurrence_matches_both_scan_forms():
+    from oracle.mamba import ssd_recurrence
+    from targets.mamba import ssd_chunked, ssd_quadratic
+
+    x, dA, dt, B, C = _ssd_inputs()
+    ref = ssd_recurrence(x, dA, dt, B, C)
+    s = x.shape[2]
+    causal = torch.ones(s, s, dtype=torch.float64).tril()
+    yq = ssd_quadratic(x, dA, dt, B, C, causal)
+    assert (yq - ref).abs().max() / ref.abs().max() < 1e-10
+    for chunk in (1, 5, 6, 24):
+        yc = ssd_chunked(x, dA, dt, B, C, chunk)
+        assert (yc - ref).abs().max() / ref.abs().max() < 1e-10, chunk
+    # a planted mistake (decay sign flipped) is caught
+    bad = ssd_recurrence(x, -dA, dt, B, C)
+    assert (bad - ref).abs().max() / ref.abs().max() > 1e-2
+
+
+def test_ssd_chunked_program_groups():
+    """Token-major program form with shared B/C groups == per-head recurrence with repeated groups."""
+    from oracle.mamba import ssd_chunked_program, ssd_recurrence
+
+    bs, s, h, p, n, g = 2, 16, 4, 3, 5, 2
+    gen = torch.Generator().manual_seed(1)
+    x = torch.randn(bs * s, h * p, generator=gen, dtype=torch.float64)
+    bm = torch.randn(bs * s, g * n, generator=gen, dtype=torch.float64)
+    c = torch.randn(bs * s, g * n, generator=gen, dtype=torch.float64)
+    dt = torch.rand(bs * s, h, generator=gen, dtype=torch.float64) * 0.1
+    A = -torch.rand(h, generator=gen, dtype=torch.float64) * 4
+    D = torch.rand(h, generator=gen, dtype=torch.float64)
+    a = {"batch": bs, "seq": s, "heads": h, "head_dim": p, "state_dim": n, "ngroups": g}
+    y = ssd_chunked_program(c, bm, x, dt, A, D, a).reshape(bs, s, h, p)
+    for head in range(h):
+        gi = head // (h // g)
+        xs = x.reshape(bs, s, h, p)[:, :, head].unsqueeze(1)
+        Bs = bm.reshape(bs, s, g, n)[:, :, gi].unsqueeze(1)
+        Cs = c.reshape(bs, s, g, n)[:, :, gi].unsqueeze(1)
+        dts = dt.reshape(bs, s, h)[:, :, head].unsqueeze(1)
+        ref = ssd_recurrence(xs, dts * A[head], dts, Bs, Cs)[:, 0] + D[head] * xs[:, 0]
+        assert torch.allclose(y[:, :, head], ref, atol=1e-12)
+
+
+@pytest.mark.parametrize("causal,hk", [(False, 4), (True, 4), (True, 2), (True, 1)])
+def test_llama_attention_matches_sdpa(causal, hk):
+    from oracle.llama import attention
+
+    g = torch.Generator().manual_seed(2)
+    q = torch.randn(2, 4, 33, 16, generator=g, dtype=torch.float64)
+    k = torch.randn(2, hk, 33, 16, generator=g, dtype=torch.float64)
+    v = torch.randn(2, hk, 33, 16, generator=g, dtype=torch.float64)
+    ref = F.scaled_dot_product_attention(q, k, v, is_causal=causal, enable_gqa=hk != 4)
+    assert torch.allclose(attention(q, k, v, causal), ref, atol=1e-12)
+
+
+@pytest.mark.parametrize("kv,causal", [(None, False), (2, True)])
+def test_llama_oracle_matches_module(kv, causal):
+    from oracle.llama import block_forward
+    from targets.llama_block import LlamaBlockConfig, build_llama_block
+
+    cfg = LlamaBlockConfig(batch=2, seq=32, hidden=64, heads=4, kv_heads=kv, intermediate=96, causal=causal,
+                           dtype=torch.float64)
+    m = build_llama_block(cfg, seed=3)
+    x = m.example_inputs(seed=4)[0]
+    with torch.no_grad():
+        ref = m(x)
+    w = {k: v for k, v in m.state_dict().items() if not k.startswith(("rope", "attn_bias"))}
+    rope = (m.rope_cos, m.rope_sin)  # the module builds its tables in fp32 (reference models/llama_block.py:73-79)
+    out = block_forward(x, w, heads=cfg.heads, kv_heads=cfg.n_kv, eps=cfg.eps, theta=cfg.rope_theta, causal=causal,
+                        rope=rope)
+    assert (out - ref).abs().max() < 1e-12
+    from oracle.llama import rope_tables
+
+    c64, s64 = rope_tables(cfg.seq, cfg.head_dim, cfg.rope_theta)
+    assert (c64 - m.rope_cos).abs().max() < 1e-5 and (s64 - m.rope_sin).abs().max() < 1e-5
+
+
+def test_mamba_oracle_matches_module():
+    from oracle.mamba import backbone_forward
+    from targets.mamba import MambaConfig, build_mamba_model
+
+    cfg = MambaConfig(batch=2, seq=24, d_model=32, expand=2, headdim=16, d_state=8, chunk=8, n_layers=2,
+                      ngroups=1, use_conv=True, dtype=torch.float64, a_log_range=(0.0, math.log(16.0)))
+    for mode in ("quadratic", "chunked"):
+        cfg.mode = mode
+        m = build_mamba_model(cfg, seed=5)
+        x = m.example_inputs(seed=6)[0]
+        with torch.no_grad():
+            ref = m(x)
+        out = backbone_forward(x, dict(m.state_dict()), cfg)
+        assert (out - ref).abs().max() / ref.abs().max() < 1e-10, mode
+
+
+def test_interpreters_agree_and_reproduce_reference_check(tmp_path):
+    """The oracle interpreter (float64) and the product interpreter (float32) agree on
+    the reference's default Llama program; the product one reproduces the recorded check."""
+    from oracle import interpret as oi
+    from targets.llama_block import build_llama_block
+    from torch_helion import CompileConfig, compile_model
+
+    block = build_llama_block()
+    x = block.example_inputs()
+    res = compile_model(block, x, CompileConfig(run_name="r", results_dir=tmp_path, backend="none"))
+    recorded = json.loads((GOLDEN / "llama_block" / "08_reference_check.json").read_text())
+    assert res.reference_check["max_rel_err"] == recorded["max_rel_err"]
+    from torch_helion.codegen.interpret import program_outputs
+
+    mine = program_outputs(res.program, res.graph.params, list(x))[0]
+    ora = oi.program_outputs(res.program, res.graph.params, list(x))[0]
+    assert oi.max_rel_err(mine, ora) < 1e-5
+    with torch.no_grad():
+        eager = block(*x)
+    assert abs(oi.max_rel_err(ora, eager) - recorded["max_rel_err"]) < 2e-4
+
+
+def test_oracle_conv_matches_torch_conv1d():
+    from oracle.interpret import conv1d
+
+    g = torch.Generator().manual_seed(7)
+    bs, s, c, k = 2, 11, 6, 4
+    x = torch.randn(bs * s, c, generator=g, dtype=torch.float64)
+    w = torch.randn(c, k, generator=g, dtype=torch.float64)
+    y = conv1d(x, w, {"batch": bs, "seq": s, "activation": "silu"})
+    xb = x.reshape(bs, s, c).transpose(1, 2)
+    ref = F.silu(F.conv1d(F.pad(xb, (k - 1, 0)), w.unsqueeze(1), groups=c)).transpose(1, 2).reshape(bs * s, c)
+    assert torch.allclose(y, ref, atol=1e-12)

@@ -133,10 +133,12 @@ class Provenance:
         return self.base_index(_unravel(torch.arange(self.numel), self.shape)).reshape(self.shape)
 
 
-def trace_layout(graph: OpGraph, name: str) -> Provenance:
+def trace_layout(graph: OpGraph, name: str, until: str | None = None) -> Provenance:
+    """Provenance of ``name`` back to its first non-layout producer, or to the
+    node ``until`` if the chain reaches it first."""
     chain: list[OpNode] = []
     cur = graph[name]
-    while cur.kind == "layout" and cur.op in TRACEABLE and len(cur.inputs) == 1:
+    while cur.kind == "layout" and cur.op in TRACEABLE and len(cur.inputs) == 1 and cur.name != until:
         chain.append(cur)
         cur = graph[cur.inputs[0]]
     chain.reverse()

@@ -478,7 +478,11 @@ def match_attention(g: OpGraph) -> int:
 
 def match_conv(g: OpGraph) -> int:
     """``silu?(conv1d(pad(x^T, (k-1, 0)), w, groups=C))^T`` over each sequence ->
-    ``conv1d(x2d, w[C, k])`` on the token-major tensor (depthwise causal conv)."""
+    ``conv1d(x2d, w[C, k])`` on the token-major tensor (depthwise causal conv).
+
+    ``x`` may be a feature slice of a wider tensor (Mamba's xBC is a slice of
+    the in_proj output); the slice stays in front of the conv, where
+    ``push_slice_into_gemm`` later folds it into the projection weights."""
     n = 0
     for node in list(g):
         if node.op != "conv1d_raw":
@@ -495,14 +499,20 @@ def match_conv(g: OpGraph) -> int:
         if node.attrs["groups"] != ch or tuple(wv.shape) != (ch, 1, kk) or list(pad.attrs["pad"]) != [kk - 1, 0]:
             continue
         seq = s_pad - (kk - 1)
-        prov = trace_layout(g, pad.inputs[0])           # [B, C, S] view of a token-major [B*S, C] base
-        if prov.shape != (bs, ch, seq) or math.prod(prov.base_shape) != bs * seq * ch:
+        # the token-major source: the latest node of the chain holding [B, S, C] in row-major order
+        src = None
+        full = trace_layout(g, pad.inputs[0])
+        for cand in reversed([full.base] + full.chain):
+            if math.prod(g[cand].type.shape) != bs * seq * ch or g[cand].type.shape[-1] != ch:
+                continue
+            prov = trace_layout(g, pad.inputs[0], until=cand)
+            if prov.base == cand and prov.shape == (bs, ch, seq) and prov.matches(
+                    lambda p: (p[:, 0] * seq + p[:, 2]) * ch + p[:, 1]):
+                src = cand
+                break
+        if src is None:
             continue
-        if not prov.matches(lambda p: (p[:, 0] * seq + p[:, 2]) * ch + p[:, 1]):
-            continue
-        # the consumer: transpose back to [B, S, C], optionally through silu
-        act = None
-        y = node
+        act, y = None, node
         users = g.users(y.name)
         if len(users) == 1 and users[0].op == "silu":
             act, y = "silu", users[0]
@@ -519,15 +529,36 @@ def match_conv(g: OpGraph) -> int:
                 break
         if final is None:
             continue
+        if act is None and final.name not in g.outputs:
+            # silu applied after the transpose back (the reference's _conv does this),
+            # as one op or in its decomposed form x * sigmoid(x)
+            act_node = _silu_of(g, final.name)
+            if act_node is not None:
+                act, final = "silu", act_node
         wc = g.add_const(wv.reshape(ch, kk).contiguous(), name=g.fresh_name(w + "_dw"))
         attrs = {"batch": bs, "seq": seq, "width": ch, "kernel": kk}
         if act:
             attrs["activation"] = act
-        x2d = _ensure_2d(g, prov.base)
-        _convert(final, "conv1d", [x2d, wc.name], attrs, type=TensorType((bs * seq, ch), final.type.dtype))
+        x2d = _ensure_2d(g, src)
+        conv = g.add("conv1d", [x2d, wc.name], TensorType((bs * seq, ch), final.type.dtype), attrs,
+                     origin=f"match_conv({node.name})")
+        _rebuild_chain(g, [], conv.name, final)
         n += 1
     g.toposort()
     return n
+
+
+def _silu_of(g: OpGraph, name: str) -> OpNode | None:
+    """The node computing silu(name) if that is ``name``'s only consumer chain."""
+    users = g.users(name)
+    if len(users) == 1 and users[0].op == "silu":
+        return users[0]
+    sig = [u for u in users if u.op == "sigmoid"]
+    mul = [u for u in users if u.op == "mul" and "scalar" not in u.attrs]
+    if len(users) == 2 and len(sig) == 1 and len(mul) == 1 and sorted(mul[0].inputs) == sorted([name, sig[0].name]):
+        if g.users(sig[0].name) == [mul[0]]:
+            return mul[0]
+    return None
 
 
 def _flat(p: torch.Tensor, shape: tuple[int, ...]) -> torch.Tensor:
