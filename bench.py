@@ -83,12 +83,38 @@ def cpu_baseline(model, cfg, x, out_gpu, sample_seqs: int = 1) -> tuple[dict, di
     return base, parity
 
 
+def bench_mamba_c2(args) -> dict:
+    """Mamba-2 layer (bf16, B=2, L=1024, d=512) through compile_model."""
+    import torch
+    from targets.mamba import build_mamba_block, config_c2
+    from torch_helion import CompileConfig, compile_model
+    from torch_helion.hip.bench import bench_program
+
+    log("Mamba-2 layer (config 1)")
+    cfg = config_c2()
+    model = build_mamba_block(cfg, seed=0)
+    x = model.example_inputs(seed=0)
+    res = compile_model(model, x, CompileConfig(run_name="bench_mamba_c2", results_dir=REPO / "gpurun_out" / "results",
+                                                backend="hip", device_check=True, reference_check=False,
+                                                verify_passes=False, planner_mode="exhaustive"))
+    b = bench_program(res.device_program, x, res.hw, warmup=args.warmup, reps=args.steps)
+    us = b["us_median"]
+    return {"us": us, "tokens_per_s": cfg.batch * cfg.seq / (us * 1e-6), "kernels": len(res.program.kernels),
+            "kernels_us": {k: round(v["us"], 2) for k, v in b["kernels"].items()},
+            "kernels_frac": {k: round(v["frac"], 4) for k, v in b["kernels"].items()},
+            "parity": res.validation,
+            "config": {"workload": "mamba2-layer", "batch": cfg.batch, "seq_len": cfg.seq, "d_model": cfg.d_model,
+                       "heads": cfg.nheads, "head_dim": cfg.headdim, "d_state": cfg.d_state, "ngroups": cfg.groups,
+                       "chunk": cfg.chunk, "conv": cfg.d_conv}}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-mamba", action="store_true", help="skip the Mamba-2 layer (config 1) line")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU; --gpus must be 1 (see DESIGN.md for how the block would shard)"}))
@@ -135,6 +161,8 @@ def main() -> int:
         "kernels_frac": {k: round(v["frac"], 4) for k, v in b["kernels"].items()},
         "us_p10": b["us_p10"], "us_p90": b["us_p90"],
     }
+    if not args.no_mamba:
+        line["mamba2_layer"] = bench_mamba_c2(args)
     if not args.no_cpu_baseline:
         log("cpu baseline: oracle fp32 forward of one sequence on the host")
         base, parity = cpu_baseline(model, cfg, x, out_gpu)

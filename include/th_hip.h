@@ -147,6 +147,7 @@ typedef struct th_rmsnorm_desc {
   const float* gain;      /* [K] fp32 */
   void* out; int64_t ld_out;
   float inv_k, eps;
+  float* out32; int64_t ld_out32;   /* optional fp32 copy of out */
 } th_rmsnorm_desc;
 
 int th_rmsnorm(const th_rmsnorm_desc* desc, void* stream);
@@ -171,6 +172,64 @@ typedef struct th_attn_desc {
 } th_attn_desc;
 
 int th_attention_prefill(const th_attn_desc* desc, void* stream);
+
+/* ------------------------------------------------------------ SSD scan
+ * The Mamba-2 scan, per (batch b, head h) over token-major operands:
+ *   y_t = sum_{s<=t} (C_t . B_s) exp(cum_t - cum_s) dt_s x_s + D_h x_t  [* gate_t]
+ * evaluated chunk by chunk (states of each chunk, an inter-chunk carry, then
+ * the outputs) with every exponent a difference of running sums inside one
+ * chunk or between chunk ends, so nothing overflows at any length.
+ * Two operand forms:
+ *   ssd_chunked kind (new): cum = running sum of dt*A, with dt [T, H] and A [H];
+ *   ssd kind (reference: optimizer/evaluate.py:123-138, codegen/emit.py:254-324):
+ *   cum and dt given as [T, H*pad] with one value per head group (column
+ *   h*pad), D given as a full [T, H*P] constant.
+ * B/C are shared by heads_per_group = heads / ngroups heads.
+ */
+typedef struct th_ssd_desc {
+  int32_t batch, seq, heads, head_dim, state_dim, ngroups, chunk;
+  int32_t dtype;                      /* TH_BF16 or TH_F32: x, b, c, dt, cum, dskip, gate */
+  const void* x;  int64_t ld_x;       /* [B*S, H*P] */
+  const void* b;  int64_t ld_b;       /* [B*S, G*N] */
+  const void* c;  int64_t ld_c;       /* [B*S, G*N] */
+  const void* dt; int64_t ld_dt;      /* [B*S, H*dt_stride] */
+  int32_t dt_stride;                  /* columns between heads in dt and cum (1 or pad) */
+  int32_t pad_;
+  const void* cum; int64_t ld_cum;    /* NULL: cum from dt and A; else precomputed running sum */
+  const float* A;                     /* [H] (used when cum == NULL) */
+  const float* D;                     /* [H] or NULL */
+  const void* dskip; int64_t ld_dskip;/* optional full [B*S, H*P] D (reference form) */
+  const void* gate; int64_t ld_gate;  /* optional [B*S, H*P] multiplier of the result */
+  int32_t gate_dtype, y_dtype;
+  void* y; int64_t ld_y;              /* [B*S, H*P] */
+  float* y32; int64_t ld_y32;         /* optional fp32 copy of y */
+  float* workspace;                   /* th_ssd_workspace_bytes(...) bytes */
+  int64_t workspace_bytes;
+} th_ssd_desc;
+
+int64_t th_ssd_workspace_bytes(int32_t batch, int32_t seq, int32_t heads, int32_t head_dim,
+                               int32_t state_dim, int32_t chunk);
+
+/* One OpIR ssd / ssd_chunked KernelSpec. */
+int th_ssd_chunked(const th_ssd_desc* desc, void* stream);
+
+/* --------------------------------------------------------- conv1d kind
+ * Depthwise causal convolution over each sequence of a token-major tensor
+ * (reference eager definition: models/mamba.py:278-283, not capturable there):
+ *   y[b,t,ch] = act( sum_{j<k} w[ch,j] * x[b, t-(k-1)+j, ch] ),  x = 0 before t = 0
+ */
+typedef struct th_conv_desc {
+  int32_t batch, seq, width, kernel;
+  int32_t activation;                 /* 0 none, 1 SiLU */
+  int32_t x_dtype, y_dtype;
+  int32_t pad_;
+  const void* x; int64_t ld_x;        /* [B*S, width] */
+  const float* w;                     /* [width, kernel] fp32 */
+  void* y; int64_t ld_y;
+  float* y32; int64_t ld_y32;         /* optional fp32 copy */
+} th_conv_desc;
+
+int th_conv1d_causal(const th_conv_desc* desc, void* stream);
 
 /* ------------------------------------------------- epilogue VM (fallback)
  * Evaluates an OpIR epilogue SSA (registered ops, reference:

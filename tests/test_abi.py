@@ -45,7 +45,7 @@ def test_every_declared_symbol_is_exported_and_bound(lib):
 
 _STRUCTS = {
     "th_epi_out": "EpiOut", "th_gemm_desc": "GemmDesc", "th_rmsnorm_desc": "RmsNormDesc",
-    "th_attn_desc": "AttnDesc", "th_vm_operand": "VmOperand", "th_vm_op": "VmOp", "th_vm_out": "VmOut",
+    "th_attn_desc": "AttnDesc", "th_ssd_desc": "SsdDesc", "th_conv_desc": "ConvDesc", "th_vm_operand": "VmOperand", "th_vm_op": "VmOp", "th_vm_out": "VmOut",
     "th_vm_desc": "VmDesc",
 }
 
@@ -116,7 +116,7 @@ def test_gemm_rejects_bad_descriptors(lib, field, value, msg):
 def test_null_descriptors_are_rejected(lib):
     from torch_helion.hip import abi
 
-    for fn in ("th_gemm", "th_rmsnorm", "th_attention_prefill", "th_epilogue_vm"):
+    for fn in ("th_gemm", "th_rmsnorm", "th_attention_prefill", "th_epilogue_vm", "th_ssd_chunked", "th_conv1d_causal"):
         assert getattr(lib, fn)(None, None) == abi.TH_ERR_INVALID, fn
         assert "null descriptor" in abi.last_error(lib)
 

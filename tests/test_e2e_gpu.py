@@ -92,3 +92,45 @@ def test_device_program_reruns_are_identical(gpu, tmp_path):
     a = res.run(*x)[0].clone()
     b = res.run(*x)[0].clone()
     assert torch.equal(a, b)
+
+
+def _mamba_oracle(model, cfg, x):
+    from oracle.mamba import backbone_forward
+
+    return backbone_forward(x.double(), {k: v.double() for k, v in model.state_dict().items()}, cfg)
+
+
+def test_mamba_block_fp32_conv_groups(gpu, tmp_path):
+    import math
+
+    from targets.mamba import MambaConfig, build_mamba_block
+
+    announce("e2e mamba fp32 conv ngroups=1")
+    cfg = MambaConfig(batch=2, seq=256, d_model=256, expand=2, headdim=64, d_state=64, chunk=64, n_layers=1,
+                      ngroups=1, use_conv=True, dtype=torch.float32, a_log_range=(0.0, math.log(16.0)))
+    m = build_mamba_block(cfg, seed=0)
+    x = m.example_inputs(seed=0)
+    res = _compile(m, x, tmp_path, "mamba_fp32")
+    kinds = [k.kind for k in res.program.kernels]
+    assert "ssd_chunked" in kinds and "conv1d" in kinds, kinds
+    out = res.run(*x)[0].double().cpu()
+    ref = _mamba_oracle(m, cfg, x[0])
+    rel = ((out - ref).abs().max() / ref.abs().max()).item()
+    assert rel < 1e-4, rel
+
+
+def test_mamba_layer_c2_bf16(gpu, tmp_path):
+    """BASELINE config 1 (C2): Mamba-2 block bf16, B=2, L=1024, d=512, 16 heads x 64, N=64, G=1, conv 4, chunk 64."""
+    from targets.mamba import build_mamba_block, config_c2
+
+    announce("e2e mamba C2 bf16")
+    cfg = config_c2()
+    m = build_mamba_block(cfg, seed=0)
+    x = m.example_inputs(seed=0)
+    res = _compile(m, x, tmp_path, "mamba_c2")
+    assert res.validation["ok"], res.validation
+    out = res.device_program.outputs(fp32=True)[0].double().cpu()
+    ref = _mamba_oracle(m, cfg, x[0])
+    rel = ((out - ref).abs().max() / ref.abs().max()).item()
+    assert rel < 2e-2, rel
+    assert (out - ref).abs().max().item() < 5e-2

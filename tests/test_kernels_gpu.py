@@ -249,3 +249,87 @@ def test_epilogue_vm(gpu):
     ops.epilogue_vm(M, N, [(x.to(gpu), False), (col.to(gpu), True)], ops_, [(out, 4)], 6, ws)
     torch.cuda.synchronize()
     assert _maxabs(out, ref) < 1e-2
+
+
+def _ssd_case(bs, s, h, p, n, g, dtype, seed):
+    gen = torch.Generator().manual_seed(seed)
+    x = torch.randn(bs * s, h * p, generator=gen)
+    bm = torch.randn(bs * s, g * n, generator=gen) * 0.5
+    cm = torch.randn(bs * s, g * n, generator=gen) * 0.5
+    dt = torch.rand(bs * s, h, generator=gen) * 0.099 + 0.001
+    A = -torch.exp(torch.rand(h, generator=gen) * math.log(16.0))
+    D = torch.rand(h, generator=gen)
+    gate = torch.randn(bs * s, h * p, generator=gen)
+    return [t.to(dtype) for t in (x, bm, cm, dt)] + [A, D, gate.to(dtype)]
+
+
+@pytest.mark.parametrize("bs,s,h,p,n,g,chunk,dtype", [
+    (2, 256, 4, 64, 64, 1, 64, torch.float32), (1, 200, 4, 32, 32, 2, 64, torch.float32),
+    (2, 512, 2, 64, 128, 1, 256, torch.float32), (2, 1024, 16, 64, 64, 1, 64, torch.bfloat16),
+])
+def test_ssd_chunked_vs_recurrence(gpu, bs, s, h, p, n, g, chunk, dtype):
+    from oracle.mamba import ssd_chunked_program
+    from torch_helion.hip import ops
+
+    announce(f"ssd_chunked bs={bs} s={s} h={h} p={p} n={n} g={g} chunk={chunk} {dtype}")
+    x, bm, cm, dt, A, D, gate = _ssd_case(bs, s, h, p, n, g, dtype, seed=s + h)
+    a = {"batch": bs, "seq": s, "heads": h, "head_dim": p, "state_dim": n, "ngroups": g}
+    ref = ssd_chunked_program(cm.double(), bm.double(), x.double(), dt.double(), A.double(), D.double(), a)
+    ref = ref * gate.double()
+    ws = torch.empty(ops.ssd_workspace_bytes(bs, s, h, p, n, chunk) // 4 + 1, device=gpu)
+    out = torch.empty(bs * s, h * p, dtype=dtype, device=gpu)
+    out32 = torch.empty(bs * s, h * p, device=gpu)
+    ops.ssd_chunked(x=x.to(gpu), b=bm.to(gpu), c=cm.to(gpu), dt=dt.to(gpu), out=out, out32=out32, workspace=ws,
+                    batch=bs, seq=s, heads=h, head_dim=p, state_dim=n, ngroups=g, chunk=chunk, A=A.to(gpu),
+                    D=D.to(gpu), gate=gate.to(gpu))
+    torch.cuda.synchronize()
+    if dtype == torch.float32:
+        assert _rel(out32, ref) < F32_REL
+    else:
+        assert _maxabs(out32, ref) < BF16_TOL
+
+
+def test_ssd_reference_form_padded_cum(gpu):
+    """The reference's ssd kind: cum and dt padded to 32 columns per head, cum centred, full D."""
+    from oracle.interpret import ssd_quadratic
+    from torch_helion.hip import ops
+
+    announce("ssd reference form")
+    bs, s, h, p, n, pad = 2, 256, 4, 32, 32, 32
+    x, bm, cm, dt, A, D, _ = _ssd_case(bs, s, h, p, n, h, torch.float32, seed=11)
+    da = (dt * A).reshape(bs, s, h)
+    cum = torch.cumsum(da, 1) - 0.5 * da.sum(1, keepdim=True)             # centred per sequence
+    cum_pad = cum.reshape(bs * s, h, 1).expand(bs * s, h, pad).reshape(bs * s, h * pad).contiguous()
+    dt_pad = dt.reshape(bs * s, h, 1).expand(bs * s, h, pad).reshape(bs * s, h * pad).contiguous()
+    d_full = D.repeat_interleave(p).reshape(1, -1).expand(bs * s, h * p).contiguous()
+    mask = torch.ones(s, s).tril()
+    attrs = {"batch": bs, "seq": s, "heads": h, "head_dim": p, "state_dim": n, "pad": pad}
+    ref = ssd_quadratic(cm.double(), bm.double(), x.double(), cum_pad.double(), dt_pad.double(), mask.double(),
+                        d_full.double(), attrs)
+    ws = torch.empty(ops.ssd_workspace_bytes(bs, s, h, p, n, 64) // 4 + 1, device=gpu)
+    out = torch.empty(bs * s, h * p, device=gpu)
+    ops.ssd_chunked(x=x.to(gpu), b=bm.to(gpu), c=cm.to(gpu), dt=dt_pad.to(gpu), out=out, workspace=ws, batch=bs,
+                    seq=s, heads=h, head_dim=p, state_dim=n, ngroups=h, chunk=64, cum=cum_pad.to(gpu), dt_stride=pad,
+                    dskip=d_full.to(gpu))
+    torch.cuda.synchronize()
+    assert _rel(out, ref) < F32_REL
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_conv1d_causal(gpu, dtype):
+    from oracle.interpret import conv1d
+    from torch_helion.hip import ops
+
+    announce(f"conv1d {dtype}")
+    bs, s, c, k = 2, 300, 1152, 4
+    gen = torch.Generator().manual_seed(5)
+    x = torch.randn(bs * s, c, generator=gen).to(dtype)
+    w = torch.randn(c, k, generator=gen) * 0.3
+    ref = conv1d(x.double(), w.double(), {"batch": bs, "seq": s, "activation": "silu"})
+    out = torch.empty(bs * s, c, dtype=dtype, device=gpu)
+    ops.conv1d_causal(x.to(gpu), w.to(gpu), out, batch=bs, seq=s, activation="silu")
+    torch.cuda.synchronize()
+    if dtype == torch.float32:
+        assert _rel(out, ref) < F32_REL
+    else:
+        assert _maxabs(out, ref) < BF16_TOL

@@ -22,6 +22,8 @@ struct NormK {
   int64_t M, K;
   int xdt, odt;
   float inv_k, eps;
+  float* out32;
+  int64_t ldo32;
 };
 
 // NCH = 16-byte chunks per lane held in registers (0 = stream the row twice).
@@ -76,6 +78,10 @@ __global__ void __launch_bounds__(256) rmsnorm_kernel(NormK p) {
     chunk_vals(w, v);
     const int64_t base = c * per;
     for (int q = 0; q < per; ++q) v[q] = v[q] * r * p.gain[base + q];
+    if (p.out32) {
+      float* o32 = p.out32 + row * p.ldo32 + base;
+      for (int q = 0; q < per; ++q) o32[q] = v[q];
+    }
     if (p.odt == TH_BF16) {
       uint16_t* orow = (uint16_t*)p.out + row * p.ldo + base;
       if (per == 8) {
@@ -196,6 +202,8 @@ extern "C" int th_rmsnorm(const th_rmsnorm_desc* d, void* stream) {
   NormK k{};
   k.x = d->x; k.ldx = d->ld_x; k.out = d->out; k.ldo = d->ld_out; k.gain = d->gain;
   k.M = d->M; k.K = d->K; k.xdt = d->x_dtype; k.odt = d->out_dtype; k.inv_k = d->inv_k; k.eps = d->eps;
+  k.out32 = d->out32; k.ldo32 = d->ld_out32;
+  TH_CHECK_ARG(!d->out32 || d->ld_out32 >= d->K, "th_rmsnorm: ld_out32 < K");
   const int64_t nch = d->K / per;
   const dim3 grid((unsigned)cdiv(d->M, 4));
   hipStream_t s = (hipStream_t)stream;

@@ -1,0 +1,377 @@
+// Mamba-2 SSD scan (ssd / ssd_chunked kinds) and the depthwise causal conv1d.
+//
+// Scan, per (batch b, head h), in three launches:
+//   1. ssd_state_kernel   one workgroup per chunk: the running sum ``cl`` of
+//      dt*A inside the chunk (an LDS scan), w_l = dt_l exp(cl_last - cl_l) and
+//      the chunk state S_c[p, n] = sum_l x_l[p] w_l B_l[n];
+//   2. ssd_carry_kernel   per state element, sequentially over chunks:
+//      H_0 = 0, H_{c+1} = exp(tot_c) H_c + S_c (tot_c = the chunk's total decay);
+//   3. ssd_out_kernel     one workgroup per (chunk, 64-row block): the state
+//      term exp(cl_t) C_t . H_c, the within-chunk term
+//      sum_{s<=t} (C_t . B_s) exp(cl_t - cl_s) dt_s x_s, plus D x_t, times gate.
+// Every exponent is a difference of running sums within a chunk or a chunk
+// total, so no exponent is positive except through round-off. All arithmetic is
+// fp32 (VALU), operands are staged in LDS; states live in a caller workspace.
+//
+// The reference's own ``ssd`` kind passes the running sum ``cum`` directly
+// (already centred, reference optimizer/passes.py:501-525); only differences of
+// it are used here, so its centring offset cancels.
+#include <algorithm>
+
+#include "common.h"
+
+namespace th {
+
+struct SsdK {
+  int B, S, H, P, N, G, Q, nc, hpg, RB, dt_stride, dtype;
+  const void* x; int64_t ldx;
+  const void* b; int64_t ldb;
+  const void* c; int64_t ldc;
+  const void* dt; int64_t lddt;
+  const void* cum; int64_t ldcum;
+  const float* A;
+  const float* D;
+  const void* dskip; int64_t lddskip;
+  const void* gate; int64_t ldgate; int gdt;
+  void* y; int64_t ldy; int ydt;
+  float* y32; int64_t ldy32;
+  float* states;  // [B][H][nc][P*N]
+  float* tot;     // [B][H][nc]
+};
+
+// Running sum of dA (or the given cum re-based) for chunk ``c`` into cl[0..Q),
+// dt into dts[0..Q); rows past the end of the sequence get dt = 0 and repeat
+// the last running sum. Needs 2*256 floats of scratch in ``tmp``.
+__device__ void chunk_running_sum(const SsdK& p, int b, int h, int c, float* cl, float* dts, float* tmp) {
+  const int tid = threadIdx.x;
+  const int t0 = c * p.Q;
+  const int rows = min(p.Q, p.S - t0);
+  float v = 0.f, dtv = 0.f;
+  if (tid < p.Q) {
+    const int l = min(tid, rows - 1);
+    const int64_t tok = (int64_t)b * p.S + t0 + l;
+    const float d = load_elem(p.dt, tok * p.lddt + (int64_t)h * p.dt_stride, p.dtype);
+    dtv = tid < rows ? d : 0.f;
+    if (p.cum == nullptr) {
+      v = tid < rows ? d * p.A[h] : 0.f;
+    } else {
+      v = load_elem(p.cum, tok * p.ldcum + (int64_t)h * p.dt_stride, p.dtype);
+    }
+  }
+  if (p.cum == nullptr) {
+    // inclusive Hillis-Steele scan over Q <= 256 values
+    float* a = tmp;
+    float* bb = tmp + 256;
+    a[tid] = v;
+    __syncthreads();
+    for (int off = 1; off < p.Q; off <<= 1) {
+      float s = a[tid];
+      if (tid >= off && tid < p.Q) s += a[tid - off];
+      bb[tid] = s;
+      __syncthreads();
+      float* t = a; a = bb; bb = t;
+    }
+    if (tid < p.Q) cl[tid] = a[tid];
+  } else {
+    // re-base on the running sum just before the chunk (its first row for chunk 0,
+    // where no earlier state exists and only differences are used)
+    float base;
+    if (c == 0) {
+      base = load_elem(p.cum, ((int64_t)b * p.S) * p.ldcum + (int64_t)h * p.dt_stride, p.dtype);
+    } else {
+      base = load_elem(p.cum, ((int64_t)b * p.S + t0 - 1) * p.ldcum + (int64_t)h * p.dt_stride, p.dtype);
+    }
+    if (tid < p.Q) cl[tid] = v - base;
+  }
+  if (tid < p.Q) dts[tid] = dtv;
+  __syncthreads();
+}
+
+__global__ void __launch_bounds__(256) ssd_state_kernel(SsdK p) {
+  extern __shared__ float sm[];
+  float* cl = sm;            // 256
+  float* dts = cl + 256;     // 256
+  float* tmp = dts + 256;    // 512
+  float* xs = tmp + 512;     // 32 * P
+  float* bs = xs + 32 * p.P; // 32 * N
+  const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z, tid = threadIdx.x;
+  const int g = h / p.hpg;
+  chunk_running_sum(p, b, h, c, cl, dts, tmp);
+  const int t0 = c * p.Q;
+  const int rows = min(p.Q, p.S - t0);
+  const float last = cl[p.Q - 1];
+  const int PN = p.P * p.N;
+  const int no = PN / 256;  // P*N is a multiple of 256 (checked on the host)
+  float acc[64];
+#pragma unroll
+  for (int i = 0; i < 64; ++i) acc[i] = 0.f;
+  for (int l0 = 0; l0 < rows; l0 += 32) {
+    for (int e = tid; e < 32 * p.P; e += 256) {
+      const int ll = e / p.P, pp = e - ll * p.P;
+      const int l = l0 + ll;
+      float v = 0.f;
+      if (l < rows) {
+        const int64_t tok = (int64_t)b * p.S + t0 + l;
+        v = load_elem(p.x, tok * p.ldx + (int64_t)h * p.P + pp, p.dtype) * dts[l] * __expf(last - cl[l]);
+      }
+      xs[e] = v;
+    }
+    for (int e = tid; e < 32 * p.N; e += 256) {
+      const int ll = e / p.N, nn = e - ll * p.N;
+      const int l = l0 + ll;
+      bs[e] = l < rows ? load_elem(p.b, ((int64_t)b * p.S + t0 + l) * p.ldb + (int64_t)g * p.N + nn, p.dtype) : 0.f;
+    }
+    __syncthreads();
+    for (int ll = 0; ll < 32; ++ll) {
+#pragma unroll
+      for (int i = 0; i < 64; ++i) {
+        if (i < no) {
+          const int o = tid + 256 * i;
+          const int pp = o / p.N, nn = o - pp * p.N;
+          acc[i] += xs[ll * p.P + pp] * bs[ll * p.N + nn];
+        }
+      }
+    }
+    __syncthreads();
+  }
+  float* st = p.states + (((int64_t)b * p.H + h) * p.nc + c) * PN;
+#pragma unroll
+  for (int i = 0; i < 64; ++i)
+    if (i < no) st[tid + 256 * i] = acc[i];
+  if (tid == 0) p.tot[((int64_t)b * p.H + h) * p.nc + c] = last;
+}
+
+__global__ void __launch_bounds__(256) ssd_carry_kernel(SsdK p) {
+  const int h = blockIdx.y, b = blockIdx.z;
+  const int PN = p.P * p.N;
+  const int e = blockIdx.x * 256 + threadIdx.x;
+  if (e >= PN) return;
+  float* st = p.states + ((int64_t)b * p.H + h) * p.nc * PN;
+  const float* tot = p.tot + ((int64_t)b * p.H + h) * p.nc;
+  float carry = 0.f;
+  for (int c = 0; c < p.nc; ++c) {
+    const float s = st[(int64_t)c * PN + e];
+    st[(int64_t)c * PN + e] = carry;
+    carry = (c == 0 ? 0.f : __expf(tot[c]) * carry) + s;
+  }
+}
+
+__global__ void __launch_bounds__(256) ssd_out_kernel(SsdK p) {
+  extern __shared__ float sm[];
+  const int RB = p.RB, P = p.P, N = p.N;
+  float* cl = sm;                       // 256
+  float* dts = cl + 256;                // 256
+  float* tmp = dts + 256;               // 512
+  float* cs = tmp + 512;                // RB * (N+1)
+  float* region = cs + RB * (N + 1);    // Hs [P*(N+1)]  |  Bs [RB*(N+1)] + Xs [RB*(P+1)] + M [RB*(RB+1)]
+  float* hs = region;
+  float* bsm = region;
+  float* xsm = bsm + RB * (N + 1);
+  float* msm = xsm + RB * (P + 1);
+  const int nrb = p.Q / RB;
+  const int c = blockIdx.x / nrb, rbi = blockIdx.x - c * nrb;
+  const int h = blockIdx.y, b = blockIdx.z, tid = threadIdx.x;
+  const int g = h / p.hpg;
+  chunk_running_sum(p, b, h, c, cl, dts, tmp);
+  const int t0 = c * p.Q;
+  const int rows = min(p.Q, p.S - t0);
+  const int r0 = rbi * RB;
+  if (r0 >= rows) return;  // whole row block past the end of the sequence (uniform per workgroup)
+  const int tpr = 256 / RB;            // threads per output row
+  const int pc = P / tpr;              // columns per thread
+  const int r = tid / tpr, q = tid - r * tpr;
+  const int64_t tok0 = (int64_t)b * p.S + t0;
+  float acc[32];
+#pragma unroll
+  for (int i = 0; i < 32; ++i) acc[i] = 0.f;
+
+  for (int e = tid; e < RB * N; e += 256) {
+    const int rr = e / N, nn = e - rr * N;
+    cs[rr * (N + 1) + nn] = (r0 + rr < rows) ? load_elem(p.c, (tok0 + r0 + rr) * p.ldc + (int64_t)g * N + nn, p.dtype) : 0.f;
+  }
+  // state entering the chunk (zero for the first chunk)
+  if (c > 0) {
+    const float* st = p.states + (((int64_t)b * p.H + h) * p.nc + c) * (int64_t)(P * N);
+    for (int e = tid; e < P * N; e += 256) {
+      const int pp = e / N, nn = e - pp * N;
+      hs[pp * (N + 1) + nn] = st[e];
+    }
+    __syncthreads();
+    const float* crow = cs + r * (N + 1);
+    for (int n = 0; n < N; ++n) {
+      const float cv = crow[n];
+#pragma unroll
+      for (int i = 0; i < 32; ++i)
+        if (i < pc) acc[i] += cv * hs[(q + tpr * i) * (N + 1) + n];
+    }
+    const float sc = __expf(cl[r0 + r]);
+#pragma unroll
+    for (int i = 0; i < 32; ++i) acc[i] *= sc;
+  }
+  __syncthreads();
+  // within the chunk: row blocks jb <= rbi
+  for (int jb = 0; jb <= rbi; ++jb) {
+    const int j0 = jb * RB;
+    for (int e = tid; e < RB * N; e += 256) {
+      const int jj = e / N, nn = e - jj * N;
+      bsm[jj * (N + 1) + nn] = (j0 + jj < rows) ? load_elem(p.b, (tok0 + j0 + jj) * p.ldb + (int64_t)g * N + nn, p.dtype) : 0.f;
+    }
+    for (int e = tid; e < RB * P; e += 256) {
+      const int jj = e / P, pp = e - jj * P;
+      xsm[jj * (P + 1) + pp] = (j0 + jj < rows) ? load_elem(p.x, (tok0 + j0 + jj) * p.ldx + (int64_t)h * P + pp, p.dtype) : 0.f;
+    }
+    __syncthreads();
+    // M[r][j] = (C_r . B_j) exp(cl_r - cl_j) dt_j  for j <= r
+    for (int e = tid; e < RB * RB; e += 256) {
+      const int rr = e / RB, jj = e - rr * RB;
+      float m = 0.f;
+      if (j0 + jj <= r0 + rr && j0 + jj < rows) {
+        float dot = 0.f;
+        const float* crow = cs + rr * (N + 1);
+        const float* brow = bsm + jj * (N + 1);
+        for (int n = 0; n < N; ++n) dot += crow[n] * brow[n];
+        m = dot * __expf(cl[r0 + rr] - cl[j0 + jj]) * dts[j0 + jj];
+      }
+      msm[rr * (RB + 1) + jj] = m;
+    }
+    __syncthreads();
+    const float* mrow = msm + r * (RB + 1);
+    for (int j = 0; j < RB; ++j) {
+      const float m = mrow[j];
+#pragma unroll
+      for (int i = 0; i < 32; ++i)
+        if (i < pc) acc[i] += m * xsm[j * (P + 1) + q + tpr * i];
+    }
+    __syncthreads();
+  }
+  if (r0 + r >= rows) return;
+  const int64_t tok = tok0 + r0 + r;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {
+    if (i >= pc) continue;
+    const int pp = q + tpr * i;
+    const int64_t col = (int64_t)h * P + pp;
+    const float xv = load_elem(p.x, tok * p.ldx + col, p.dtype);
+    float v = acc[i];
+    if (p.dskip) v += xv * load_elem(p.dskip, tok * p.lddskip + col, p.dtype);
+    else if (p.D) v += xv * p.D[h];
+    if (p.gate) v *= load_elem(p.gate, tok * p.ldgate + col, p.gdt);
+    store_elem(p.y, tok * p.ldy + col, p.ydt, v);
+    if (p.y32) p.y32[tok * p.ldy32 + col] = v;
+  }
+}
+
+// ------------------------------------------------------------------ conv1d
+struct ConvK {
+  int B, S, W, K, act, xdt, ydt;
+  const void* x; int64_t ldx;
+  const float* w;
+  void* y; int64_t ldy;
+  float* y32; int64_t ldy32;
+};
+
+__global__ void __launch_bounds__(256) conv1d_causal_kernel(ConvK p) {
+  const int ch = blockIdx.y * 256 + threadIdx.x;
+  const int64_t tok = blockIdx.x;  // b*S + t
+  if (ch >= p.W) return;
+  const int t = (int)(tok % p.S);
+  float acc = 0.f;
+  for (int j = 0; j < p.K; ++j) {
+    const int tt = t - (p.K - 1) + j;
+    if (tt < 0) continue;
+    acc += p.w[(int64_t)ch * p.K + j] * load_elem(p.x, (tok - (p.K - 1) + j) * p.ldx + ch, p.xdt);
+  }
+  if (p.act == 1) acc = acc * sigmoidf_(acc);
+  store_elem(p.y, tok * p.ldy + ch, p.ydt, acc);
+  if (p.y32) p.y32[tok * p.ldy32 + ch] = acc;
+}
+
+static size_t state_lds(int P, int N) { return (size_t)(256 * 4 + 32 * P + 32 * N) * 4; }
+static size_t out_lds(int RB, int P, int N) {
+  const size_t intra = (size_t)RB * (N + 1) + (size_t)RB * (P + 1) + (size_t)RB * (RB + 1);
+  const size_t inter = (size_t)P * (N + 1);
+  return (size_t)(256 * 4 + RB * (N + 1) + std::max(intra, inter)) * 4;
+}
+
+}  // namespace th
+
+using namespace th;
+
+extern "C" int64_t th_ssd_workspace_bytes(int32_t batch, int32_t seq, int32_t heads, int32_t head_dim,
+                                          int32_t state_dim, int32_t chunk) {
+  if (batch <= 0 || seq <= 0 || heads <= 0 || head_dim <= 0 || state_dim <= 0 || chunk <= 0) return -1;
+  const int64_t nc = cdiv(seq, chunk);
+  return (int64_t)batch * heads * nc * ((int64_t)head_dim * state_dim + 1) * 4;
+}
+
+extern "C" int th_ssd_chunked(const th_ssd_desc* d, void* stream) {
+  TH_CHECK_ARG(d != nullptr, "th_ssd_chunked: null descriptor");
+  TH_CHECK_ARG(d->batch > 0 && d->seq > 0 && d->heads > 0 && d->head_dim > 0 && d->state_dim > 0,
+               "th_ssd_chunked: sizes must be positive");
+  TH_CHECK_ARG(d->chunk > 0 && d->chunk <= 256 && (d->chunk <= 64 || d->chunk % 64 == 0),
+               "th_ssd_chunked: chunk %d must be <= 64 or a multiple of 64 up to 256", d->chunk);
+  const int g = d->ngroups > 0 ? d->ngroups : d->heads;
+  TH_CHECK_ARG(d->heads % g == 0, "th_ssd_chunked: heads %d not a multiple of ngroups %d", d->heads, g);
+  TH_CHECK_ARG(d->head_dim <= 128 && d->state_dim <= 128, "th_ssd_chunked: head_dim/state_dim above 128");
+  TH_CHECK_ARG((d->head_dim * d->state_dim) % 256 == 0, "th_ssd_chunked: head_dim*state_dim must be a multiple of 256");
+  TH_CHECK_ARG(d->dtype == TH_BF16 || d->dtype == TH_F32, "th_ssd_chunked: dtype unsupported");
+  TH_CHECK_ARG(d->y_dtype == TH_BF16 || d->y_dtype == TH_F32, "th_ssd_chunked: y_dtype unsupported");
+  TH_CHECK_ARG(d->x && d->b && d->c && d->dt && d->y && d->workspace, "th_ssd_chunked: null operand");
+  TH_CHECK_ARG(d->cum != nullptr || d->A != nullptr, "th_ssd_chunked: needs A or cum");
+  TH_CHECK_ARG(d->dt_stride >= 1, "th_ssd_chunked: dt_stride must be >= 1");
+  TH_CHECK_ARG(!d->gate || d->gate_dtype == TH_BF16 || d->gate_dtype == TH_F32, "th_ssd_chunked: gate dtype");
+  const int64_t need = th_ssd_workspace_bytes(d->batch, d->seq, d->heads, d->head_dim, d->state_dim, d->chunk);
+  TH_CHECK_ARG(d->workspace_bytes >= need, "th_ssd_chunked: workspace %lld < %lld bytes", (long long)d->workspace_bytes,
+               (long long)need);
+  const int RB = std::min(d->chunk, 64);
+  TH_CHECK_ARG(256 % RB == 0 && d->head_dim % (256 / RB) == 0 && d->head_dim / (256 / RB) <= 32,
+               "th_ssd_chunked: head_dim %d does not fit the row-block mapping", d->head_dim);
+  if (!device_ready()) {
+    set_error("th_ssd_chunked: th_init was not called for the current device");
+    return TH_ERR_NOT_INIT;
+  }
+  SsdK k{};
+  k.B = d->batch; k.S = d->seq; k.H = d->heads; k.P = d->head_dim; k.N = d->state_dim; k.G = g;
+  k.Q = d->chunk; k.nc = (int)cdiv(d->seq, d->chunk); k.hpg = d->heads / g; k.RB = RB; k.dt_stride = d->dt_stride;
+  k.dtype = d->dtype;
+  k.x = d->x; k.ldx = d->ld_x; k.b = d->b; k.ldb = d->ld_b; k.c = d->c; k.ldc = d->ld_c;
+  k.dt = d->dt; k.lddt = d->ld_dt; k.cum = d->cum; k.ldcum = d->ld_cum; k.A = d->A; k.D = d->D;
+  k.dskip = d->dskip; k.lddskip = d->ld_dskip; k.gate = d->gate; k.ldgate = d->ld_gate; k.gdt = d->gate_dtype;
+  k.y = d->y; k.ldy = d->ld_y; k.ydt = d->y_dtype; k.y32 = d->y32; k.ldy32 = d->ld_y32;
+  k.states = d->workspace;
+  k.tot = d->workspace + (int64_t)k.B * k.H * k.nc * k.P * k.N;
+  hipStream_t s = (hipStream_t)stream;
+  const size_t l1 = state_lds(k.P, k.N), l3 = out_lds(RB, k.P, k.N);
+  TH_CHECK_HIP(hipFuncSetAttribute((const void*)ssd_state_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)l1));
+  TH_CHECK_HIP(hipFuncSetAttribute((const void*)ssd_out_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)l3));
+  hipLaunchKernelGGL(ssd_state_kernel, dim3(k.nc, k.H, k.B), dim3(256), l1, s, k);
+  TH_CHECK_LAUNCH();
+  hipLaunchKernelGGL(ssd_carry_kernel, dim3((unsigned)cdiv(k.P * k.N, 256), k.H, k.B), dim3(256), 0, s, k);
+  TH_CHECK_LAUNCH();
+  hipLaunchKernelGGL(ssd_out_kernel, dim3(k.nc * (k.Q / RB), k.H, k.B), dim3(256), l3, s, k);
+  TH_CHECK_LAUNCH();
+  return TH_OK;
+}
+
+extern "C" int th_conv1d_causal(const th_conv_desc* d, void* stream) {
+  TH_CHECK_ARG(d != nullptr, "th_conv1d_causal: null descriptor");
+  TH_CHECK_ARG(d->batch > 0 && d->seq > 0 && d->width > 0 && d->kernel > 0 && d->kernel <= 8,
+               "th_conv1d_causal: bad sizes (kernel must be 1..8)");
+  TH_CHECK_ARG(d->x && d->w && d->y, "th_conv1d_causal: null operand");
+  TH_CHECK_ARG((d->x_dtype == TH_BF16 || d->x_dtype == TH_F32) && (d->y_dtype == TH_BF16 || d->y_dtype == TH_F32),
+               "th_conv1d_causal: dtype unsupported");
+  TH_CHECK_ARG(d->ld_x >= d->width && d->ld_y >= d->width, "th_conv1d_causal: row stride < width");
+  TH_CHECK_ARG(d->activation == 0 || d->activation == 1, "th_conv1d_causal: activation %d unknown", d->activation);
+  if (!device_ready()) {
+    set_error("th_conv1d_causal: th_init was not called for the current device");
+    return TH_ERR_NOT_INIT;
+  }
+  ConvK k{};
+  k.B = d->batch; k.S = d->seq; k.W = d->width; k.K = d->kernel; k.act = d->activation;
+  k.xdt = d->x_dtype; k.ydt = d->y_dtype; k.x = d->x; k.ldx = d->ld_x; k.w = d->w;
+  k.y = d->y; k.ldy = d->ld_y; k.y32 = d->y32; k.ldy32 = d->ld_y32;
+  hipLaunchKernelGGL(conv1d_causal_kernel, dim3((unsigned)((int64_t)k.B * k.S), (unsigned)cdiv(k.W, 256)), dim3(256), 0,
+                     (hipStream_t)stream, k);
+  TH_CHECK_LAUNCH();
+  return TH_OK;
+}

@@ -68,6 +68,7 @@ class RmsNormDesc(C.Structure):
         ("M", _i64), ("K", _i64),
         ("x", _p), ("ld_x", _i64), ("x_dtype", _i32), ("out_dtype", _i32),
         ("gain", _p), ("out", _p), ("ld_out", _i64), ("inv_k", C.c_float), ("eps", C.c_float),
+        ("out32", _p), ("ld_out32", _i64),
     ]
 
 
@@ -77,6 +78,26 @@ class AttnDesc(C.Structure):
         ("head_dim", _i32), ("scale", C.c_float), ("causal", _i32), ("dtype", _i32), ("pad_", _i32),
         ("q", _p), ("ld_q", _i64), ("k", _p), ("ld_k", _i64), ("v", _p), ("ld_v", _i64),
         ("o", _p), ("ld_o", _i64),
+    ]
+
+
+class SsdDesc(C.Structure):
+    _fields_ = [
+        ("batch", _i32), ("seq", _i32), ("heads", _i32), ("head_dim", _i32), ("state_dim", _i32), ("ngroups", _i32),
+        ("chunk", _i32), ("dtype", _i32),
+        ("x", _p), ("ld_x", _i64), ("b", _p), ("ld_b", _i64), ("c", _p), ("ld_c", _i64), ("dt", _p), ("ld_dt", _i64),
+        ("dt_stride", _i32), ("pad_", _i32),
+        ("cum", _p), ("ld_cum", _i64), ("A", _p), ("D", _p), ("dskip", _p), ("ld_dskip", _i64),
+        ("gate", _p), ("ld_gate", _i64), ("gate_dtype", _i32), ("y_dtype", _i32),
+        ("y", _p), ("ld_y", _i64), ("y32", _p), ("ld_y32", _i64), ("workspace", _p), ("workspace_bytes", _i64),
+    ]
+
+
+class ConvDesc(C.Structure):
+    _fields_ = [
+        ("batch", _i32), ("seq", _i32), ("width", _i32), ("kernel", _i32), ("activation", _i32),
+        ("x_dtype", _i32), ("y_dtype", _i32), ("pad_", _i32),
+        ("x", _p), ("ld_x", _i64), ("w", _p), ("y", _p), ("ld_y", _i64), ("y32", _p), ("ld_y32", _i64),
     ]
 
 
@@ -113,6 +134,9 @@ SIGNATURES: dict[str, tuple] = {
     "th_rmsnorm": (_i32, [C.POINTER(RmsNormDesc), _p]),
     "th_attention_prefill": (_i32, [C.POINTER(AttnDesc), _p]),
     "th_epilogue_vm": (_i32, [C.POINTER(VmDesc), _p]),
+    "th_ssd_workspace_bytes": (_i64, [_i32, _i32, _i32, _i32, _i32, _i32]),
+    "th_ssd_chunked": (_i32, [C.POINTER(SsdDesc), _p]),
+    "th_conv1d_causal": (_i32, [C.POINTER(ConvDesc), _p]),
 }
 
 

@@ -138,7 +138,7 @@ def gemm(call: GemmCall, kernel: str | None = None) -> None:
 
 # --------------------------------------------------------------- RMSNorm
 def rmsnorm(x: torch.Tensor, gain: torch.Tensor, eps: float, out: torch.Tensor, inv_k: float | None = None,
-            kernel: str | None = None) -> torch.Tensor:
+            kernel: str | None = None, out32: torch.Tensor | None = None) -> torch.Tensor:
     lib = _lib(x)
     d = abi.RmsNormDesc()
     d.M, d.K = x.shape
@@ -149,6 +149,8 @@ def rmsnorm(x: torch.Tensor, gain: torch.Tensor, eps: float, out: torch.Tensor, 
     d.gain = gain.data_ptr()
     d.inv_k = 1.0 / x.shape[1] if inv_k is None else inv_k
     d.eps = eps
+    if out32 is not None:
+        d.out32, d.ld_out32 = out32.data_ptr(), _row_major(out32, "th_rmsnorm out32")
     abi.check(lib.th_rmsnorm(C.byref(d), _stream(x)), "th_rmsnorm", kernel)
     return out
 
@@ -195,3 +197,54 @@ def epilogue_vm(M: int, N: int, operands: list[tuple[torch.Tensor, bool]], ops: 
         d.out[i].ptr, d.out[i].ld, d.out[i].dtype, d.out[i].slot = t.data_ptr(), _row_major(t, "vm out"), th_dtype(t), slot
     d.workspace = workspace.data_ptr()
     abi.check(lib.th_epilogue_vm(C.byref(d), _stream(ref)), "th_epilogue_vm", kernel)
+
+
+# ------------------------------------------------------------------- SSD
+def ssd_workspace_bytes(batch: int, seq: int, heads: int, head_dim: int, state_dim: int, chunk: int) -> int:
+    return int(abi.load().th_ssd_workspace_bytes(batch, seq, heads, head_dim, state_dim, chunk))
+
+
+def ssd_chunked(*, x, b, c, dt, out, workspace, batch, seq, heads, head_dim, state_dim, ngroups, chunk, A=None, D=None,
+                cum=None, dt_stride=1, dskip=None, gate=None, out32=None, kernel: str | None = None) -> None:
+    lib = _lib(x)
+    d = abi.SsdDesc()
+    d.batch, d.seq, d.heads, d.head_dim, d.state_dim, d.ngroups, d.chunk = batch, seq, heads, head_dim, state_dim, ngroups, chunk
+    d.dtype = th_dtype(x)
+    for t in (b, c, dt) + ((cum,) if cum is not None else ()) + ((dskip,) if dskip is not None else ()):
+        if t.dtype != x.dtype:
+            raise abi.HipBackendError("th_ssd_chunked", abi.TH_ERR_INVALID, "scan operands must share one dtype", kernel)
+    d.x, d.ld_x = x.data_ptr(), _row_major(x, "ssd x")
+    d.b, d.ld_b = b.data_ptr(), _row_major(b, "ssd b")
+    d.c, d.ld_c = c.data_ptr(), _row_major(c, "ssd c")
+    d.dt, d.ld_dt, d.dt_stride = dt.data_ptr(), _row_major(dt, "ssd dt"), dt_stride
+    if cum is not None:
+        d.cum, d.ld_cum = cum.data_ptr(), _row_major(cum, "ssd cum")
+    if A is not None:
+        d.A = A.data_ptr()
+    if D is not None:
+        d.D = D.data_ptr()
+    if dskip is not None:
+        d.dskip, d.ld_dskip = dskip.data_ptr(), _row_major(dskip, "ssd dskip")
+    if gate is not None:
+        d.gate, d.ld_gate, d.gate_dtype = gate.data_ptr(), _row_major(gate, "ssd gate"), th_dtype(gate)
+    d.y, d.ld_y, d.y_dtype = out.data_ptr(), _row_major(out, "ssd y"), th_dtype(out)
+    if out32 is not None:
+        d.y32, d.ld_y32 = out32.data_ptr(), _row_major(out32, "ssd y32")
+    d.workspace, d.workspace_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
+    abi.check(lib.th_ssd_chunked(C.byref(d), _stream(x)), "th_ssd_chunked", kernel)
+
+
+def conv1d_causal(x, w, out, *, batch: int, seq: int, activation: str | None, out32=None, kernel: str | None = None) -> None:
+    lib = _lib(x)
+    if w.dtype != torch.float32 or not w.is_contiguous():
+        raise abi.HipBackendError("th_conv1d_causal", abi.TH_ERR_INVALID, "weights must be contiguous fp32 [C, K]", kernel)
+    d = abi.ConvDesc()
+    d.batch, d.seq, d.width, d.kernel = batch, seq, w.shape[0], w.shape[1]
+    d.activation = 1 if activation == "silu" else 0
+    d.x_dtype, d.y_dtype = th_dtype(x), th_dtype(out)
+    d.x, d.ld_x = x.data_ptr(), _row_major(x, "conv x")
+    d.w = w.data_ptr()
+    d.y, d.ld_y = out.data_ptr(), _row_major(out, "conv y")
+    if out32 is not None:
+        d.y32, d.ld_y32 = out32.data_ptr(), _row_major(out32, "conv y32")
+    abi.check(lib.th_conv1d_causal(C.byref(d), _stream(x)), "th_conv1d_causal", kernel)

@@ -224,10 +224,11 @@ class DeviceProgram:
                 gvec = row.reshape(-1).to(self.device).contiguous()
                 xbuf = self.buffers[lhs_tensor]
                 out = self.buffers[spec.outputs[0].tensor]
+                out32 = self.shadow.get(spec.outputs[0].tensor)
                 inv_k, eps = rs
 
                 def run() -> None:
-                    ops.rmsnorm(xbuf, gvec, eps, out, inv_k=inv_k, kernel=spec.name)
+                    ops.rmsnorm(xbuf, gvec, eps, out, inv_k=inv_k, kernel=spec.name, out32=out32)
 
                 return Launch(spec.name, "rmsnorm", run, "th_rmsnorm", {"inv_k": inv_k, "eps": eps})
         return None

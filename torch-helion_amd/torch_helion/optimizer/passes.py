@@ -549,16 +549,29 @@ def match_conv(g: OpGraph) -> int:
 
 
 def _silu_of(g: OpGraph, name: str) -> OpNode | None:
-    """The node computing silu(name) if that is ``name``'s only consumer chain."""
+    """The node computing silu(name) if that is ``name``'s only consumer chain,
+    as one ``silu`` op or decomposed ``x * sigmoid(x)``, optionally wrapped in
+    the up/down casts a low-precision decomposition adds."""
     users = g.users(name)
+    cast_in = None
+    if len(users) == 1 and users[0].op == "cast":
+        cast_in = users[0]
+        name, users = cast_in.name, g.users(cast_in.name)
+    act = None
     if len(users) == 1 and users[0].op == "silu":
-        return users[0]
-    sig = [u for u in users if u.op == "sigmoid"]
-    mul = [u for u in users if u.op == "mul" and "scalar" not in u.attrs]
-    if len(users) == 2 and len(sig) == 1 and len(mul) == 1 and sorted(mul[0].inputs) == sorted([name, sig[0].name]):
-        if g.users(sig[0].name) == [mul[0]]:
-            return mul[0]
-    return None
+        act = users[0]
+    else:
+        sig = [u for u in users if u.op == "sigmoid"]
+        mul = [u for u in users if u.op == "mul" and "scalar" not in u.attrs]
+        if (len(users) == 2 and len(sig) == 1 and len(mul) == 1 and sorted(mul[0].inputs) == sorted([name, sig[0].name])
+                and g.users(sig[0].name) == [mul[0]]):
+            act = mul[0]
+    if act is None:
+        return None
+    after = g.users(act.name)
+    if cast_in is not None and len(after) == 1 and after[0].op == "cast":
+        return after[0]
+    return act
 
 
 def _flat(p: torch.Tensor, shape: tuple[int, ...]) -> torch.Tensor:
@@ -942,6 +955,7 @@ def canonicalize(graph: OpGraph, verify_inputs: list[torch.Tensor] | None = None
     with the raw graph's (max relative error <= ``tolerance``)."""
     g = graph.copy()
     g.metadata["output_shapes_raw"] = {o: list(g[o].type.shape) for o in g.outputs}
+    raw_shapes = [list(g[o].type.shape) for o in g.outputs]
     ref = graph_outputs(g, verify_inputs) if verify_inputs is not None else None
     log: list[dict] = []
     for name, fn in PASSES:
@@ -954,4 +968,7 @@ def canonicalize(graph: OpGraph, verify_inputs: list[torch.Tensor] | None = None
             if err > tolerance:
                 raise PassError(f"pass {name} changed the numerics (max rel err {err:.3e})")
         log.append(entry)
+    # passes may rename an output node (an identity reshape folded into its base):
+    # record the caller-visible shape under the final names, by position
+    g.metadata["output_shapes"] = {o: shp for o, shp in zip(g.outputs, raw_shapes)}
     return g, log
