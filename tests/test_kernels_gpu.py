@@ -61,6 +61,32 @@ def test_gemm_bf16_plain(gpu, M, N, K):
     assert _maxabs(o16, ref) < BF16_TOL
 
 
+@pytest.mark.parametrize("M,N,K,n_acc", [(8200, 4096, 1024, 1), (2000, 768, 4096, 2), (777, 1024, 2048, 4)])
+def test_gemm_bf16_deep_k_ragged_m(gpu, M, N, K, n_acc):
+    """Many 64-wide K tiles, M not a multiple of the row tile (256-row tiles at 8200 x 4096), RMS fold on."""
+    from torch_helion.hip import abi, ops
+
+    announce(f"gemm bf16 deep-K M={M} N={N} K={K} n_acc={n_acc}")
+    g = torch.Generator().manual_seed(M + K)
+    x = torch.randn(M, K, generator=g).bfloat16()
+    ws = [(torch.randn(K, N, generator=g) * 0.02).bfloat16() for _ in range(n_acc)]
+    xf = x.float()
+    r = ((xf * xf).sum(-1, keepdim=True) / K + 1e-5).pow(-0.5)
+    xd = x.to(gpu)
+    packed = ops.pack_rhs([w.to(gpu) for w in ws], torch.bfloat16)
+    outs = [torch.empty(M, N, dtype=torch.float32, device=gpu) for _ in range(n_acc)]
+    ss = torch.empty(M, dtype=torch.float32, device=gpu)
+    ops.gemm(ops.GemmCall(M, N, K, n_acc, xd, packed, [ops.EpiSpec(abi.EPI_ACC, o, a=i) for i, o in enumerate(outs)],
+                          sumsq=True, rscale_mask=(1 << n_acc) - 2, inv_k=1.0 / K, eps=1e-5, sumsq_out=ss))
+    torch.cuda.synchronize()
+    for i, (o, w) in enumerate(zip(outs, ws)):
+        ref = xf @ w.float()
+        if i > 0:
+            ref = ref * r
+        assert _rel(o, ref) < 1e-5, i
+    assert _rel(ss, (xf * xf).sum(-1)) < 1e-5
+
+
 def test_gemm_bf16_rms_swiglu(gpu):
     from torch_helion.hip import abi, ops
 
@@ -120,6 +146,39 @@ def test_gemm_qkv_rope(gpu, dtype):
     else:
         for o, ref in ((oq, q_ref), (ok, k_ref), (ov, v), (ok2, k_ref)):
             assert _maxabs(o, ref) < BF16_TOL
+
+
+@pytest.mark.parametrize("hd,n_acc", [(128, 1), (64, 2)])
+def test_gemm_rope_whole_heads_per_wave(gpu, hd, n_acc):
+    """Fused RoPE where every wave's column half holds whole heads (the q-projection shape class),
+    with the RMS fold, a table period shorter than M, and bf16 + fp32 outputs of the same op."""
+    from torch_helion.hip import abi, ops
+
+    announce(f"gemm bf16 rope hd={hd} n_acc={n_acc}")
+    B, S, H, K, eps = 4, 250, 8, 512, 1e-5
+    M, N = B * S, H * hd
+    g = torch.Generator().manual_seed(hd + n_acc)
+    x = torch.randn(M, K, generator=g).bfloat16()
+    ws = [(torch.randn(K, N, generator=g) * 0.05).bfloat16() for _ in range(n_acc)]
+    cos, sin = _rope_tables(S, hd, theta=500000.0)
+    xf = x.float()
+    r = ((xf * xf).sum(-1, keepdim=True) / K + eps).pow(-0.5)
+    accs = [(xf @ w.float()) * r for w in ws]
+    cf, sf = cos.repeat(B, H), sin.repeat(B, H)
+    refs = [a * cf + _rot_heads(a, hd) * sf for a in accs]
+    xd = x.to(gpu)
+    packed = ops.pack_rhs([w.to(gpu) for w in ws], torch.bfloat16)
+    o16 = [torch.empty(M, N, dtype=torch.bfloat16, device=gpu) for _ in range(n_acc)]
+    o32 = [torch.empty(M, N, dtype=torch.float32, device=gpu) for _ in range(n_acc)]
+    outs = [ops.EpiSpec(abi.EPI_ROPE, o, a=i) for i, o in enumerate(o16)] + \
+           [ops.EpiSpec(abi.EPI_ROPE, o, a=i) for i, o in enumerate(o32)]
+    ops.gemm(ops.GemmCall(M, N, K, n_acc, xd, packed, outs, sumsq=True, rscale_mask=(1 << n_acc) - 1,
+                          inv_k=1.0 / K, eps=eps, rope_cos=cos.to(gpu).contiguous(), rope_sin=sin.to(gpu).contiguous(),
+                          rope_head_dim=hd, rope_period=S))
+    torch.cuda.synchronize()
+    for i, ref in enumerate(refs):
+        assert _rel(o32[i], ref) < 1e-5, i
+        assert _maxabs(o16[i], ref) < BF16_TOL, i
 
 
 def test_gemm_extra_ops(gpu):

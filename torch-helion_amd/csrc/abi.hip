@@ -13,6 +13,7 @@ namespace th {
 static thread_local std::string g_last_error;
 static std::mutex g_init_mutex;
 static bool g_ready[64];
+static int g_cus[64];
 
 void set_error(const char* fmt, ...) {
   char buf[1024];
@@ -27,6 +28,12 @@ bool device_ready() {
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return false;
   return g_ready[dev];
+}
+
+int device_cus() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  return g_cus[dev];
 }
 
 }  // namespace th
@@ -49,6 +56,7 @@ extern "C" int th_init(int device) {
                   prop.gcnArchName);
     return TH_ERR_UNSUPPORTED;
   }
+  th::g_cus[device] = prop.multiProcessorCount;
   th::g_ready[device] = true;
   th::g_last_error.clear();
   return TH_OK;

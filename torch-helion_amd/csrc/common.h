@@ -41,10 +41,14 @@ __device__ __forceinline__ void store_elem(void* p, int64_t i, int dtype, float 
 }
 
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + __expf(-x)); }
+// log(1 + exp(x)) without a large-x guard: the OpIR softplus rewrite drops
+// torch's threshold, so this is the value the program defines.
+__device__ __forceinline__ float softplusf_(float x) { return __logf(1.f + __expf(x)); }
 
 // --------------------------------------------------------------- host side
 void set_error(const char* fmt, ...);
 bool device_ready();  // th_init was called for the current device
+int device_cus();     // compute units of the current device (0 before th_init)
 
 #define TH_CHECK_ARG(cond, ...)            \
   do {                                     \

@@ -20,6 +20,8 @@
 //          RoPE partner column, other accumulators) from LDS and writes 4
 //          consecutive columns per thread, so global stores are coalesced.
 #include <algorithm>
+#include <cstdlib>
+#include <type_traits>
 
 #include "common.h"
 
@@ -59,9 +61,8 @@ struct GemmK {
 // 8 XCDs; remap so each XCD owns a contiguous range of logical tiles, then walk
 // that range in groups of 8 tile-rows so neighbouring blocks on one XCD share
 // lhs rows and rhs columns in that XCD's L2.
-__device__ __forceinline__ void map_tile(int tiles_m, int tiles_n, int& tm, int& tn) {
+__device__ __forceinline__ void map_tile_id(int pid, int tiles_m, int tiles_n, int& tm, int& tn) {
   const int nb = tiles_m * tiles_n;
-  int pid = blockIdx.x;
   if ((nb & 7) == 0) pid = (pid & 7) * (nb >> 3) + (pid >> 3);
   const int G = 8;
   const int group = pid / (G * tiles_n);
@@ -70,6 +71,10 @@ __device__ __forceinline__ void map_tile(int tiles_m, int tiles_n, int& tm, int&
   const int in_group = pid - group * G * tiles_n;
   tm = first + in_group % gm;
   tn = in_group / gm;
+}
+
+__device__ __forceinline__ void map_tile(int tiles_m, int tiles_n, int& tm, int& tn) {
+  map_tile_id(blockIdx.x, tiles_m, tiles_n, tm, tn);
 }
 
 __device__ __forceinline__ float4 load4(const void* p, int64_t off, int dtype, bool vec, int valid) {
@@ -188,10 +193,7 @@ __device__ void epilogue_slab(const GemmK& p, const float* slab, int srow, int r
           } else {
             v.x = a.x + x.x; v.y = a.y + x.y; v.z = a.z + x.z; v.w = a.w + x.w;
             if (op == TH_EPI_SOFTPLUS_ADD) {
-              v.x = __logf(1.f + __expf(v.x));
-              v.y = __logf(1.f + __expf(v.y));
-              v.z = __logf(1.f + __expf(v.z));
-              v.w = __logf(1.f + __expf(v.w));
+              v.x = softplusf_(v.x); v.y = softplusf_(v.y); v.z = softplusf_(v.z); v.w = softplusf_(v.w);
             }
           }
           break;
@@ -216,6 +218,16 @@ __device__ __forceinline__ float sumsq8_bf16(uint4 w) {
     s += lo * lo + hi * hi;
   }
   return s;
+}
+
+// Sum of squares of an MFMA operand fragment (8 bf16) with v_dot2_f32_bf16:
+// each bf16 product is exact in fp32, accumulation is fp32.
+__device__ __forceinline__ float sumsq8_dot(bf16x8_t v, float acc) {
+  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(v, v, 0, 1), __builtin_shufflevector(v, v, 0, 1), acc, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(v, v, 2, 3), __builtin_shufflevector(v, v, 2, 3), acc, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(v, v, 4, 5), __builtin_shufflevector(v, v, 4, 5), acc, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(v, v, 6, 7), __builtin_shufflevector(v, v, 6, 7), acc, false);
+  return acc;
 }
 
 // --------------------------------------------------------------- bf16 MFMA
@@ -347,6 +359,548 @@ __global__ void __launch_bounds__(256, 1) gemm_bf16_kernel(GemmK p) {
     epilogue_slab(p, slab, SROW, WM, rs + s * WM, m0 + s * WM, tni, tid);
     __syncthreads();
   }
+}
+
+// ------------------------------------------------- bf16 MFMA, direct-to-LDS
+// Same tiling and epilogue as gemm_bf16_kernel, with the operand tiles
+// streamed from HBM straight into LDS by buffer_load_dwordx4 ... lds (gfx950):
+// no staging VGPRs and no ds_write. Requires K % 64 == 0.
+//
+// LDS layout: row R of a tile holds its 8 16-byte K chunks with chunk c in
+// slot c ^ g(R), g(R) = (R & 7) ^ ((R >> 3) & 1). An MFMA fragment read (32
+// consecutive rows, one chunk) then touches 16 distinct bank quads in every
+// group of 16 lanes (64 banks x 4 bytes) and 8 distinct ones in every group of
+// 8 lanes (32 banks): no bank conflicts under either service pattern.
+// LDS fill: the wave's i-th load of a tile writes 1 KB = LDS rows
+// 32*i + 8*wave .. +8 (128 bytes each); lane l lands in row +l/8, slot l%8, so
+// it fetches global chunk (l%8) ^ g(row) = (l%8) ^ (l/8) ^ (wave&1). Out-of-range
+// rows of A read as zero (the buffer descriptor ends at the block's last valid
+// row).
+//
+// Pipeline (2 stages): the loads of tile kt+1 are in flight during tile kt.
+// Within a tile the fragments of step ks+1 are read from LDS while the MFMAs of
+// step ks run; the barrier sits in the middle of the last step, after which the
+// first fragments of tile kt+1 are read and the loads of tile kt+2 issued into
+// the stage everyone has just finished reading.
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  // word 3 = 0x00020000: raw 32-bit data format, the gfx9 default for untyped buffer access
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  // s_waitcnt fields (gfx9): vmcnt[3:0], expcnt[6:4], lgkmcnt[11:8], vmcnt_hi[15:14]
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+template <int BM, int BNC, bool SUMSQ>
+__global__ void __launch_bounds__(256, 1) gemm_bf16_dl_kernel(GemmK p) {
+#if defined(__HIP_DEVICE_COMPILE__)  // the buffer-resource type exists only in the device pass
+  constexpr int WM = BM / 2, WN = BNC / 2;
+  constexpr int TM = WM / 32, TN = WN / 32;
+  constexpr int LA = BM / 32, LB = BNC / 32;  // 1 KB loads per wave per tile
+  constexpr int STAGE = (BM + BNC) * 128;
+  constexpr int SROW = BNC + 8;
+  constexpr int EPI_BYTES = WM * SROW * 4;
+  constexpr int MAIN_BYTES = 2 * STAGE;
+  constexpr int BODY = MAIN_BYTES > EPI_BYTES ? MAIN_BYTES : EPI_BYTES;
+  constexpr int NMF = TM * TN;
+  __shared__ __attribute__((aligned(16))) char smem[BODY + BM * 4];
+  float* rs = (float*)(smem + BODY);
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  int tmi, tni;
+  map_tile(p.tiles_m, p.tiles_n, tmi, tni);
+  const int64_t m0 = (int64_t)tmi * BM;
+  const int64_t arows = min((int64_t)BM, p.M - m0);
+  const __amdgpu_buffer_rsrc_t rsa = make_rsrc((const uint16_t*)p.A + m0 * p.lda, (uint32_t)(arows * p.lda * 2));
+  const __amdgpu_buffer_rsrc_t rsb =
+      make_rsrc((const uint16_t*)p.B + (int64_t)tni * BNC * p.ldb, (uint32_t)(BNC * p.ldb * 2));
+  // Per-lane byte offsets of each load's row (VGPR offsets, so the descriptor's
+  // range check sees the row); the K position goes in the scalar offset.
+  const int lrow = lane >> 3;
+  const uint32_t chunk = (uint32_t)(((lane & 7) ^ lrow ^ (wave & 1)) << 4);
+  uint32_t voa[LA], vob[LB];
+#pragma unroll
+  for (int i = 0; i < LA; ++i) voa[i] = (uint32_t)((32 * i + 8 * wave + lrow) * p.lda * 2) + chunk;
+#pragma unroll
+  for (int i = 0; i < LB; ++i) vob[i] = (uint32_t)((32 * i + 8 * wave + lrow) * p.ldb * 2) + chunk;
+  const int nk = (int)(p.K / 64);
+
+  auto issue_tile = [&](int kt, int st) {
+    char* sa = smem + st * STAGE;
+    char* sb = sa + BM * 128;
+    const uint32_t kofs = (uint32_t)kt * 128;
+#pragma unroll
+    for (int i = 0; i < LA; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, (lds_ptr_t)(sa + (4 * i + wave) * 1024), 16, voa[i], kofs, 0, 0);
+#pragma unroll
+    for (int i = 0; i < LB; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsb, (lds_ptr_t)(sb + (4 * i + wave) * 1024), 16, vob[i], kofs, 0, 0);
+  };
+
+  bf16x8_t fa[2][TM], fb[2][TN];
+  f32x16_t acc[TM][TN];
+  float ss[TM];
+#pragma unroll
+  for (int t = 0; t < TM; ++t) {
+    ss[t] = 0.f;
+#pragma unroll
+    for (int u = 0; u < TN; ++u)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[t][u][r] = 0.f;
+  }
+
+  auto read_frags = [&](int st, int ks, int slot) {
+    const char* sa = smem + st * STAGE;
+    const char* sb = sa + BM * 128;
+    const int c = ((ks * 2 + (lane >> 5)) ^ (lane & 7) ^ ((lane >> 3) & 1)) << 4;
+#pragma unroll
+    for (int t = 0; t < TM; ++t) fa[slot][t] = *(const bf16x8_t*)(sa + (wm * WM + t * 32 + (lane & 31)) * 128 + c);
+#pragma unroll
+    for (int u = 0; u < TN; ++u) fb[slot][u] = *(const bf16x8_t*)(sb + (wn * WN + u * 32 + (lane & 31)) * 128 + c);
+  };
+  auto mfmas = [&](int slot, int lo, int hi) {
+#pragma unroll
+    for (int i = 0; i < NMF; ++i) {
+      if (i < lo || i >= hi) continue;
+      const int t = i / TN, u = i % TN;
+      acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[slot][t], fb[slot][u], acc[t][u], 0, 0, 0);
+    }
+  };
+  // The two waves that share A rows (wn = 0, 1) split the row sums of squares:
+  // wave wn accumulates the 32-row groups t with t % 2 == wn.
+  auto sumsq_frags = [&](int slot) {
+    if constexpr (SUMSQ) {
+#pragma unroll
+      for (int t = 0; t < TM; ++t)
+        if ((t & 1) == wn) ss[t] = sumsq8_dot(fa[slot][t], ss[t]);
+    }
+  };
+
+  issue_tile(0, 0);
+  if (nk > 1) {
+    issue_tile(1, 1);
+    wait_vmcnt<LA + LB>();
+  } else {
+    wait_vmcnt<0>();
+  }
+  __syncthreads();
+  read_frags(0, 0, 0);
+
+  // sched_barrier(0) fences keep the compiler from sinking a fragment read
+  // next to the MFMA that consumes it: every read is issued one full step
+  // (NMF MFMAs) ahead of its use.
+  for (int kt = 0; kt < nk; ++kt) {
+    const int st = kt & 1;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const int slot = ks & 1;
+      if (ks < 3) {
+        read_frags(st, ks + 1, slot ^ 1);
+        __builtin_amdgcn_sched_barrier(0);
+        mfmas(slot, 0, NMF);
+        sumsq_frags(slot);
+        __builtin_amdgcn_sched_barrier(0);
+      } else {
+        mfmas(slot, 0, NMF / 2);
+        __builtin_amdgcn_sched_barrier(0);
+        if (kt + 1 < nk) {
+          wait_vmcnt<0>();
+          __syncthreads();
+          read_frags(st ^ 1, 0, 0);
+          if (kt + 2 < nk) issue_tile(kt + 2, st);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        mfmas(slot, NMF / 2, NMF);
+        sumsq_frags(slot);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  }
+
+  if constexpr (SUMSQ) {
+#pragma unroll
+    for (int t = 0; t < TM; ++t) {
+      const float v = ss[t] + __shfl_xor(ss[t], 32);
+      if ((t & 1) == wn && lane < 32) {
+        const int r = wm * WM + t * 32 + lane;
+        rs[r] = rsqrtf(v * p.inv_k + p.eps);
+        const int64_t gr = m0 + r;
+        if (p.sumsq_out && tni == 0 && gr < p.M) p.sumsq_out[gr] = v;
+      }
+    }
+  }
+  __syncthreads();
+
+  float* slab = (float*)smem;
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    if (wm == s) {
+#pragma unroll
+      for (int t = 0; t < TM; ++t)
+#pragma unroll
+        for (int u = 0; u < TN; ++u)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int row = t * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            const int col = wn * WN + u * 32 + (lane & 31);
+            slab[row * SROW + col] = acc[t][u][r];
+          }
+    }
+    __syncthreads();
+    epilogue_slab(p, slab, SROW, WM, rs + s * WM, m0 + s * WM, tni, tid);
+    __syncthreads();
+  }
+#endif
+}
+
+// ------------------------- bf16 MFMA, persistent blocks + per-wave epilogue
+// One block per CU walks the output tiles L = blockIdx.x, +gridDim.x, ... in
+// map_tile order (each XCD keeps its contiguous tile range). Per tile the main
+// loop is the direct-to-LDS loop above, except that wave (wm, wn) computes
+// rows wm*WM .. of the wn-th column half of EVERY accumulator: subtile u holds
+// accumulator u % n_acc, columns wn*bn/2 + (u / n_acc)*32 .. +32. An output op
+// that combines accumulators (SWIGLU, ROPE_PAIR) or rotates within a head
+// (ROPE with head_dim | bn/2) then finds every operand in its own wave, so the
+// epilogue needs no block barrier: each wave transposes 16 rows at a time
+// through a private slice of LDS stage 1 and writes 4 consecutive columns per
+// lane. Before the epilogue starts, the next tile's first K tile is already
+// streaming into stage 0, so its latency hides behind the epilogue.
+template <int BM, int BNC, bool SUMSQ>
+__global__ void __launch_bounds__(256, 1) gemm_bf16_pk_kernel(GemmK p) {
+#if defined(__HIP_DEVICE_COMPILE__)  // the buffer-resource type exists only in the device pass
+  constexpr int WM = BM / 2, WN = BNC / 2;
+  constexpr int TM = WM / 32, TN = WN / 32;
+  constexpr int LA = BM / 32, LB = BNC / 32;
+  constexpr int STAGE = (BM + BNC) * 128;
+  constexpr int NMF = TM * TN;
+  constexpr int WS = WN + 8;                 // epilogue slice row stride (floats)
+  constexpr int SLICE = 16 * WS * 4;         // bytes per wave: 16 rows
+  static_assert(4 * SLICE <= STAGE, "epilogue slices must fit in one stage");
+  __shared__ __attribute__((aligned(16))) char smem[2 * STAGE + BM * 4];
+  float* rsx = (float*)(smem + 2 * STAGE);  // row scales of the current tile
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int n_acc = p.n_acc, bn = p.bn, hbn = bn >> 1;
+  const int tiles = p.tiles_m * p.tiles_n;
+  const int nk = (int)(p.K / 64);
+
+  // subtile u: LDS row of its B fragment and its column in the epilogue slice
+  int brow[TN], lcol[TN];
+#pragma unroll
+  for (int u = 0; u < TN; ++u) {
+    const int a = u % n_acc, c32 = u / n_acc;
+    brow[u] = a * bn + wn * hbn + c32 * 32 + (lane & 31);
+    lcol[u] = a * hbn + c32 * 32;
+  }
+
+  const int lrow = lane >> 3;
+  const uint32_t chunk = (uint32_t)(((lane & 7) ^ lrow ^ (wave & 1)) << 4);
+  uint32_t voa[LA], vob[LB];
+#pragma unroll
+  for (int i = 0; i < LA; ++i) voa[i] = (uint32_t)((32 * i + 8 * wave + lrow) * p.lda * 2) + chunk;
+#pragma unroll
+  for (int i = 0; i < LB; ++i) vob[i] = (uint32_t)((32 * i + 8 * wave + lrow) * p.ldb * 2) + chunk;
+
+  auto tile_rsrc = [&](int L, int& tm, int& tn, __amdgpu_buffer_rsrc_t& ra, __amdgpu_buffer_rsrc_t& rb) {
+    map_tile_id(L, p.tiles_m, p.tiles_n, tm, tn);
+    const int64_t m0 = (int64_t)tm * BM;
+    const int64_t arows = min((int64_t)BM, p.M - m0);
+    ra = make_rsrc((const uint16_t*)p.A + m0 * p.lda, (uint32_t)(arows * p.lda * 2));
+    rb = make_rsrc((const uint16_t*)p.B + (int64_t)tn * BNC * p.ldb, (uint32_t)(BNC * p.ldb * 2));
+  };
+  auto issue_tile = [&](const __amdgpu_buffer_rsrc_t& ra, const __amdgpu_buffer_rsrc_t& rb, int kt, int st) {
+    char* sa = smem + st * STAGE;
+    char* sb = sa + BM * 128;
+    const uint32_t kofs = (uint32_t)kt * 128;
+#pragma unroll
+    for (int i = 0; i < LA; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr_t)(sa + (4 * i + wave) * 1024), 16, voa[i], kofs, 0, 0);
+#pragma unroll
+    for (int i = 0; i < LB; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_ptr_t)(sb + (4 * i + wave) * 1024), 16, vob[i], kofs, 0, 0);
+  };
+
+  bf16x8_t fa[2][TM], fb[2][TN];
+  f32x16_t acc[TM][TN];
+  float ss[TM];
+  auto read_frags = [&](int st, int ks, int slot) {
+    const char* sa = smem + st * STAGE;
+    const char* sb = sa + BM * 128;
+    const int c = ((ks * 2 + (lane >> 5)) ^ (lane & 7) ^ ((lane >> 3) & 1)) << 4;
+#pragma unroll
+    for (int t = 0; t < TM; ++t) fa[slot][t] = *(const bf16x8_t*)(sa + (wm * WM + t * 32 + (lane & 31)) * 128 + c);
+#pragma unroll
+    for (int u = 0; u < TN; ++u) fb[slot][u] = *(const bf16x8_t*)(sb + brow[u] * 128 + c);
+  };
+  auto mfmas = [&](int slot, int lo, int hi) {
+#pragma unroll
+    for (int i = 0; i < NMF; ++i) {
+      if (i < lo || i >= hi) continue;
+      const int t = i / TN, u = i % TN;
+      acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[slot][t], fb[slot][u], acc[t][u], 0, 0, 0);
+    }
+  };
+  // wave wn accumulates the row sums of squares of the 32-row groups t % 2 == wn
+  auto sumsq_frags = [&](int slot) {
+    if constexpr (SUMSQ) {
+#pragma unroll
+      for (int t = 0; t < TM; ++t)
+        if ((t & 1) == wn) ss[t] = sumsq8_dot(fa[slot][t], ss[t]);
+    }
+  };
+
+  int L = blockIdx.x;
+  if (L >= tiles) return;
+  int tmi, tni;
+  __amdgpu_buffer_rsrc_t rsa, rsb;
+  tile_rsrc(L, tmi, tni, rsa, rsb);
+  issue_tile(rsa, rsb, 0, 0);
+  if (nk > 1) issue_tile(rsa, rsb, 1, 1);
+
+  char* slice = smem + STAGE + wave * SLICE;
+  float* wsl = (float*)slice;
+
+  for (;;) {
+    // K tile 0 of tile L is in flight into stage 0 (and K tile 1 into stage 1)
+    if (nk > 1)
+      wait_vmcnt<LA + LB>();
+    else
+      wait_vmcnt<0>();
+    __syncthreads();
+    read_frags(0, 0, 0);
+#pragma unroll
+    for (int t = 0; t < TM; ++t) {
+      ss[t] = 0.f;
+#pragma unroll
+      for (int u = 0; u < TN; ++u)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[t][u][r] = 0.f;
+    }
+
+    for (int kt = 0; kt < nk; ++kt) {
+      const int st = kt & 1;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const int slot = ks & 1;
+        if (ks < 3) {
+          read_frags(st, ks + 1, slot ^ 1);
+          __builtin_amdgcn_sched_barrier(0);
+          mfmas(slot, 0, NMF);
+          sumsq_frags(slot);
+          __builtin_amdgcn_sched_barrier(0);
+        } else {
+          mfmas(slot, 0, NMF / 2);
+          __builtin_amdgcn_sched_barrier(0);
+          if (kt + 1 < nk) {
+            wait_vmcnt<0>();
+            __syncthreads();
+            read_frags(st ^ 1, 0, 0);
+            if (kt + 2 < nk) issue_tile(rsa, rsb, kt + 2, st);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+          mfmas(slot, NMF / 2, NMF);
+          sumsq_frags(slot);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+    }
+
+    if constexpr (SUMSQ) {
+#pragma unroll
+      for (int t = 0; t < TM; ++t) {
+        const float v = ss[t] + __shfl_xor(ss[t], 32);
+        if ((t & 1) == wn && lane < 32) {
+          const int r = wm * WM + t * 32 + lane;
+          rsx[r] = rsqrtf(v * p.inv_k + p.eps);
+          const int64_t gr = (int64_t)tmi * BM + r;
+          if (p.sumsq_out && tni == 0 && gr < p.M) p.sumsq_out[gr] = v;
+        }
+      }
+    }
+
+    // Every wave is done with both stages; start the next tile's first K tile.
+    __syncthreads();
+    const int Ln = L + (int)gridDim.x;
+    const bool more = Ln < tiles;
+    int tmn = 0, tnn = 0;
+    __amdgpu_buffer_rsrc_t rsan = rsa, rsbn = rsb;
+    if (more) {
+      tile_rsrc(Ln, tmn, tnn, rsan, rsbn);
+      issue_tile(rsan, rsbn, 0, 0);
+    }
+
+    // ---- epilogue of tile (tmi, tni), wave-private
+    const int64_t row_w = (int64_t)tmi * BM + wm * WM;  // first row of this wave
+    const int64_t col_w = (int64_t)tni * bn + wn * hbn;  // first column of this wave (every accumulator)
+    const int qlog = __builtin_ctz((unsigned)(hbn >> 2));  // quads per row = hbn / 4
+    // Rows 16*h .. +16 of the 32-row group t go through the slice. The copy out
+    // of the accumulators is unrolled per (t, h) so every register index is a
+    // constant; the read-back below is an ordinary loop.
+    auto write_slice = [&](const f32x16_t(&at)[TN], auto hc) {
+      constexpr int H = decltype(hc)::value;
+#pragma unroll
+      for (int u = 0; u < TN; ++u)
+#pragma unroll
+        for (int rr = 0; rr < 8; ++rr) {
+          const int row16 = 8 * (rr >> 2) + 4 * (lane >> 5) + (rr & 3);
+          wsl[row16 * WS + lcol[u] + (lane & 31)] = at[u][H * 8 + rr];
+        }
+    };
+    using H0 = std::integral_constant<int, 0>;
+    using H1 = std::integral_constant<int, 1>;
+    for (int t = 0; t < TM; ++t) {
+      for (int h = 0; h < 2; ++h) {
+        switch (t * 2 + h) {
+          case 0: write_slice(acc[0], H0{}); break;
+          case 1: write_slice(acc[0], H1{}); break;
+          case 2: if constexpr (TM > 1) write_slice(acc[1 % TM], H0{}); break;
+          case 3: if constexpr (TM > 1) write_slice(acc[1 % TM], H1{}); break;
+          case 4: if constexpr (TM > 2) write_slice(acc[2 % TM], H0{}); break;
+          case 5: if constexpr (TM > 2) write_slice(acc[2 % TM], H1{}); break;
+          case 6: if constexpr (TM > 3) write_slice(acc[3 % TM], H0{}); break;
+          default: if constexpr (TM > 3) write_slice(acc[3 % TM], H1{}); break;
+        }
+        static_assert(TM <= 4, "write_slice cases cover four 32-row groups");
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+        const int64_t row0 = row_w + t * 32 + h * 16;
+        const float* rsrow = rsx + wm * WM + t * 32 + h * 16;
+        const int nu = 1 << (qlog - 2);  // units per lane: 16 rows x hbn/4 quads / 64 lanes (2, 4 or 8)
+        for (int o = 0; o < p.n_out; ++o) {
+          const EpiOutK& eo = p.out[o];
+          const int op = eo.op, ia = eo.a, ib = eo.b;
+          const bool scale_a = (p.rscale_mask >> ia) & 1u;
+          const bool scale_b = ib >= 0 && ((p.rscale_mask >> ib) & 1u);
+          // Global operand reads (extra operand, or the RoPE cos/sin rows) are
+          // issued four units at a time before their first use, so their
+          // latencies overlap.
+          const bool uses_e = op == TH_EPI_ADD || op == TH_EPI_SOFTPLUS_ADD || op == TH_EPI_MUL;
+          const bool uses_t = op == TH_EPI_ROPE || op == TH_EPI_ROPE_PAIR;
+          auto fetch = [&](int k, float4& x, float4& y) {
+            x = y = make_float4(0.f, 0.f, 0.f, 0.f);
+            const int un = lane + 64 * k;
+            const int r16 = un >> qlog;
+            const int cl = (un & ((1 << qlog) - 1)) << 2;
+            const int64_t gm = row0 + r16, gn = col_w + cl;
+            if (k >= nu || gm >= p.M || gn >= p.N) return;
+            if (uses_e) {
+              const int e = eo.e;
+              x = load4(p.extra[e], gm * p.ld_extra[e] + gn, p.extra_dtype[e], p.extra_vec[e] != 0,
+                        (int)min((int64_t)4, p.N - gn));
+            } else if (uses_t) {
+              const int64_t toff = (int64_t)((int)gm % p.period) * p.hd + (int)gn % p.hd;
+              x = *(const float4*)(p.rcos + toff);
+              y = *(const float4*)(p.rsin + toff);
+            }
+          };
+          auto unit = [&](int k, const float4& xk, const float4& yk) {
+            const int un = lane + 64 * k;
+            const int r16 = un >> qlog;
+            const int cl = (un & ((1 << qlog) - 1)) << 2;
+            const int64_t gm = row0 + r16, gn = col_w + cl;
+            if (k >= nu || gm >= p.M || gn >= p.N) return;
+            const int valid = (int)min((int64_t)4, p.N - gn);
+            const float rr = SUMSQ ? rsrow[r16] : 1.f;
+            const float* srow = wsl + r16 * WS;
+            float4 a = *(const float4*)(srow + ia * hbn + cl);
+            if (scale_a) { a.x *= rr; a.y *= rr; a.z *= rr; a.w *= rr; }
+            float4 v;
+            switch (op) {
+              case TH_EPI_ACC:
+                v = a;
+                break;
+              case TH_EPI_ROPE:
+              case TH_EPI_ROPE_PAIR: {
+                float4 rot;
+                const int within = (int)gn % p.hd;
+                if (op == TH_EPI_ROPE) {
+                  const int half = p.hd >> 1;
+                  const int pc = within < half ? cl + half : cl - half;
+                  const float sg = within < half ? -1.f : 1.f;
+                  rot = *(const float4*)(srow + ia * hbn + pc);
+                  const float s2 = scale_a ? sg * rr : sg;
+                  rot.x *= s2; rot.y *= s2; rot.z *= s2; rot.w *= s2;
+                } else {
+                  rot = *(const float4*)(srow + ib * hbn + cl);
+                  if (scale_b) { rot.x *= rr; rot.y *= rr; rot.z *= rr; rot.w *= rr; }
+                }
+                const float4 c = xk, s = yk;
+                v.x = a.x * c.x + rot.x * s.x;
+                v.y = a.y * c.y + rot.y * s.y;
+                v.z = a.z * c.z + rot.z * s.z;
+                v.w = a.w * c.w + rot.w * s.w;
+                break;
+              }
+              case TH_EPI_SILU:
+                v.x = a.x * sigmoidf_(a.x);
+                v.y = a.y * sigmoidf_(a.y);
+                v.z = a.z * sigmoidf_(a.z);
+                v.w = a.w * sigmoidf_(a.w);
+                break;
+              case TH_EPI_SWIGLU: {
+                float4 b = *(const float4*)(srow + ib * hbn + cl);
+                if (scale_b) { b.x *= rr; b.y *= rr; b.z *= rr; b.w *= rr; }
+                v.x = a.x * sigmoidf_(a.x) * b.x;
+                v.y = a.y * sigmoidf_(a.y) * b.y;
+                v.z = a.z * sigmoidf_(a.z) * b.z;
+                v.w = a.w * sigmoidf_(a.w) * b.w;
+                break;
+              }
+              default: {  // TH_EPI_ADD, TH_EPI_SOFTPLUS_ADD, TH_EPI_MUL
+                const float4 x = xk;
+                if (op == TH_EPI_MUL) {
+                  v.x = a.x * x.x; v.y = a.y * x.y; v.z = a.z * x.z; v.w = a.w * x.w;
+                } else {
+                  v.x = a.x + x.x; v.y = a.y + x.y; v.z = a.z + x.z; v.w = a.w + x.w;
+                  if (op == TH_EPI_SOFTPLUS_ADD) {
+                    v.x = softplusf_(v.x); v.y = softplusf_(v.y); v.z = softplusf_(v.z); v.w = softplusf_(v.w);
+                  }
+                }
+                break;
+              }
+            }
+            store4(eo.ptr, gm * eo.ld + gn, eo.dtype, eo.vec != 0, valid, v);
+          };
+          for (int k0 = 0; k0 < nu; k0 += 4) {
+            float4 x0, x1, x2, x3, y0, y1, y2, y3;
+            fetch(k0, x0, y0);
+            fetch(k0 + 1, x1, y1);
+            fetch(k0 + 2, x2, y2);
+            fetch(k0 + 3, x3, y3);
+            unit(k0, x0, y0);
+            unit(k0 + 1, x1, y1);
+            unit(k0 + 2, x2, y2);
+            unit(k0 + 3, x3, y3);
+          }
+        }
+        // the next 16 rows overwrite this slice
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      }
+    }
+
+    __syncthreads();  // every wave is done with its stage-1 slice
+    if (!more) break;
+    if (nk > 1) issue_tile(rsan, rsbn, 1, 1);
+    L = Ln;
+    tmi = tmn;
+    tni = tnn;
+    rsa = rsan;
+    rsb = rsbn;
+  }
+#endif
 }
 
 // --------------------------------------------------------------- fp32 MFMA
@@ -513,6 +1067,17 @@ static int64_t packed_kp(int64_t K, int in_dtype) {
 
 static bool aligned(const void* p, int bytes) { return ((uintptr_t)p % bytes) == 0; }
 
+// TH_GEMM_MAINLOOP=0|1|2 caps the bf16 main loop at register-staged (0),
+// direct-to-LDS (1) or persistent (2, the default); a shape still takes a
+// simpler loop when the faster one does not apply to it.
+static int forced_main_loop() {
+  static const int v = [] {
+    const char* e = getenv("TH_GEMM_MAINLOOP");
+    return (e && e[0] >= '0' && e[0] <= '2') ? e[0] - '0' : -1;
+  }();
+  return v;
+}
+
 }  // namespace th
 
 using namespace th;
@@ -567,6 +1132,36 @@ extern "C" int th_gemm_pack_rhs(const void* const* src, const int64_t* ld_src, i
 template <int BM, int BNC>
 static void launch_bf16(const GemmK& k, hipStream_t s) {
   hipLaunchKernelGGL((gemm_bf16_kernel<BM, BNC>), dim3(k.tiles_m * k.tiles_n), dim3(256), 0, s, k);
+}
+
+template <int BM, int BNC>
+static void launch_bf16_dl(const GemmK& k, hipStream_t s) {
+  if (k.sumsq)
+    hipLaunchKernelGGL((gemm_bf16_dl_kernel<BM, BNC, true>), dim3(k.tiles_m * k.tiles_n), dim3(256), 0, s, k);
+  else
+    hipLaunchKernelGGL((gemm_bf16_dl_kernel<BM, BNC, false>), dim3(k.tiles_m * k.tiles_n), dim3(256), 0, s, k);
+}
+
+template <int BM, int BNC>
+static void launch_bf16_pk(const GemmK& k, hipStream_t s) {
+  const int tiles = k.tiles_m * k.tiles_n;
+  const int cus = device_cus();
+  const int grid = cus > 0 && tiles > cus ? cus : tiles;
+  if (k.sumsq)
+    hipLaunchKernelGGL((gemm_bf16_pk_kernel<BM, BNC, true>), dim3(grid), dim3(256), 0, s, k);
+  else
+    hipLaunchKernelGGL((gemm_bf16_pk_kernel<BM, BNC, false>), dim3(grid), dim3(256), 0, s, k);
+}
+
+enum class MainLoop { staged, direct, persistent };
+
+template <int BM, int BNC>
+static void launch_bf16_any(const GemmK& k, MainLoop m, hipStream_t s) {
+  switch (m) {
+    case MainLoop::persistent: launch_bf16_pk<BM, BNC>(k, s); break;
+    case MainLoop::direct: launch_bf16_dl<BM, BNC>(k, s); break;
+    default: launch_bf16<BM, BNC>(k, s); break;
+  }
 }
 
 template <int BNC>
@@ -674,11 +1269,25 @@ extern "C" int th_gemm(const th_gemm_desc* d, void* stream) {
     const int64_t big_blocks = cdiv(d->M, 256) * k.tiles_n;
     const bool big = big_blocks >= 512;
     k.tiles_m = (int)cdiv(d->M, big ? 256 : 128);
+    // Direct-to-LDS main loop: whole 64-wide K tiles, and 32-bit buffer offsets
+    // (one block's rows of lhs and of the packed rhs under 2 GiB).
+    const bool direct = d->K % 64 == 0 && (int64_t)256 * d->ld_lhs * 2 < ((int64_t)1 << 31) &&
+                        (int64_t)bnc * k.ldb * 2 < ((int64_t)1 << 31);
+    // Persistent blocks with the per-wave epilogue: each wave holds half of
+    // every accumulator's columns (bn/2, a multiple of 32), so a fused RoPE
+    // head must fit in that half.
+    bool wave_epi = bn >= 64 && d->M < ((int64_t)1 << 31) && d->N < ((int64_t)1 << 31);
+    for (int o = 0; o < d->n_out; ++o)
+      if (d->out[o].op == TH_EPI_ROPE) wave_epi &= (bn / 2) % k.hd == 0;
+    MainLoop ml = MainLoop::staged;
+    const int force = forced_main_loop();
+    if (direct) ml = wave_epi ? MainLoop::persistent : MainLoop::direct;
+    if (force >= 0 && force < (int)ml) ml = (MainLoop)force;
     switch (bnc) {
-      case 64: big ? launch_bf16<256, 64>(k, s) : launch_bf16<128, 64>(k, s); break;
-      case 128: big ? launch_bf16<256, 128>(k, s) : launch_bf16<128, 128>(k, s); break;
-      case 192: big ? launch_bf16<256, 192>(k, s) : launch_bf16<128, 192>(k, s); break;
-      case 256: big ? launch_bf16<256, 256>(k, s) : launch_bf16<128, 256>(k, s); break;
+      case 64: big ? launch_bf16_any<256, 64>(k, ml, s) : launch_bf16_any<128, 64>(k, ml, s); break;
+      case 128: big ? launch_bf16_any<256, 128>(k, ml, s) : launch_bf16_any<128, 128>(k, ml, s); break;
+      case 192: big ? launch_bf16_any<256, 192>(k, ml, s) : launch_bf16_any<128, 192>(k, ml, s); break;
+      case 256: big ? launch_bf16_any<256, 256>(k, ml, s) : launch_bf16_any<128, 256>(k, ml, s); break;
       default: set_error("th_gemm: no bf16 kernel for tile %d", bnc); return TH_ERR_UNSUPPORTED;
     }
   }
