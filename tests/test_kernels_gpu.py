@@ -325,6 +325,9 @@ def _ssd_case(bs, s, h, p, n, g, dtype, seed):
 @pytest.mark.parametrize("bs,s,h,p,n,g,chunk,dtype", [
     (2, 256, 4, 64, 64, 1, 64, torch.float32), (1, 200, 4, 32, 32, 2, 64, torch.float32),
     (2, 512, 2, 64, 128, 1, 256, torch.float32), (2, 1024, 16, 64, 64, 1, 64, torch.bfloat16),
+    # bf16 runs on the MFMA path: ragged length, groups, N=32, N=128 with 256-row chunks, 128- and 32-row chunks
+    (1, 200, 4, 32, 32, 2, 64, torch.bfloat16), (2, 512, 2, 64, 128, 1, 256, torch.bfloat16),
+    (2, 300, 4, 64, 64, 1, 128, torch.bfloat16), (1, 100, 2, 64, 64, 1, 32, torch.bfloat16),
 ])
 def test_ssd_chunked_vs_recurrence(gpu, bs, s, h, p, n, g, chunk, dtype):
     from oracle.mamba import ssd_chunked_program
@@ -348,14 +351,16 @@ def test_ssd_chunked_vs_recurrence(gpu, bs, s, h, p, n, g, chunk, dtype):
         assert _maxabs(out32, ref) < BF16_TOL
 
 
-def test_ssd_reference_form_padded_cum(gpu):
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_ssd_reference_form_padded_cum(gpu, dtype):
     """The reference's ssd kind: cum and dt padded to 32 columns per head, cum centred, full D."""
     from oracle.interpret import ssd_quadratic
     from torch_helion.hip import ops
 
-    announce("ssd reference form")
+    announce(f"ssd reference form {dtype}")
     bs, s, h, p, n, pad = 2, 256, 4, 32, 32, 32
-    x, bm, cm, dt, A, D, _ = _ssd_case(bs, s, h, p, n, h, torch.float32, seed=11)
+    x, bm, cm, dt, A, D, _ = _ssd_case(bs, s, h, p, n, h, dtype, seed=11)
+    dt = dt.float()
     da = (dt * A).reshape(bs, s, h)
     cum = torch.cumsum(da, 1) - 0.5 * da.sum(1, keepdim=True)             # centred per sequence
     cum_pad = cum.reshape(bs * s, h, 1).expand(bs * s, h, pad).reshape(bs * s, h * pad).contiguous()
@@ -363,6 +368,8 @@ def test_ssd_reference_form_padded_cum(gpu):
     d_full = D.repeat_interleave(p).reshape(1, -1).expand(bs * s, h * p).contiguous()
     mask = torch.ones(s, s).tril()
     attrs = {"batch": bs, "seq": s, "heads": h, "head_dim": p, "state_dim": n, "pad": pad}
+    if dtype != torch.float32:  # the kernel reads every operand in one dtype
+        cum_pad, dt_pad, d_full = cum_pad.to(dtype), dt_pad.to(dtype), d_full.to(dtype)
     ref = ssd_quadratic(cm.double(), bm.double(), x.double(), cum_pad.double(), dt_pad.double(), mask.double(),
                         d_full.double(), attrs)
     ws = torch.empty(ops.ssd_workspace_bytes(bs, s, h, p, n, 64) // 4 + 1, device=gpu)
@@ -371,7 +378,10 @@ def test_ssd_reference_form_padded_cum(gpu):
                     seq=s, heads=h, head_dim=p, state_dim=n, ngroups=h, chunk=64, cum=cum_pad.to(gpu), dt_stride=pad,
                     dskip=d_full.to(gpu))
     torch.cuda.synchronize()
-    assert _rel(out, ref) < F32_REL
+    if dtype == torch.float32:
+        assert _rel(out, ref) < F32_REL
+    else:
+        assert _maxabs(out, ref) < BF16_TOL
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])

@@ -17,6 +17,7 @@
 // (already centred, reference optimizer/passes.py:501-525); only differences of
 // it are used here, so its centring offset cancels.
 #include <algorithm>
+#include <cstdlib>
 
 #include "common.h"
 
@@ -261,6 +262,219 @@ __global__ void __launch_bounds__(256) ssd_out_kernel(SsdK p) {
   }
 }
 
+// ------------------------------------------------------ bf16 MFMA scan path
+// Same three-step scan with every product on v_mfma_f32_32x32x16_bf16 (bf16
+// operands, fp32 accumulation). Operand layouts of the 32x32x16 MFMA, lane l:
+//   A (32 x 16): row l%32, k = 8*(l/32) .. +8      B (16 x 32): col l%32, same k
+//   C (32 x 32): register r holds row 8*(r/4) + 4*(l/32) + r%4, col l%32.
+// The computed operands w_l x_l (chunk states), M = (C B^T) o L and the carried
+// state H are fp32; each enters the MFMA as hi + lo, two bf16 parts with
+// hi = bf16(v), lo = bf16(v - hi), so they carry ~16 mantissa bits. Inputs x,
+// B, C are bf16 already; all sums are fp32.
+
+__device__ __forceinline__ bf16x8_t pack8_bf16(const float* v) {
+  uint4 w;
+  w.x = (uint32_t)f32_to_bf16(v[0]) | ((uint32_t)f32_to_bf16(v[1]) << 16);
+  w.y = (uint32_t)f32_to_bf16(v[2]) | ((uint32_t)f32_to_bf16(v[3]) << 16);
+  w.z = (uint32_t)f32_to_bf16(v[4]) | ((uint32_t)f32_to_bf16(v[5]) << 16);
+  w.w = (uint32_t)f32_to_bf16(v[6]) | ((uint32_t)f32_to_bf16(v[7]) << 16);
+  return __builtin_bit_cast(bf16x8_t, w);
+}
+
+__device__ __forceinline__ void split8_bf16(const float* v, bf16x8_t& hi, bf16x8_t& lo) {
+  float h[8], l[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const uint16_t hb = f32_to_bf16(v[i]);
+    h[i] = bf16_to_f32(hb);
+    l[i] = v[i] - h[i];
+  }
+  hi = pack8_bf16(h);
+  lo = pack8_bf16(l);
+}
+
+__device__ __forceinline__ bf16x8_t ldg_bf16x8(const void* base, int64_t elem, bool ok) {
+  if (!ok) return __builtin_bit_cast(bf16x8_t, make_uint4(0, 0, 0, 0));
+  return *(const bf16x8_t*)((const uint16_t*)base + elem);
+}
+
+__device__ __forceinline__ int crow_of(int r, int lane) { return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3); }
+
+// Token-major bf16 rows [tok0 + l, col0 .. col0 + 8*C8) of chunk rows l < Q into
+// an LDS matrix dst[col][l] (row stride QS), each value times wl[l] (or 1).
+__device__ void stage_transposed(const void* src, int64_t ld, int64_t tok0, int64_t col0, int C8, int Q, int rows,
+                                 const float* wl, uint16_t* dst, int QS, uint16_t* dst_lo = nullptr) {
+  for (int e = threadIdx.x; e < Q * C8; e += 256) {
+    const int l = e / C8, c8 = e - l * C8;
+    uint4 raw = make_uint4(0, 0, 0, 0);
+    if (l < rows) raw = *(const uint4*)((const uint16_t*)src + (tok0 + l) * ld + col0 + c8 * 8);
+    const uint32_t ws[4] = {raw.x, raw.y, raw.z, raw.w};
+    uint16_t* d = dst + (c8 * 8) * QS + l;
+    if (wl) {
+      const float w = wl[l];
+      uint16_t* dl = dst_lo + (c8 * 8) * QS + l;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float v = __uint_as_float((i & 1) ? (ws[i >> 1] & 0xffff0000u) : (ws[i >> 1] << 16)) * w;
+        const uint16_t hb = f32_to_bf16(v);
+        d[i * QS] = hb;
+        dl[i * QS] = f32_to_bf16(v - bf16_to_f32(hb));
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        d[(2 * i) * QS] = (uint16_t)(ws[i] & 0xffffu);
+        d[(2 * i + 1) * QS] = (uint16_t)(ws[i] >> 16);
+      }
+    }
+  }
+}
+
+// S_c[p][n] = sum_l (w_l x_l[p]) B_l[n],  w_l = dt_l exp(cl_last - cl_l).
+__global__ void __launch_bounds__(256) ssd_state_mfma_kernel(SsdK p) {
+  extern __shared__ float sm[];
+  float* cl = sm;          // 256
+  float* dts = cl + 256;   // 256
+  float* tmp = dts + 256;  // 512
+  const int Q = p.Q, P = p.P, N = p.N, QS = Q + 8;
+  uint16_t* xt = (uint16_t*)(tmp + 512);  // [P][QS]  w_l x_l (hi part), transposed
+  uint16_t* xl = xt + P * QS;             // [P][QS]  its lo part
+  uint16_t* bt = xl + P * QS;             // [N][QS]  B_l, transposed
+  const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z, tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = h / p.hpg;
+  chunk_running_sum(p, b, h, c, cl, dts, tmp);
+  const int t0 = c * Q;
+  const int rows = min(Q, p.S - t0);
+  const float last = cl[Q - 1];
+  if (tid < Q) tmp[tid] = dts[tid] * __expf(last - cl[tid]);  // w_l (0 past the sequence end: dt = 0)
+  __syncthreads();
+  const int64_t tok0 = (int64_t)b * p.S + t0;
+  stage_transposed(p.x, p.ldx, tok0, (int64_t)h * P, P >> 3, Q, rows, tmp, xt, QS, xl);
+  stage_transposed(p.b, p.ldb, tok0, (int64_t)g * N, N >> 3, Q, rows, nullptr, bt, QS);
+  __syncthreads();
+  const int TN = N >> 5;
+  float* st = p.states + (((int64_t)b * p.H + h) * p.nc + c) * (int64_t)(P * N);
+  for (int tile = wave; tile < (P >> 5) * TN; tile += 4) {
+    const int ti = tile / TN, tj = tile - ti * TN;
+    f32x16_t acc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+    const uint16_t* ar = xt + (ti * 32 + (lane & 31)) * QS + 8 * (lane >> 5);
+    const uint16_t* arl = ar + P * QS;
+    const uint16_t* br = bt + (tj * 32 + (lane & 31)) * QS + 8 * (lane >> 5);
+    for (int k0 = 0; k0 < Q; k0 += 16) {
+      const bf16x8_t bv = *(const bf16x8_t*)(br + k0);
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(*(const bf16x8_t*)(ar + k0), bv, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(*(const bf16x8_t*)(arl + k0), bv, acc, 0, 0, 0);
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) st[(int64_t)(ti * 32 + crow_of(r, lane)) * N + tj * 32 + (lane & 31)] = acc[r];
+  }
+  if (tid == 0) p.tot[((int64_t)b * p.H + h) * p.nc + c] = last;
+}
+
+// One workgroup per chunk; each wave takes 32x32 output tiles (32 rows t,
+// 32 columns p):
+//   y = exp(cl_t) C_t H^T + sum_{s<=t} [(C_t . B_s) exp(cl_t - cl_s) dt_s] x_s + D x_t, times gate,
+// where H is the state entering the chunk (the carry kernel's output).
+template <int KS>  // state_dim / 16
+__global__ void __launch_bounds__(256) ssd_out_mfma_kernel(SsdK p) {
+  extern __shared__ float sm[];
+  float* cl = sm;
+  float* dts = cl + 256;
+  float* tmp = dts + 256;
+  const int Q = p.Q, P = p.P, N = KS * 16, QS = Q + 8;
+  constexpr int MS = 40;                  // M scratch row stride (bf16)
+  uint16_t* xt = (uint16_t*)(tmp + 512);  // [P][QS] x transposed
+  uint16_t* ms = xt + P * QS;             // per wave [32][MS]
+  const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z, tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = h / p.hpg;
+  chunk_running_sum(p, b, h, c, cl, dts, tmp);
+  const int t0 = c * Q;
+  const int rows = min(Q, p.S - t0);
+  const int64_t tok0 = (int64_t)b * p.S + t0;
+  stage_transposed(p.x, p.ldx, tok0, (int64_t)h * P, P >> 3, Q, rows, nullptr, xt, QS);
+  __syncthreads();
+  uint16_t* msw = ms + wave * 2 * 32 * MS;  // hi tile, then lo tile
+  uint16_t* msl = msw + 32 * MS;
+  const float* H = p.states + (((int64_t)b * p.H + h) * p.nc + c) * (int64_t)(P * N);
+  const int TP = P >> 5, ntb = (rows + 31) >> 5;
+  const int64_t ccol = (int64_t)g * N + 8 * (lane >> 5);
+  for (int unit = wave; unit < ntb * TP; unit += 4) {
+    const int tb = unit / TP, pt = unit - tb * TP;
+    const int trow = tb * 32 + (lane & 31);
+    bf16x8_t cf[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) cf[ks] = ldg_bf16x8(p.c, (tok0 + trow) * p.ldc + ccol + ks * 16, trow < rows);
+    f32x16_t acc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+    if (c > 0) {
+      const float* hr = H + (int64_t)(pt * 32 + (lane & 31)) * N + 8 * (lane >> 5);
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const float4 h0 = *(const float4*)(hr + ks * 16), h1 = *(const float4*)(hr + ks * 16 + 4);
+        const float hv[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
+        bf16x8_t hh, hl;
+        split8_bf16(hv, hh, hl);
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(cf[ks], hh, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(cf[ks], hl, acc, 0, 0, 0);
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[r] *= __expf(cl[tb * 32 + crow_of(r, lane)]);
+    }
+    for (int sb = 0; sb <= tb; ++sb) {
+      const int srow = sb * 32 + (lane & 31);
+      f32x16_t gacc;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) gacc[r] = 0.f;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+        gacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+            cf[ks], ldg_bf16x8(p.b, (tok0 + srow) * p.ldb + ccol + ks * 16, srow < rows), gacc, 0, 0, 0);
+      // M[t][s] = G o L, written to this wave's scratch as bf16 (A-operand layout on read)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int tr = crow_of(r, lane), t = tb * 32 + tr;
+        const float m = (srow <= t && srow < rows) ? gacc[r] * __expf(cl[t] - cl[srow]) * dts[srow] : 0.f;
+        const uint16_t mh = f32_to_bf16(m);
+        msw[tr * MS + (lane & 31)] = mh;
+        msl[tr * MS + (lane & 31)] = f32_to_bf16(m - bf16_to_f32(mh));
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+      for (int k2 = 0; k2 < 2; ++k2) {
+        const int mo = (lane & 31) * MS + k2 * 16 + 8 * (lane >> 5);
+        const bf16x8_t bx = *(const bf16x8_t*)(xt + (pt * 32 + (lane & 31)) * QS + sb * 32 + k2 * 16 + 8 * (lane >> 5));
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(*(const bf16x8_t*)(msw + mo), bx, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(*(const bf16x8_t*)(msl + mo), bx, acc, 0, 0, 0);
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+    const int pp = pt * 32 + (lane & 31);
+    const int64_t col = (int64_t)h * P + pp;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int t = tb * 32 + crow_of(r, lane);
+      if (t >= rows) continue;
+      const int64_t tok = tok0 + t;
+      const float xv = load_elem(p.x, tok * p.ldx + col, p.dtype);
+      float v = acc[r];
+      if (p.dskip) v += xv * load_elem(p.dskip, tok * p.lddskip + col, p.dtype);
+      else if (p.D) v += xv * p.D[h];
+      if (p.gate) v *= load_elem(p.gate, tok * p.ldgate + col, p.gdt);
+      store_elem(p.y, tok * p.ldy + col, p.ydt, v);
+      if (p.y32) p.y32[tok * p.ldy32 + col] = v;
+    }
+  }
+}
+
 // ------------------------------------------------------------------ conv1d
 struct ConvK {
   int B, S, W, K, act, xdt, ydt;
@@ -287,10 +501,21 @@ __global__ void __launch_bounds__(256) conv1d_causal_kernel(ConvK p) {
 }
 
 static size_t state_lds(int P, int N) { return (size_t)(256 * 4 + 32 * P + 32 * N) * 4; }
+static size_t state_mfma_lds(int Q, int P, int N) { return 1024 * 4 + (size_t)(2 * P + N) * (Q + 8) * 2; }
+static size_t out_mfma_lds(int Q, int P) { return 1024 * 4 + (size_t)P * (Q + 8) * 2 + 4 * 2 * 32 * 40 * 2; }
 static size_t out_lds(int RB, int P, int N) {
   const size_t intra = (size_t)RB * (N + 1) + (size_t)RB * (P + 1) + (size_t)RB * (RB + 1);
   const size_t inter = (size_t)P * (N + 1);
   return (size_t)(256 * 4 + RB * (N + 1) + std::max(intra, inter)) * 4;
+}
+
+// TH_SSD_VALU=1 keeps the fp32 VALU kernels for bf16 inputs too.
+static bool ssd_force_valu() {
+  static const bool v = [] {
+    const char* e = getenv("TH_SSD_VALU");
+    return e && e[0] == '1';
+  }();
+  return v;
 }
 
 }  // namespace th
@@ -341,6 +566,31 @@ extern "C" int th_ssd_chunked(const th_ssd_desc* d, void* stream) {
   k.states = d->workspace;
   k.tot = d->workspace + (int64_t)k.B * k.H * k.nc * k.P * k.N;
   hipStream_t s = (hipStream_t)stream;
+  // MFMA path: bf16 operands, 32-multiple tiles, 16-byte aligned rows.
+  auto al16 = [](const void* q) { return ((uintptr_t)q & 15) == 0; };
+  const bool mfma = d->dtype == TH_BF16 && k.P % 32 == 0 && k.P <= 128 && (k.N == 32 || k.N == 64 || k.N == 128) &&
+                    k.Q % 32 == 0 && d->ld_x % 8 == 0 && d->ld_b % 8 == 0 && d->ld_c % 8 == 0 && al16(d->x) &&
+                    al16(d->b) && al16(d->c) && state_mfma_lds(k.Q, k.P, k.N) <= 163840 &&
+                    out_mfma_lds(k.Q, k.P) <= 163840 && !ssd_force_valu();
+  if (mfma) {
+    const size_t l1 = state_mfma_lds(k.Q, k.P, k.N), l3 = out_mfma_lds(k.Q, k.P);
+    const void* outk = k.N == 32 ? (const void*)ssd_out_mfma_kernel<2>
+                       : k.N == 64 ? (const void*)ssd_out_mfma_kernel<4> : (const void*)ssd_out_mfma_kernel<8>;
+    TH_CHECK_HIP(hipFuncSetAttribute((const void*)ssd_state_mfma_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)l1));
+    TH_CHECK_HIP(hipFuncSetAttribute(outk, hipFuncAttributeMaxDynamicSharedMemorySize, (int)l3));
+    hipLaunchKernelGGL(ssd_state_mfma_kernel, dim3(k.nc, k.H, k.B), dim3(256), l1, s, k);
+    TH_CHECK_LAUNCH();
+    hipLaunchKernelGGL(ssd_carry_kernel, dim3((unsigned)cdiv(k.P * k.N, 256), k.H, k.B), dim3(256), 0, s, k);
+    TH_CHECK_LAUNCH();
+    if (k.N == 32)
+      hipLaunchKernelGGL(ssd_out_mfma_kernel<2>, dim3(k.nc, k.H, k.B), dim3(256), l3, s, k);
+    else if (k.N == 64)
+      hipLaunchKernelGGL(ssd_out_mfma_kernel<4>, dim3(k.nc, k.H, k.B), dim3(256), l3, s, k);
+    else
+      hipLaunchKernelGGL(ssd_out_mfma_kernel<8>, dim3(k.nc, k.H, k.B), dim3(256), l3, s, k);
+    TH_CHECK_LAUNCH();
+    return TH_OK;
+  }
   const size_t l1 = state_lds(k.P, k.N), l3 = out_lds(RB, k.P, k.N);
   TH_CHECK_HIP(hipFuncSetAttribute((const void*)ssd_state_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)l1));
   TH_CHECK_HIP(hipFuncSetAttribute((const void*)ssd_out_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)l3));
