@@ -49,6 +49,7 @@ __device__ __forceinline__ float softplusf_(float x) { return __logf(1.f + __exp
 void set_error(const char* fmt, ...);
 bool device_ready();  // th_init was called for the current device
 int device_cus();     // compute units of the current device (0 before th_init)
+int ssd_init_device();  // per-device set-up of the scan kernels (called by th_init)
 
 #define TH_CHECK_ARG(cond, ...)            \
   do {                                     \

@@ -396,7 +396,18 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-template <int BM, int BNC, bool SUMSQ>
+// Wait until at most n tiles of PER loads each are still in flight (n < 4).
+template <int PER>
+__device__ __forceinline__ void wait_tiles(int n) {
+  switch (n) {
+    case 0: wait_vmcnt<0>(); break;
+    case 1: wait_vmcnt<PER>(); break;
+    case 2: wait_vmcnt<(2 * PER < 64 ? 2 * PER : 63)>(); break;
+    default: wait_vmcnt<(3 * PER < 64 ? 3 * PER : 63)>(); break;
+  }
+}
+
+template <int BM, int BNC, bool SUMSQ, int STAGES>
 __global__ void __launch_bounds__(256, 1) gemm_bf16_dl_kernel(GemmK p) {
 #if defined(__HIP_DEVICE_COMPILE__)  // the buffer-resource type exists only in the device pass
   constexpr int WM = BM / 2, WN = BNC / 2;
@@ -405,7 +416,8 @@ __global__ void __launch_bounds__(256, 1) gemm_bf16_dl_kernel(GemmK p) {
   constexpr int STAGE = (BM + BNC) * 128;
   constexpr int SROW = BNC + 8;
   constexpr int EPI_BYTES = WM * SROW * 4;
-  constexpr int MAIN_BYTES = 2 * STAGE;
+  constexpr int MAIN_BYTES = STAGES * STAGE;
+  static_assert(STAGES >= 2 && STAGES <= 4 && (STAGES - 1) * (LA + LB) < 64, "stage count");
   constexpr int BODY = MAIN_BYTES > EPI_BYTES ? MAIN_BYTES : EPI_BYTES;
   constexpr int NMF = TM * TN;
   __shared__ __attribute__((aligned(16))) char smem[BODY + BM * 4];
@@ -483,13 +495,10 @@ __global__ void __launch_bounds__(256, 1) gemm_bf16_dl_kernel(GemmK p) {
     }
   };
 
-  issue_tile(0, 0);
-  if (nk > 1) {
-    issue_tile(1, 1);
-    wait_vmcnt<LA + LB>();
-  } else {
-    wait_vmcnt<0>();
-  }
+  // K tile j lives in stage j % STAGES; the first STAGES tiles start at once.
+  const int pre = min(STAGES, nk);
+  for (int j = 0; j < pre; ++j) issue_tile(j, j);
+  wait_tiles<LA + LB>(pre - 1);
   __syncthreads();
   read_frags(0, 0, 0);
 
@@ -497,7 +506,7 @@ __global__ void __launch_bounds__(256, 1) gemm_bf16_dl_kernel(GemmK p) {
   // next to the MFMA that consumes it: every read is issued one full step
   // (NMF MFMAs) ahead of its use.
   for (int kt = 0; kt < nk; ++kt) {
-    const int st = kt & 1;
+    const int st = kt % STAGES;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
       const int slot = ks & 1;
@@ -511,10 +520,12 @@ __global__ void __launch_bounds__(256, 1) gemm_bf16_dl_kernel(GemmK p) {
         mfmas(slot, 0, NMF / 2);
         __builtin_amdgcn_sched_barrier(0);
         if (kt + 1 < nk) {
-          wait_vmcnt<0>();
+          // tile kt+1 must have landed; tiles kt+2 .. kt+STAGES-1 may still be in flight
+          wait_tiles<LA + LB>(max(0, min(STAGES - 2, nk - 2 - kt)));
           __syncthreads();
-          read_frags(st ^ 1, 0, 0);
-          if (kt + 2 < nk) issue_tile(kt + 2, st);
+          read_frags((kt + 1) % STAGES, 0, 0);
+          // every wave has read all of stage st: refill it with tile kt+STAGES
+          if (kt + STAGES < nk) issue_tile(kt + STAGES, st);
         }
         __builtin_amdgcn_sched_barrier(0);
         mfmas(slot, NMF / 2, NMF);
@@ -1053,7 +1064,7 @@ static int choose_bn(int64_t N, int n_acc, int in_dtype) {
     }
   }
   switch (n_acc) {
-    case 1: return N >= 192 ? 256 : (N > 64 ? 128 : 64);
+    case 1: return N >= 2048 ? 256 : (N >= 768 ? 128 : 64);
     case 2: return N >= 128 ? 128 : (N > 32 ? 64 : 32);
     case 3: return 64;
     default: return N > 32 ? 64 : 32;
@@ -1134,12 +1145,18 @@ static void launch_bf16(const GemmK& k, hipStream_t s) {
   hipLaunchKernelGGL((gemm_bf16_kernel<BM, BNC>), dim3(k.tiles_m * k.tiles_n), dim3(256), 0, s, k);
 }
 
+// 64-row tiles are for small problems: deeper pipelines there hide the
+// global-load latency that a short K loop cannot amortise.
+template <int BM, int BNC>
+constexpr int dl_stages() { return BM > 64 ? 2 : (BNC <= 128 ? 4 : 3); }
+
 template <int BM, int BNC>
 static void launch_bf16_dl(const GemmK& k, hipStream_t s) {
+  constexpr int S = dl_stages<BM, BNC>();
   if (k.sumsq)
-    hipLaunchKernelGGL((gemm_bf16_dl_kernel<BM, BNC, true>), dim3(k.tiles_m * k.tiles_n), dim3(256), 0, s, k);
+    hipLaunchKernelGGL((gemm_bf16_dl_kernel<BM, BNC, true, S>), dim3(k.tiles_m * k.tiles_n), dim3(256), 0, s, k);
   else
-    hipLaunchKernelGGL((gemm_bf16_dl_kernel<BM, BNC, false>), dim3(k.tiles_m * k.tiles_n), dim3(256), 0, s, k);
+    hipLaunchKernelGGL((gemm_bf16_dl_kernel<BM, BNC, false, S>), dim3(k.tiles_m * k.tiles_n), dim3(256), 0, s, k);
 }
 
 template <int BM, int BNC>
@@ -1157,10 +1174,14 @@ enum class MainLoop { staged, direct, persistent };
 
 template <int BM, int BNC>
 static void launch_bf16_any(const GemmK& k, MainLoop m, hipStream_t s) {
-  switch (m) {
-    case MainLoop::persistent: launch_bf16_pk<BM, BNC>(k, s); break;
-    case MainLoop::direct: launch_bf16_dl<BM, BNC>(k, s); break;
-    default: launch_bf16<BM, BNC>(k, s); break;
+  if constexpr (BM == 64) {  // 64-row tiles exist for the direct loop only
+    launch_bf16_dl<BM, BNC>(k, s);
+  } else {
+    switch (m) {
+      case MainLoop::persistent: launch_bf16_pk<BM, BNC>(k, s); break;
+      case MainLoop::direct: launch_bf16_dl<BM, BNC>(k, s); break;
+      default: launch_bf16<BM, BNC>(k, s); break;
+    }
   }
 }
 
@@ -1266,9 +1287,12 @@ extern "C" int th_gemm(const th_gemm_desc* d, void* stream) {
       default: set_error("th_gemm: no fp32 kernel for tile %d", bnc); return TH_ERR_UNSUPPORTED;
     }
   } else {
-    const int64_t big_blocks = cdiv(d->M, 256) * k.tiles_n;
-    const bool big = big_blocks >= 512;
-    k.tiles_m = (int)cdiv(d->M, big ? 256 : 128);
+    // Row tile: 256 when that still gives two blocks per CU, 128 when it gives
+    // one, else 64 (small problems need the parallelism more than the reuse).
+    const int64_t cus = device_cus() > 0 ? device_cus() : 256;
+    int bm = cdiv(d->M, 256) * k.tiles_n >= 2 * cus ? 256 : cdiv(d->M, 128) * k.tiles_n >= cus ? 128 : 64;
+    const bool big = bm == 256;
+    k.tiles_m = (int)cdiv(d->M, bm);
     // Direct-to-LDS main loop: whole 64-wide K tiles, and 32-bit buffer offsets
     // (one block's rows of lhs and of the packed rhs under 2 GiB).
     const bool direct = d->K % 64 == 0 && (int64_t)256 * d->ld_lhs * 2 < ((int64_t)1 << 31) &&
@@ -1283,11 +1307,16 @@ extern "C" int th_gemm(const th_gemm_desc* d, void* stream) {
     const int force = forced_main_loop();
     if (direct) ml = wave_epi ? MainLoop::persistent : MainLoop::direct;
     if (force >= 0 && force < (int)ml) ml = (MainLoop)force;
+    if (bm == 64 && ml == MainLoop::persistent) ml = MainLoop::direct;  // 64-row tiles: direct loop only
+    if (bm == 64 && ml == MainLoop::staged) {  // the staged loop has no 64-row tile
+      k.tiles_m = (int)cdiv(d->M, 128);
+      bm = 128;
+    }
     switch (bnc) {
-      case 64: big ? launch_bf16_any<256, 64>(k, ml, s) : launch_bf16_any<128, 64>(k, ml, s); break;
-      case 128: big ? launch_bf16_any<256, 128>(k, ml, s) : launch_bf16_any<128, 128>(k, ml, s); break;
-      case 192: big ? launch_bf16_any<256, 192>(k, ml, s) : launch_bf16_any<128, 192>(k, ml, s); break;
-      case 256: big ? launch_bf16_any<256, 256>(k, ml, s) : launch_bf16_any<128, 256>(k, ml, s); break;
+      case 64: bm == 64 ? launch_bf16_any<64, 64>(k, ml, s) : big ? launch_bf16_any<256, 64>(k, ml, s) : launch_bf16_any<128, 64>(k, ml, s); break;
+      case 128: bm == 64 ? launch_bf16_any<64, 128>(k, ml, s) : big ? launch_bf16_any<256, 128>(k, ml, s) : launch_bf16_any<128, 128>(k, ml, s); break;
+      case 192: bm == 64 ? launch_bf16_any<64, 192>(k, ml, s) : big ? launch_bf16_any<256, 192>(k, ml, s) : launch_bf16_any<128, 192>(k, ml, s); break;
+      case 256: bm == 64 ? launch_bf16_any<64, 256>(k, ml, s) : big ? launch_bf16_any<256, 256>(k, ml, s) : launch_bf16_any<128, 256>(k, ml, s); break;
       default: set_error("th_gemm: no bf16 kernel for tile %d", bnc); return TH_ERR_UNSUPPORTED;
     }
   }

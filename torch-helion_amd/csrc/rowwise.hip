@@ -24,29 +24,24 @@ struct NormK {
   float inv_k, eps;
   float* out32;
   int64_t ldo32;
+  int ovec, o32vec;  // fp32 out / out32 rows are 16-byte aligned
 };
 
-// NCH = 16-byte chunks per lane held in registers (0 = stream the row twice).
-template <int NCH>
+// NCH = 16-byte chunks per lane held in registers (0 = stream the row twice);
+// XB = bf16 input (8 values per chunk) or fp32 (4). Every load and store is a
+// 16-byte vector access except fp32 outputs whose rows are not 16-byte aligned.
+template <int NCH, bool XB>
 __global__ void __launch_bounds__(256) rmsnorm_kernel(NormK p) {
+  constexpr int PER = XB ? 8 : 4;
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= p.M) return;
-  const int per = p.xdt == TH_BF16 ? 8 : 4;  // elements per chunk
-  const int64_t nch = p.K / per;              // K is a multiple of `per`
-  const char* xr = (const char*)p.x + row * p.ldx * (p.xdt == TH_BF16 ? 2 : 4);
-  float ss = 0.f;
-  uint4 keep[NCH > 0 ? NCH : 1];
-  if (NCH > 0) {
-#pragma unroll
-    for (int i = 0; i < NCH; ++i) {
-      const int64_t c = lane + 64 * i;
-      keep[i] = c < nch ? ((const uint4*)xr)[c] : make_uint4(0, 0, 0, 0);
-    }
-  }
-  auto chunk_vals = [&](uint4 w, float* v) {
-    if (p.xdt == TH_BF16) {
+  const int64_t nch = p.K / PER;  // K is a multiple of PER
+  const uint4* xr = (const uint4*)((const char*)p.x + row * p.ldx * (XB ? 2 : 4));
+  auto vals = [&](uint4 w, float* v) {
+    if constexpr (XB) {
       const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
       for (int q = 0; q < 4; ++q) {
         v[2 * q] = __uint_as_float(ws[q] << 16);
         v[2 * q + 1] = __uint_as_float(ws[q] & 0xffff0000u);
@@ -56,35 +51,51 @@ __global__ void __launch_bounds__(256) rmsnorm_kernel(NormK p) {
       v[2] = __uint_as_float(w.z); v[3] = __uint_as_float(w.w);
     }
   };
-  if (NCH > 0) {
+  float ss = 0.f;
+  uint4 keep[NCH > 0 ? NCH : 1];
+  if constexpr (NCH > 0) {
 #pragma unroll
     for (int i = 0; i < NCH; ++i) {
-      float v[8];
-      chunk_vals(keep[i], v);
-      for (int q = 0; q < per; ++q) ss += v[q] * v[q];
+      const int64_t c = lane + 64 * i;
+      keep[i] = c < nch ? xr[c] : make_uint4(0, 0, 0, 0);
+      float v[PER];
+      vals(keep[i], v);
+#pragma unroll
+      for (int q = 0; q < PER; ++q) ss += v[q] * v[q];
     }
   } else {
     for (int64_t c = lane; c < nch; c += 64) {
-      float v[8];
-      chunk_vals(((const uint4*)xr)[c], v);
-      for (int q = 0; q < per; ++q) ss += v[q] * v[q];
+      float v[PER];
+      vals(xr[c], v);
+#pragma unroll
+      for (int q = 0; q < PER; ++q) ss += v[q] * v[q];
     }
   }
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
   const float r = rsqrtf(ss * p.inv_k + p.eps);
-  auto emit = [&](int64_t c, uint4 w) {
-    float v[8];
-    chunk_vals(w, v);
-    const int64_t base = c * per;
-    for (int q = 0; q < per; ++q) v[q] = v[q] * r * p.gain[base + q];
-    if (p.out32) {
-      float* o32 = p.out32 + row * p.ldo32 + base;
-      for (int q = 0; q < per; ++q) o32[q] = v[q];
+  auto store_f32 = [&](float* dst, bool vec, const float* v) {
+    if (vec) {
+#pragma unroll
+      for (int q = 0; q < PER; q += 4) *(float4*)(dst + q) = make_float4(v[q], v[q + 1], v[q + 2], v[q + 3]);
+    } else {
+#pragma unroll
+      for (int q = 0; q < PER; ++q) dst[q] = v[q];
     }
+  };
+  auto emit = [&](int64_t c, uint4 w) {
+    float v[PER];
+    vals(w, v);
+    const int64_t base = c * PER;
+#pragma unroll
+    for (int q = 0; q < PER; q += 4) {
+      const float4 g = *(const float4*)(p.gain + base + q);
+      v[q] *= r * g.x; v[q + 1] *= r * g.y; v[q + 2] *= r * g.z; v[q + 3] *= r * g.w;
+    }
+    if (p.out32) store_f32(p.out32 + row * p.ldo32 + base, p.o32vec, v);
     if (p.odt == TH_BF16) {
       uint16_t* orow = (uint16_t*)p.out + row * p.ldo + base;
-      if (per == 8) {
+      if constexpr (XB) {
         uint4 o;
         o.x = (uint32_t)f32_to_bf16(v[0]) | ((uint32_t)f32_to_bf16(v[1]) << 16);
         o.y = (uint32_t)f32_to_bf16(v[2]) | ((uint32_t)f32_to_bf16(v[3]) << 16);
@@ -92,21 +103,21 @@ __global__ void __launch_bounds__(256) rmsnorm_kernel(NormK p) {
         o.w = (uint32_t)f32_to_bf16(v[6]) | ((uint32_t)f32_to_bf16(v[7]) << 16);
         *(uint4*)orow = o;
       } else {
-        for (int q = 0; q < per; ++q) orow[q] = f32_to_bf16(v[q]);
+#pragma unroll
+        for (int q = 0; q < PER; ++q) orow[q] = f32_to_bf16(v[q]);
       }
     } else {
-      float* orow = (float*)p.out + row * p.ldo + base;
-      for (int q = 0; q < per; ++q) orow[q] = v[q];
+      store_f32((float*)p.out + row * p.ldo + base, p.ovec, v);
     }
   };
-  if (NCH > 0) {
+  if constexpr (NCH > 0) {
 #pragma unroll
     for (int i = 0; i < NCH; ++i) {
       const int64_t c = lane + 64 * i;
       if (c < nch) emit(c, keep[i]);
     }
   } else {
-    for (int64_t c = lane; c < nch; c += 64) emit(c, ((const uint4*)xr)[c]);
+    for (int64_t c = lane; c < nch; c += 64) emit(c, xr[c]);
   }
 }
 
@@ -205,14 +216,30 @@ extern "C" int th_rmsnorm(const th_rmsnorm_desc* d, void* stream) {
   k.out32 = d->out32; k.ldo32 = d->ld_out32;
   TH_CHECK_ARG(!d->out32 || d->ld_out32 >= d->K, "th_rmsnorm: ld_out32 < K");
   const int64_t nch = d->K / per;
+  auto al16 = [](const void* q) { return ((uintptr_t)q & 15) == 0; };
+  k.ovec = d->out_dtype == TH_F32 && al16(d->out) && d->ld_out % 4 == 0;
+  k.o32vec = d->out32 && al16(d->out32) && d->ld_out32 % 4 == 0;
+  TH_CHECK_ARG(al16(d->gain), "th_rmsnorm: gain must be 16-byte aligned");
   const dim3 grid((unsigned)cdiv(d->M, 4));
   hipStream_t s = (hipStream_t)stream;
-  if (nch <= 64) hipLaunchKernelGGL(rmsnorm_kernel<1>, grid, dim3(256), 0, s, k);
-  else if (nch <= 128) hipLaunchKernelGGL(rmsnorm_kernel<2>, grid, dim3(256), 0, s, k);
-  else if (nch <= 256) hipLaunchKernelGGL(rmsnorm_kernel<4>, grid, dim3(256), 0, s, k);
-  else if (nch <= 512) hipLaunchKernelGGL(rmsnorm_kernel<8>, grid, dim3(256), 0, s, k);
-  else if (nch <= 1024) hipLaunchKernelGGL(rmsnorm_kernel<16>, grid, dim3(256), 0, s, k);
-  else hipLaunchKernelGGL(rmsnorm_kernel<0>, grid, dim3(256), 0, s, k);
+  const int nsel = nch <= 64 ? 1 : nch <= 128 ? 2 : nch <= 256 ? 4 : nch <= 512 ? 8 : nch <= 1024 ? 16 : 0;
+  const bool xb = d->x_dtype == TH_BF16;
+#define TH_NORM_LAUNCH(N_)                                                     \
+  do {                                                                         \
+    if (xb)                                                                    \
+      hipLaunchKernelGGL((rmsnorm_kernel<N_, true>), grid, dim3(256), 0, s, k);  \
+    else                                                                       \
+      hipLaunchKernelGGL((rmsnorm_kernel<N_, false>), grid, dim3(256), 0, s, k); \
+  } while (0)
+  switch (nsel) {
+    case 1: TH_NORM_LAUNCH(1); break;
+    case 2: TH_NORM_LAUNCH(2); break;
+    case 4: TH_NORM_LAUNCH(4); break;
+    case 8: TH_NORM_LAUNCH(8); break;
+    case 16: TH_NORM_LAUNCH(16); break;
+    default: TH_NORM_LAUNCH(0); break;
+  }
+#undef TH_NORM_LAUNCH
   TH_CHECK_LAUNCH();
   return TH_OK;
 }

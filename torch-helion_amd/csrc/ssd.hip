@@ -509,6 +509,18 @@ static size_t out_lds(int RB, int P, int N) {
   return (size_t)(256 * 4 + RB * (N + 1) + std::max(intra, inter)) * 4;
 }
 
+constexpr size_t kMaxLds = 163840;  // 160 KiB per workgroup on gfx950
+
+// Raise the dynamic-LDS limit of the scan kernels once per device (th_init),
+// so that launching them needs no attribute call (and can be graph-captured).
+int ssd_init_device() {
+  const void* fns[] = {(const void*)ssd_state_kernel, (const void*)ssd_out_kernel, (const void*)ssd_state_mfma_kernel,
+                       (const void*)ssd_out_mfma_kernel<2>, (const void*)ssd_out_mfma_kernel<4>,
+                       (const void*)ssd_out_mfma_kernel<8>};
+  for (const void* f : fns) TH_CHECK_HIP(hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxLds));
+  return TH_OK;
+}
+
 // TH_SSD_VALU=1 keeps the fp32 VALU kernels for bf16 inputs too.
 static bool ssd_force_valu() {
   static const bool v = [] {
@@ -570,14 +582,10 @@ extern "C" int th_ssd_chunked(const th_ssd_desc* d, void* stream) {
   auto al16 = [](const void* q) { return ((uintptr_t)q & 15) == 0; };
   const bool mfma = d->dtype == TH_BF16 && k.P % 32 == 0 && k.P <= 128 && (k.N == 32 || k.N == 64 || k.N == 128) &&
                     k.Q % 32 == 0 && d->ld_x % 8 == 0 && d->ld_b % 8 == 0 && d->ld_c % 8 == 0 && al16(d->x) &&
-                    al16(d->b) && al16(d->c) && state_mfma_lds(k.Q, k.P, k.N) <= 163840 &&
-                    out_mfma_lds(k.Q, k.P) <= 163840 && !ssd_force_valu();
+                    al16(d->b) && al16(d->c) && state_mfma_lds(k.Q, k.P, k.N) <= kMaxLds &&
+                    out_mfma_lds(k.Q, k.P) <= kMaxLds && !ssd_force_valu();
   if (mfma) {
     const size_t l1 = state_mfma_lds(k.Q, k.P, k.N), l3 = out_mfma_lds(k.Q, k.P);
-    const void* outk = k.N == 32 ? (const void*)ssd_out_mfma_kernel<2>
-                       : k.N == 64 ? (const void*)ssd_out_mfma_kernel<4> : (const void*)ssd_out_mfma_kernel<8>;
-    TH_CHECK_HIP(hipFuncSetAttribute((const void*)ssd_state_mfma_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)l1));
-    TH_CHECK_HIP(hipFuncSetAttribute(outk, hipFuncAttributeMaxDynamicSharedMemorySize, (int)l3));
     hipLaunchKernelGGL(ssd_state_mfma_kernel, dim3(k.nc, k.H, k.B), dim3(256), l1, s, k);
     TH_CHECK_LAUNCH();
     hipLaunchKernelGGL(ssd_carry_kernel, dim3((unsigned)cdiv(k.P * k.N, 256), k.H, k.B), dim3(256), 0, s, k);
@@ -592,8 +600,7 @@ extern "C" int th_ssd_chunked(const th_ssd_desc* d, void* stream) {
     return TH_OK;
   }
   const size_t l1 = state_lds(k.P, k.N), l3 = out_lds(RB, k.P, k.N);
-  TH_CHECK_HIP(hipFuncSetAttribute((const void*)ssd_state_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)l1));
-  TH_CHECK_HIP(hipFuncSetAttribute((const void*)ssd_out_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)l3));
+  TH_CHECK_ARG(l1 <= kMaxLds && l3 <= kMaxLds, "th_ssd_chunked: shape needs more than 160 KiB of LDS");
   hipLaunchKernelGGL(ssd_state_kernel, dim3(k.nc, k.H, k.B), dim3(256), l1, s, k);
   TH_CHECK_LAUNCH();
   hipLaunchKernelGGL(ssd_carry_kernel, dim3((unsigned)cdiv(k.P * k.N, 256), k.H, k.B), dim3(256), 0, s, k);

@@ -17,11 +17,17 @@ from ..cost_models.hw_spec import HardwareSpec
 from ..cost_models.roofline import kernel_cost
 
 
-def bench_program(dp, inputs, hw: HardwareSpec, warmup: int = 10, reps: int = 50) -> dict[str, Any]:
+def bench_program(dp, inputs, hw: HardwareSpec, warmup: int = 10, reps: int = 50, graph: bool = True) -> dict[str, Any]:
+    """Whole-forward time (replaying the captured HIP graph when ``graph``, so
+    host launch overhead is out of the timed region) and per-kernel times
+    (each launch bracketed by its own events)."""
     dp.set_inputs(list(inputs))
     stream = torch.cuda.current_stream(dp.device)
+    if graph and dp.graph is None:
+        dp.capture()
+    forward = dp.replay if graph else dp.launch_all
     for _ in range(warmup):
-        dp.launch_all()
+        forward()
     torch.cuda.synchronize(dp.device)
 
     # whole program: one event pair per forward
@@ -29,7 +35,7 @@ def bench_program(dp, inputs, hw: HardwareSpec, warmup: int = 10, reps: int = 50
     ends = [torch.cuda.Event(enable_timing=True) for _ in range(reps)]
     for i in range(reps):
         starts[i].record(stream)
-        dp.launch_all()
+        forward()
         ends[i].record(stream)
     torch.cuda.synchronize(dp.device)
     per_fwd = sorted(s.elapsed_time(e) * 1e3 for s, e in zip(starts, ends))
@@ -72,6 +78,7 @@ def bench_program(dp, inputs, hw: HardwareSpec, warmup: int = 10, reps: int = 50
         "us_p90": per_fwd[min(len(per_fwd) - 1, int(0.9 * len(per_fwd)))],
         "reps": reps,
         "warmup": warmup,
+        "graph": bool(graph),
         "kernels": kernels,
         "total_flops": total_flops,
         "sum_kernel_us": sum(k["us"] for k in kernels.values()),

@@ -55,6 +55,7 @@ class DeviceProgram:
         self.buffers: dict[str, torch.Tensor] = {}
         self.workspaces: list[torch.Tensor] = []
         self.launches: list[Launch] = []
+        self.graph: torch.cuda.CUDAGraph | None = None
         self.plans: dict[str, Any] = {}
         self._host_params = params
         for name in program.params:
@@ -101,11 +102,37 @@ class DeviceProgram:
         for l in self.launches:
             l.run()
 
+    def capture(self) -> None:
+        """Record the whole launch sequence into a HIP graph (torch.cuda.CUDAGraph).
+
+        Every launch reads and writes the buffers bound at lowering time and
+        allocates nothing, so the graph replays the program on whatever the
+        input buffers hold at replay time (``set_inputs`` first). One eager run
+        precedes the capture; nothing in the sequence records a memset."""
+        with torch.cuda.device(self.device):
+            torch.cuda.synchronize()
+            self.launch_all()
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                self.launch_all()
+            torch.cuda.synchronize()
+        self.graph = g
+
+    def replay(self) -> None:
+        """Run the captured graph on the current stream (``capture`` first)."""
+        if self.graph is None:
+            raise abi.HipBackendError("replay", abi.TH_ERR_INVALID, "no graph captured; call capture() first")
+        self.graph.replay()
+
     def run(self, inputs=None) -> list[torch.Tensor]:
         """Run the program; returns the program outputs (device tensors)."""
         if inputs is not None:
             self.set_inputs(inputs)
-        self.launch_all()
+        if self.graph is not None:
+            self.replay()
+        else:
+            self.launch_all()
         return self.outputs()
 
     def outputs(self, fp32: bool = False) -> list[torch.Tensor]:
