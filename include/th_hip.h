@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define TH_ABI_VERSION 1
+#define TH_ABI_VERSION 2
 
 typedef enum th_status {
   TH_OK = 0,
@@ -93,7 +93,8 @@ typedef struct th_epi_out {
 typedef struct th_gemm_desc {
   int64_t M, N, K;
   int32_t n_acc;          /* 0 .. TH_MAX_ACC */
-  int32_t in_dtype;       /* TH_BF16 (MFMA bf16) or TH_F32 (MFMA f32) */
+  int32_t in_dtype;       /* TH_BF16 (MFMA bf16), TH_F32 (MFMA f32), or TH_F8E4M3:
+                             bf16 lhs x e4m3 rhs with per-column scales (M <= 128) */
   const void* lhs;        /* [M, K] row-major, in_dtype */
   int64_t ld_lhs;
   const void* rhs_packed; /* th_gemm_pack_rhs output for (N, K, n_acc, in_dtype) */
@@ -113,6 +114,9 @@ typedef struct th_gemm_desc {
   int32_t pad2_;
   th_epi_out out[TH_MAX_OUT];
   float* sumsq_out;       /* optional [M] fp32: raw sum_k lhs^2 */
+  const float* rhs_scale; /* TH_F8E4M3: [n_acc][N] fp32, acc_i[:, n] *= rhs_scale[i*N + n] */
+  float* workspace;       /* TH_F8E4M3: th_gemm_workspace_bytes(...) bytes */
+  int64_t workspace_bytes;
 } th_gemm_desc;
 
 /* Per-accumulator column tile th_gemm uses for (N, n_acc, in_dtype); a block
@@ -125,12 +129,17 @@ int th_gemm_acc_tile(int64_t N, int32_t n_acc, int32_t in_dtype);
 int64_t th_gemm_packed_bytes(int64_t N, int64_t K, int32_t n_acc, int32_t in_dtype);
 
 /* Pack n_acc row-major [K, N] operands (dtype src_dtype, row stride ld_src)
- * into the K-contiguous, accumulator-interleaved layout th_gemm reads.
+ * into the K-contiguous, accumulator-interleaved layout th_gemm reads
+ * (TH_F8E4M3: e4m3 bytes in, copied unchanged).
  * Replaces the reference's per-kernel weight arguments w0..w{n-1}
  * (optimizer/partition.py:121-124, bound at codegen/emit.py:469-476). */
 int th_gemm_pack_rhs(const void* const* src, const int64_t* ld_src, int32_t src_dtype,
                      int64_t N, int64_t K, int32_t n_acc, int32_t in_dtype,
                      void* packed, void* stream);
+
+/* Workspace th_gemm needs for these sizes (0 for TH_BF16 / TH_F32; the
+ * split-K partial sums for TH_F8E4M3). -1 for invalid arguments. */
+int64_t th_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t n_acc, int32_t in_dtype);
 
 /* One OpIR gemm KernelSpec. */
 int th_gemm(const th_gemm_desc* desc, void* stream);
@@ -172,6 +181,38 @@ typedef struct th_attn_desc {
 } th_attn_desc;
 
 int th_attention_prefill(const th_attn_desc* desc, void* stream);
+
+/* ------------------------------------------------------ decode attention
+ * One new query token per sequence against a KV cache: for every sequence b
+ * and query head h (kv head h / (heads_q / heads_kv)),
+ *   o[b, h] = softmax(q[b, h] . K[b, 0:len_b, kvh]^T * scale) V[b, 0:len_b, kvh]
+ * The reference has no decode path; this is the attention kind of
+ * optimizer/evaluate.py:139-146 with one query row and a cache laid out as
+ * [batch][max_len][heads_kv][head_dim] (element strides below). The keys of a
+ * sequence are split n_split ways (0 = chosen by the library); with more than
+ * one split the partial results go through the workspace.
+ */
+typedef struct th_decode_desc {
+  int32_t batch, heads_q, heads_kv, head_dim;  /* head_dim 64 or 128, heads_q/heads_kv <= 16 */
+  int32_t max_len;        /* cache capacity in tokens */
+  int32_t n_split;        /* 0: choose; else the number of key ranges per (sequence, kv head) */
+  int32_t fixed_len;      /* keys per sequence when lengths is NULL (1..max_len) */
+  int32_t dtype;          /* TH_BF16 for q, caches and o */
+  float scale;
+  int32_t pad_;
+  const int32_t* lengths; /* optional [batch] device array of valid keys per sequence (>= 1) */
+  const void* q; int64_t ld_q;                         /* [batch, heads_q*head_dim] */
+  const void* k_cache; int64_t k_stride_b, k_stride_t; /* element strides: sequence, token */
+  const void* v_cache; int64_t v_stride_b, v_stride_t;
+  void* o; int64_t ld_o;                               /* [batch, heads_q*head_dim] */
+  float* workspace; int64_t workspace_bytes;
+} th_decode_desc;
+
+/* Workspace th_attention_decode needs for these sizes (0 when it needs none). */
+int64_t th_attention_decode_workspace_bytes(int32_t batch, int32_t heads_q, int32_t heads_kv, int32_t head_dim,
+                                            int32_t max_len, int32_t n_split);
+
+int th_attention_decode(const th_decode_desc* desc, void* stream);
 
 /* ------------------------------------------------------------ SSD scan
  * The Mamba-2 scan, per (batch b, head h) over token-major operands:

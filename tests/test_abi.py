@@ -45,7 +45,7 @@ def test_every_declared_symbol_is_exported_and_bound(lib):
 
 _STRUCTS = {
     "th_epi_out": "EpiOut", "th_gemm_desc": "GemmDesc", "th_rmsnorm_desc": "RmsNormDesc",
-    "th_attn_desc": "AttnDesc", "th_ssd_desc": "SsdDesc", "th_conv_desc": "ConvDesc", "th_vm_operand": "VmOperand", "th_vm_op": "VmOp", "th_vm_out": "VmOut",
+    "th_attn_desc": "AttnDesc", "th_decode_desc": "DecodeDesc", "th_ssd_desc": "SsdDesc", "th_conv_desc": "ConvDesc", "th_vm_operand": "VmOperand", "th_vm_op": "VmOp", "th_vm_out": "VmOut",
     "th_vm_desc": "VmDesc",
 }
 
@@ -102,7 +102,7 @@ def _gemm_desc(**over):
 
 
 @pytest.mark.parametrize("field,value,msg", [
-    ("n_acc", 7, "n_acc"), ("K", 60, "multiple of 8"), ("in_dtype", 3, "in_dtype"), ("n_out", 0, "n_out"),
+    ("n_acc", 7, "n_acc"), ("K", 60, "multiple of 8"), ("in_dtype", 2, "in_dtype"), ("n_out", 0, "n_out"),
     ("rscale_mask", 1, "without sumsq"), ("lhs", 4100, "aligned"),
 ])
 def test_gemm_rejects_bad_descriptors(lib, field, value, msg):
@@ -116,7 +116,8 @@ def test_gemm_rejects_bad_descriptors(lib, field, value, msg):
 def test_null_descriptors_are_rejected(lib):
     from torch_helion.hip import abi
 
-    for fn in ("th_gemm", "th_rmsnorm", "th_attention_prefill", "th_epilogue_vm", "th_ssd_chunked", "th_conv1d_causal"):
+    for fn in ("th_gemm", "th_rmsnorm", "th_attention_prefill", "th_attention_decode", "th_epilogue_vm", "th_ssd_chunked",
+               "th_conv1d_causal"):
         assert getattr(lib, fn)(None, None) == abi.TH_ERR_INVALID, fn
         assert "null descriptor" in abi.last_error(lib)
 
@@ -156,3 +157,17 @@ def test_product_raises_without_a_device():
     prog = Program("p", [], [], {}, [])
     with pytest.raises(abi.HipBackendError):
         DeviceProgram(prog, {}, device=__import__("torch").device("cpu"))
+
+
+def test_fp8_gemm_validation(lib):
+    """e4m3 weights: at most 128 rows, K a multiple of 32, per-column scales required."""
+    from torch_helion.hip import abi
+
+    for over, msg in (({"M": 129}, "at most 128 rows"), ({"K": 48}, "K % 32"), ({}, "rhs_scale")):
+        d = _gemm_desc(in_dtype=abi.TH_F8E4M3, **over)
+        assert lib.th_gemm(C.byref(d), None) == abi.TH_ERR_INVALID, over
+        assert msg in abi.last_error(lib), (over, abi.last_error(lib))
+    # e4m3 packs whole 32-K chunks
+    assert lib.th_gemm_packed_bytes(256, 40, 1, abi.TH_F8E4M3) == 256 * 64  # K padded to 32-wide chunks
+    assert lib.th_gemm_workspace_bytes(64, 4096, 4096, 1, abi.TH_BF16) == 0
+    assert lib.th_gemm_workspace_bytes(64, 4096, 4096, 1, abi.TH_F8E4M3) > 0

@@ -181,6 +181,67 @@ def test_gemm_rope_whole_heads_per_wave(gpu, hd, n_acc):
         assert _maxabs(o16[i], ref) < BF16_TOL, i
 
 
+def _quant_e4m3(w: torch.Tensor):
+    """Per-output-channel e4m3: s_n = max|W[:, n]| / 448, q = e4m3(W / s_n)."""
+    s = (w.abs().amax(0).clamp_min(1e-12) / 448.0).float()
+    q = (w / s).to(torch.float8_e4m3fn)
+    return q, s
+
+
+@pytest.mark.parametrize("M,N,K,case", [(64, 4096, 4096, "add"), (64, 1024, 4096, "rope_kv"),
+                                        (37, 2048, 1024, "swiglu"), (100, 512, 512, "acc")])
+def test_gemm_fp8_weights(gpu, M, N, K, case):
+    """bf16 activations x e4m3 weights with per-column scales (the decode projections), split-K,
+    against fp32 math on the dequantised weights."""
+    from torch_helion.hip import abi, ops
+
+    announce(f"gemm fp8 weights M={M} N={N} K={K} {case}")
+    g = torch.Generator().manual_seed(M + N + K)
+    n_acc = {"add": 1, "rope_kv": 2, "swiglu": 2, "acc": 1}[case]
+    x = torch.randn(M, K, generator=g).bfloat16()
+    qs = [_quant_e4m3(torch.randn(K, N, generator=g) * 0.02) for _ in range(n_acc)]
+    wdq = [q.float() * s[None, :] for q, s in qs]
+    xf = x.float()
+    accs = [xf @ w for w in wdq]
+    kw = {}
+    if case in ("rope_kv", "swiglu"):
+        r = ((xf * xf).sum(-1, keepdim=True) / K + 1e-5).pow(-0.5)
+        accs = [a * r for a in accs]
+        kw = dict(sumsq=True, rscale_mask=(1 << n_acc) - 1, inv_k=1.0 / K, eps=1e-5)
+    extras, outs32 = [], []
+    if case == "add":
+        res = torch.randn(M, N, generator=g)
+        refs = [accs[0] + res]
+        extras = [res.to(gpu)]
+        ops_ = [(abi.EPI_ADD, 0, -1, 0)]
+    elif case == "rope_kv":
+        hd, pos = 128, 4096
+        cos, sin = _rope_tables(pos + 1, hd, theta=500000.0)
+        c1, s1 = cos[pos:pos + 1].contiguous(), sin[pos:pos + 1].contiguous()
+        refs = [accs[0] * c1.repeat(M, N // hd) + _rot_heads(accs[0], hd) * s1.repeat(M, N // hd), accs[1]]
+        kw.update(rope_cos=c1.to(gpu), rope_sin=s1.to(gpu), rope_head_dim=hd, rope_period=1)
+        ops_ = [(abi.EPI_ROPE, 0, -1, -1), (abi.EPI_ACC, 1, -1, -1)]
+    elif case == "swiglu":
+        refs = [accs[0] * torch.sigmoid(accs[0]) * accs[1]]
+        ops_ = [(abi.EPI_SWIGLU, 0, 1, -1)]
+    else:
+        refs = [accs[0]]
+        ops_ = [(abi.EPI_ACC, 0, -1, -1)]
+    packed = ops.pack_rhs([q.to(gpu) for q, _ in qs], torch.float8_e4m3fn)
+    scale = torch.stack([s for _, s in qs]).to(gpu).contiguous()
+    ws = torch.empty(ops.gemm_workspace_bytes(M, N, K, n_acc, torch.float8_e4m3fn), dtype=torch.uint8, device=gpu)
+    o16 = [torch.empty(M, N, dtype=torch.bfloat16, device=gpu) for _ in ops_]
+    o32 = [torch.empty(M, N, device=gpu) for _ in ops_]
+    specs = [ops.EpiSpec(op, o, a=a, b=b, e=e) for (op, a, b, e), o in zip(ops_, o16)] + \
+            [ops.EpiSpec(op, o, a=a, b=b, e=e) for (op, a, b, e), o in zip(ops_, o32)]
+    ops.gemm(ops.GemmCall(M, N, K, n_acc, x.to(gpu), packed, specs, extras=extras, in_dtype=torch.float8_e4m3fn,
+                          rhs_scale=scale, workspace=ws, **kw))
+    torch.cuda.synchronize()
+    for i, ref in enumerate(refs):
+        assert _rel(o32[i], ref) < 1e-4, (case, i, _rel(o32[i], ref))
+        assert _maxabs(o16[i], ref) < BF16_TOL, (case, i)
+
+
 def test_gemm_extra_ops(gpu):
     from torch_helion.hip import abi, ops
 
@@ -267,6 +328,40 @@ def test_attention_f32(gpu):
                           head_dim=hd, scale=hd ** -0.5, causal=True)
     torch.cuda.synchronize()
     assert _rel(out, ref) < F32_REL
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,hd,max_len,lens,n_split", [
+    (3, 8, 2, 128, 1000, [1000, 517, 1], 0), (3, 8, 2, 128, 1000, [1000, 517, 1], 5),
+    (2, 4, 4, 64, 300, [300, 33], 1), (2, 16, 1, 64, 777, [777, 640], 0),
+    (64, 32, 8, 128, 4097, None, 0),
+])
+def test_attention_decode(gpu, B, Hq, Hkv, hd, max_len, lens, n_split):
+    """KV-cache decode attention vs the oracle attention (pinned against SDPA) per sequence."""
+    from oracle.llama import attention
+    from torch_helion.hip import ops
+
+    announce(f"attention decode B={B} Hq={Hq} Hkv={Hkv} hd={hd} max_len={max_len} lens={lens} split={n_split}")
+    g = torch.Generator().manual_seed(B * 7 + hd)
+    q = torch.randn(B, Hq * hd, generator=g).bfloat16()
+    kc = torch.randn(B, max_len, Hkv, hd, generator=g).bfloat16()
+    vc = torch.randn(B, max_len, Hkv, hd, generator=g).bfloat16()
+    scale = 1.0 / math.sqrt(hd)
+    lengths = lens if lens is not None else [max_len] * B
+    refs = []
+    for b in range(B):
+        L = lengths[b]
+        qb = q[b].float().reshape(1, Hq, 1, hd)
+        kb = kc[b, :L].float().permute(1, 0, 2).unsqueeze(0)
+        vb = vc[b, :L].float().permute(1, 0, 2).unsqueeze(0)
+        refs.append(attention(qb.double(), kb.double(), vb.double(), False).reshape(Hq * hd))
+    ref = torch.stack(refs)
+    ws = torch.empty(max(ops.attention_decode_workspace_bytes(B, Hq, Hkv, hd, max_len, n_split) // 4, 1), device=gpu)
+    out = torch.empty(B, Hq * hd, dtype=torch.bfloat16, device=gpu)
+    lt = torch.tensor(lengths, dtype=torch.int32, device=gpu) if lens is not None else None
+    ops.attention_decode(q.to(gpu), kc.to(gpu), vc.to(gpu), out, scale=scale, lengths=lt,
+                         fixed_len=0 if lens is not None else max_len, n_split=n_split, workspace=ws)
+    torch.cuda.synchronize()
+    assert _maxabs(out, ref) < BF16_TOL
 
 
 @pytest.mark.parametrize("dtype,M,K", [(torch.bfloat16, 1000, 4096), (torch.float32, 77, 512), (torch.bfloat16, 33, 40960)])

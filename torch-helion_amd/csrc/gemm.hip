@@ -24,38 +24,9 @@
 #include <type_traits>
 
 #include "common.h"
+#include "gemm_internal.h"
 
 namespace th {
-
-struct EpiOutK {
-  int op, a, b, e;
-  void* ptr;
-  int64_t ld;
-  int dtype, vec;
-};
-
-struct GemmK {
-  const void* A;
-  int64_t lda;
-  const void* B;
-  int64_t ldb;
-  int64_t M, N, K;
-  int tiles_m, tiles_n;
-  int bn, n_acc;
-  int sumsq;
-  unsigned rscale_mask;
-  float inv_k, eps;
-  const void* extra[TH_MAX_EXTRA];
-  int64_t ld_extra[TH_MAX_EXTRA];
-  int extra_dtype[TH_MAX_EXTRA];
-  int extra_vec[TH_MAX_EXTRA];
-  const float* rcos;
-  const float* rsin;
-  int hd, period;
-  int n_out;
-  EpiOutK out[TH_MAX_OUT];
-  float* sumsq_out;
-};
 
 // Block id -> output tile. Consecutive workgroups are dealt round-robin to the
 // 8 XCDs; remap so each XCD owns a contiguous range of logical tiles, then walk
@@ -1053,6 +1024,36 @@ __global__ void __launch_bounds__(256) pack_rhs_kernel(PackK p) {
   }
 }
 
+// e4m3 operands, bytes copied unchanged, in fragment-major order: for each
+// group g of 32 packed rows and each 32-wide K chunk c, one 1 KiB block at
+// (g * Kp/32 + c) * 1024 whose 16-byte slot l (l = 0..63) holds row
+// 32g + l%32, k = 32c + 16*(l/32) .. +16. A wave loading 16 bytes per lane
+// then reads one contiguous KiB: exactly the MFMA operands of that chunk.
+// One thread per 16-byte slot.
+__global__ void __launch_bounds__(256) pack_rhs_fp8_kernel(PackK p) {
+  const int64_t slot = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t nch = p.Kp / 32;
+  const int64_t total = (p.rows / 32) * nch * 64;
+  if (slot >= total) return;
+  const int l = (int)(slot & 63);
+  const int64_t blk = slot >> 6;
+  const int64_t g = blk / nch, c = blk - g * nch;
+  const int64_t r = g * 32 + (l & 31);
+  const int64_t t = r / p.bnc, rem = r - t * p.bnc;
+  const int i = (int)(rem / p.bn);
+  const int64_t n = t * p.bn + (rem - (int64_t)i * p.bn);
+  const int64_t k0 = c * 32 + 16 * (l >> 5);
+  uint32_t w[4] = {0, 0, 0, 0};
+  const uint8_t* src = (const uint8_t*)p.src[i];
+#pragma unroll
+  for (int q = 0; q < 16; ++q) {
+    const int64_t k = k0 + q;
+    const uint32_t v = (n < p.N && k < p.K) ? src[k * p.ld[i] + n] : 0u;
+    w[q >> 2] |= v << (8 * (q & 3));
+  }
+  *(uint4*)((uint8_t*)p.out + slot * 16) = make_uint4(w[0], w[1], w[2], w[3]);
+}
+
 // Per-accumulator column tile bn; the block tile is n_acc * bn columns.
 static int choose_bn(int64_t N, int n_acc, int in_dtype) {
   if (in_dtype == TH_F32) {
@@ -1072,9 +1073,12 @@ static int choose_bn(int64_t N, int n_acc, int in_dtype) {
 }
 
 static int64_t packed_kp(int64_t K, int in_dtype) {
-  const int64_t a = in_dtype == TH_F32 ? 4 : 8;
+  const int64_t a = in_dtype == TH_F32 ? 4 : in_dtype == TH_F8E4M3 ? 32 : 8;  // whole 16-byte loads / 32-K chunks
   return (K + a - 1) / a * a;
 }
+
+static int elem_bytes(int dtype) { return dtype == TH_F32 ? 4 : dtype == TH_F8E4M3 ? 1 : 2; }
+static bool gemm_in_ok(int d) { return d == TH_BF16 || d == TH_F32 || d == TH_F8E4M3; }
 
 static bool aligned(const void* p, int bytes) { return ((uintptr_t)p % bytes) == 0; }
 
@@ -1100,10 +1104,17 @@ extern "C" int th_gemm_acc_tile(int64_t N, int32_t n_acc, int32_t in_dtype) {
 
 extern "C" int64_t th_gemm_packed_bytes(int64_t N, int64_t K, int32_t n_acc, int32_t in_dtype) {
   if (N <= 0 || K <= 0 || n_acc < 1 || n_acc > TH_MAX_ACC) return -1;
-  if (in_dtype != TH_BF16 && in_dtype != TH_F32) return -1;
+  if (!gemm_in_ok(in_dtype)) return -1;
   const int bn = choose_bn(N, n_acc, in_dtype);
   const int64_t rows = cdiv(N, bn) * bn * n_acc;
-  return rows * packed_kp(K, in_dtype) * (in_dtype == TH_F32 ? 4 : 2);
+  return rows * packed_kp(K, in_dtype) * elem_bytes(in_dtype);
+}
+
+extern "C" int64_t th_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t n_acc, int32_t in_dtype) {
+  if (M <= 0 || N <= 0 || K <= 0 || n_acc < 1 || n_acc > TH_MAX_ACC || !gemm_in_ok(in_dtype)) return -1;
+  if (in_dtype != TH_F8E4M3) return 0;
+  const int bn = choose_bn(N, n_acc, in_dtype);
+  return fp8_workspace_bytes(M, cdiv(N, bn) * bn * n_acc, K);
 }
 
 extern "C" int th_gemm_pack_rhs(const void* const* src, const int64_t* ld_src, int32_t src_dtype,
@@ -1112,8 +1123,9 @@ extern "C" int th_gemm_pack_rhs(const void* const* src, const int64_t* ld_src, i
   TH_CHECK_ARG(src && ld_src && packed, "th_gemm_pack_rhs: null pointer argument");
   TH_CHECK_ARG(N > 0 && K > 0, "th_gemm_pack_rhs: N=%lld K=%lld must be positive", (long long)N, (long long)K);
   TH_CHECK_ARG(n_acc >= 1 && n_acc <= TH_MAX_ACC, "th_gemm_pack_rhs: n_acc=%d out of range", n_acc);
-  TH_CHECK_ARG(in_dtype == TH_BF16 || in_dtype == TH_F32, "th_gemm_pack_rhs: in_dtype %d unsupported", in_dtype);
-  TH_CHECK_ARG(src_dtype == TH_BF16 || src_dtype == TH_F32, "th_gemm_pack_rhs: src_dtype %d unsupported", src_dtype);
+  TH_CHECK_ARG(gemm_in_ok(in_dtype), "th_gemm_pack_rhs: in_dtype %d unsupported", in_dtype);
+  TH_CHECK_ARG(in_dtype == TH_F8E4M3 ? src_dtype == TH_F8E4M3 : (src_dtype == TH_BF16 || src_dtype == TH_F32),
+               "th_gemm_pack_rhs: src_dtype %d does not fit in_dtype %d", src_dtype, in_dtype);
   PackK p{};
   for (int i = 0; i < n_acc; ++i) {
     TH_CHECK_ARG(src[i] != nullptr, "th_gemm_pack_rhs: src[%d] is null", i);
@@ -1135,7 +1147,11 @@ extern "C" int th_gemm_pack_rhs(const void* const* src, const int64_t* ld_src, i
   p.rows = cdiv(N, p.bn) * p.bnc;
   p.out = packed;
   dim3 grid((unsigned)cdiv(p.Kp, 32), (unsigned)cdiv(p.rows, 32));
-  hipLaunchKernelGGL(pack_rhs_kernel, grid, dim3(256), 0, (hipStream_t)stream, p);
+  if (in_dtype == TH_F8E4M3)
+    hipLaunchKernelGGL(pack_rhs_fp8_kernel, dim3((unsigned)cdiv((p.rows / 32) * (p.Kp / 32) * 64, 256)), dim3(256), 0,
+                       (hipStream_t)stream, p);
+  else
+    hipLaunchKernelGGL(pack_rhs_kernel, grid, dim3(256), 0, (hipStream_t)stream, p);
   TH_CHECK_LAUNCH();
   return TH_OK;
 }
@@ -1195,8 +1211,14 @@ extern "C" int th_gemm(const th_gemm_desc* d, void* stream) {
   TH_CHECK_ARG(d->M > 0 && d->N > 0 && d->K > 0, "th_gemm: M=%lld N=%lld K=%lld must be positive",
                (long long)d->M, (long long)d->N, (long long)d->K);
   TH_CHECK_ARG(d->n_acc >= 1 && d->n_acc <= TH_MAX_ACC, "th_gemm: n_acc=%d out of range 1..%d", d->n_acc, TH_MAX_ACC);
-  TH_CHECK_ARG(d->in_dtype == TH_BF16 || d->in_dtype == TH_F32, "th_gemm: in_dtype %d unsupported", d->in_dtype);
+  TH_CHECK_ARG(gemm_in_ok(d->in_dtype), "th_gemm: in_dtype %d unsupported", d->in_dtype);
   TH_CHECK_ARG(d->lhs && d->rhs_packed, "th_gemm: null lhs or rhs_packed");
+  const bool fp8 = d->in_dtype == TH_F8E4M3;
+  if (fp8) {
+    TH_CHECK_ARG(d->M <= 128, "th_gemm: fp8 weights are for at most 128 rows (got M=%lld)", (long long)d->M);
+    TH_CHECK_ARG(d->K % 32 == 0, "th_gemm: fp8 weights need K %% 32 == 0 (K=%lld)", (long long)d->K);
+    TH_CHECK_ARG(d->rhs_scale != nullptr, "th_gemm: fp8 weights need rhs_scale");
+  }
   const int align = d->in_dtype == TH_F32 ? 4 : 8;
   TH_CHECK_ARG(d->K % align == 0, "th_gemm: K=%lld must be a multiple of %d", (long long)d->K, align);
   TH_CHECK_ARG(d->ld_lhs >= d->K && d->ld_lhs % align == 0, "th_gemm: ld_lhs=%lld invalid", (long long)d->ld_lhs);
@@ -1277,6 +1299,10 @@ extern "C" int th_gemm(const th_gemm_desc* d, void* stream) {
   hipStream_t s = (hipStream_t)stream;
   const int bnc = bn * d->n_acc;
   k.tiles_n = (int)cdiv(d->N, bn);
+  if (fp8) {
+    k.tiles_m = 1;
+    return launch_gemm_fp8(k, cdiv(d->N, bn) * bnc, d->rhs_scale, d->workspace, d->workspace_bytes, s);
+  }
   if (d->in_dtype == TH_F32) {
     k.tiles_m = (int)cdiv(d->M, 64);
     switch (bnc) {

@@ -13,7 +13,7 @@ from pathlib import Path
 
 from .build import LIB_PATH
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 # th_status
 TH_OK = 0
@@ -60,6 +60,7 @@ class GemmDesc(C.Structure):
         ("rope_head_dim", _i32), ("rope_period", _i32), ("n_out", _i32), ("pad2_", _i32),
         ("out", EpiOut * MAX_OUT),
         ("sumsq_out", _p),
+        ("rhs_scale", _p), ("workspace", _p), ("workspace_bytes", _i64),
     ]
 
 
@@ -78,6 +79,18 @@ class AttnDesc(C.Structure):
         ("head_dim", _i32), ("scale", C.c_float), ("causal", _i32), ("dtype", _i32), ("pad_", _i32),
         ("q", _p), ("ld_q", _i64), ("k", _p), ("ld_k", _i64), ("v", _p), ("ld_v", _i64),
         ("o", _p), ("ld_o", _i64),
+    ]
+
+
+class DecodeDesc(C.Structure):
+    _fields_ = [
+        ("batch", _i32), ("heads_q", _i32), ("heads_kv", _i32), ("head_dim", _i32),
+        ("max_len", _i32), ("n_split", _i32), ("fixed_len", _i32), ("dtype", _i32),
+        ("scale", C.c_float), ("pad_", _i32), ("lengths", _p),
+        ("q", _p), ("ld_q", _i64),
+        ("k_cache", _p), ("k_stride_b", _i64), ("k_stride_t", _i64),
+        ("v_cache", _p), ("v_stride_b", _i64), ("v_stride_t", _i64),
+        ("o", _p), ("ld_o", _i64), ("workspace", _p), ("workspace_bytes", _i64),
     ]
 
 
@@ -130,9 +143,12 @@ SIGNATURES: dict[str, tuple] = {
     "th_gemm_acc_tile": (_i32, [_i64, _i32, _i32]),
     "th_gemm_packed_bytes": (_i64, [_i64, _i64, _i32, _i32]),
     "th_gemm_pack_rhs": (_i32, [C.POINTER(_p), C.POINTER(_i64), _i32, _i64, _i64, _i32, _i32, _p, _p]),
+    "th_gemm_workspace_bytes": (_i64, [_i64, _i64, _i64, _i32, _i32]),
     "th_gemm": (_i32, [C.POINTER(GemmDesc), _p]),
     "th_rmsnorm": (_i32, [C.POINTER(RmsNormDesc), _p]),
     "th_attention_prefill": (_i32, [C.POINTER(AttnDesc), _p]),
+    "th_attention_decode_workspace_bytes": (_i64, [_i32, _i32, _i32, _i32, _i32, _i32]),
+    "th_attention_decode": (_i32, [C.POINTER(DecodeDesc), _p]),
     "th_epilogue_vm": (_i32, [C.POINTER(VmDesc), _p]),
     "th_ssd_workspace_bytes": (_i64, [_i32, _i32, _i32, _i32, _i32, _i32]),
     "th_ssd_chunked": (_i32, [C.POINTER(SsdDesc), _p]),

@@ -16,7 +16,8 @@ import torch
 
 from . import abi
 
-_DT = {torch.float32: abi.TH_F32, torch.bfloat16: abi.TH_BF16, torch.float16: abi.TH_F16}
+_DT = {torch.float32: abi.TH_F32, torch.bfloat16: abi.TH_BF16, torch.float16: abi.TH_F16,
+       torch.float8_e4m3fn: abi.TH_F8E4M3}
 
 
 def th_dtype(t: torch.Tensor | torch.dtype) -> int:
@@ -99,11 +100,22 @@ class GemmCall:
     rope_head_dim: int = 0
     rope_period: int = 0
     sumsq_out: torch.Tensor | None = None
+    in_dtype: torch.dtype | None = None        # torch.float8_e4m3fn: bf16 lhs x e4m3 packed rhs
+    rhs_scale: torch.Tensor | None = None      # fp8: [n_acc, N] fp32 per-column scales
+    workspace: torch.Tensor | None = None      # fp8: gemm_workspace_bytes(...) bytes
 
     def descriptor(self) -> abi.GemmDesc:
         d = abi.GemmDesc()
         d.M, d.N, d.K, d.n_acc = self.M, self.N, self.K, self.n_acc
-        d.in_dtype = th_dtype(self.lhs)
+        d.in_dtype = th_dtype(self.in_dtype if self.in_dtype is not None else self.lhs)
+        if self.rhs_scale is not None:
+            if self.rhs_scale.dtype != torch.float32 or not self.rhs_scale.is_contiguous() \
+                    or self.rhs_scale.numel() != self.n_acc * self.N:
+                raise abi.HipBackendError("th_gemm", abi.TH_ERR_INVALID, "rhs_scale must be contiguous fp32 [n_acc, N]")
+            d.rhs_scale = self.rhs_scale.data_ptr()
+        if self.workspace is not None:
+            d.workspace = self.workspace.data_ptr()
+            d.workspace_bytes = self.workspace.numel() * self.workspace.element_size()
         d.lhs = self.lhs.data_ptr()
         d.ld_lhs = _row_major(self.lhs, "th_gemm lhs")
         d.rhs_packed = self.packed.data_ptr()
@@ -128,6 +140,13 @@ class GemmCall:
         if self.sumsq_out is not None:
             d.sumsq_out = self.sumsq_out.data_ptr()
         return d
+
+
+def gemm_workspace_bytes(M: int, N: int, K: int, n_acc: int, in_dtype: torch.dtype) -> int:
+    n = abi.load().th_gemm_workspace_bytes(M, N, K, n_acc, th_dtype(in_dtype))
+    if n < 0:
+        raise abi.HipBackendError("th_gemm_workspace_bytes", abi.TH_ERR_INVALID, f"M={M} N={N} K={K} n_acc={n_acc}")
+    return int(n)
 
 
 def gemm(call: GemmCall, kernel: str | None = None) -> None:
@@ -171,6 +190,44 @@ def attention_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: to
     d.v, d.ld_v = v.data_ptr(), _row_major(v, "attention v")
     d.o, d.ld_o = out.data_ptr(), _row_major(out, "attention o")
     abi.check(lib.th_attention_prefill(C.byref(d), _stream(q)), "th_attention_prefill", kernel)
+    return out
+
+
+def attention_decode_workspace_bytes(batch: int, heads_q: int, heads_kv: int, head_dim: int, max_len: int,
+                                     n_split: int = 0) -> int:
+    n = abi.load().th_attention_decode_workspace_bytes(batch, heads_q, heads_kv, head_dim, max_len, n_split)
+    if n < 0:
+        raise abi.HipBackendError("th_attention_decode_workspace_bytes", abi.TH_ERR_INVALID, "bad sizes")
+    return int(n)
+
+
+def attention_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, out: torch.Tensor, *,
+                     scale: float, lengths: torch.Tensor | None = None, fixed_len: int = 0, n_split: int = 0,
+                     workspace: torch.Tensor | None = None, kernel: str | None = None) -> torch.Tensor:
+    """One query token per sequence against a [batch, max_len, heads_kv, head_dim] KV cache.
+
+    ``q``/``out``: [batch, heads_q*head_dim]; ``lengths``: optional int32 [batch] on the device."""
+    lib = _lib(q)
+    B, max_len, hkv, hd = k_cache.shape
+    if v_cache.shape != k_cache.shape:
+        raise abi.HipBackendError("th_attention_decode", abi.TH_ERR_INVALID, "k and v caches differ in shape")
+    for t in (k_cache, v_cache):
+        if t.stride(3) != 1 or t.stride(2) != hd:
+            raise abi.HipBackendError("th_attention_decode", abi.TH_ERR_INVALID, "cache rows must be [heads_kv][head_dim] contiguous")
+    d = abi.DecodeDesc()
+    d.batch, d.heads_q, d.heads_kv, d.head_dim = B, q.shape[1] // hd, hkv, hd
+    d.max_len, d.n_split, d.fixed_len, d.dtype, d.scale = max_len, n_split, fixed_len, th_dtype(q), scale
+    if lengths is not None:
+        if lengths.dtype != torch.int32 or lengths.device != q.device:
+            raise abi.HipBackendError("th_attention_decode", abi.TH_ERR_INVALID, "lengths must be int32 on the device")
+        d.lengths = lengths.data_ptr()
+    d.q, d.ld_q = q.data_ptr(), _row_major(q, "decode q")
+    d.k_cache, d.k_stride_b, d.k_stride_t = k_cache.data_ptr(), k_cache.stride(0), k_cache.stride(1)
+    d.v_cache, d.v_stride_b, d.v_stride_t = v_cache.data_ptr(), v_cache.stride(0), v_cache.stride(1)
+    d.o, d.ld_o = out.data_ptr(), _row_major(out, "decode o")
+    if workspace is not None:
+        d.workspace, d.workspace_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
+    abi.check(lib.th_attention_decode(C.byref(d), _stream(q)), "th_attention_decode", kernel)
     return out
 
 
