@@ -108,6 +108,62 @@ def bench_mamba_c2(args) -> dict:
                        "chunk": cfg.chunk, "conv": cfg.d_conv}}
 
 
+def bench_decode_c5(args) -> dict:
+    """Llama-3-8B-shaped decode step with e4m3 weights: batch 64, KV cache 4096."""
+    import math
+
+    import torch
+    from oracle.llama import decode_step
+    from targets.llama_block import build_llama_block, config_c5
+    from torch_helion.hip.decode import DecodeBlock
+
+    log("Llama-3-8B decode step, e4m3 weights (config 4)")
+    cfg = config_c5()
+    pos = cfg.seq - 1
+    model = build_llama_block(cfg, seed=0)
+    sd = {k: v for k, v in model.state_dict().items() if not k.startswith(("rope", "attn_bias"))}
+    del model
+    dev = torch.device("cuda", 0)
+    blk = DecodeBlock(sd, hidden=cfg.hidden, heads=cfg.heads, kv_heads=cfg.n_kv, intermediate=cfg.intermediate,
+                      eps=cfg.eps, rope_theta=cfg.rope_theta, batch=cfg.batch, max_len=cfg.seq, device=dev)
+    g = torch.Generator(device=dev).manual_seed(0)
+    blk.k_cache.normal_(generator=g)
+    blk.v_cache.normal_(generator=g)
+    x = torch.randn(cfg.batch, cfg.hidden, generator=g, device=dev).bfloat16()
+    kc, vc = blk.k_cache.cpu(), blk.v_cache.cpu()  # positions < pos, for the parity check
+    blk.capture(x, pos)
+    for _ in range(args.warmup):
+        blk.replay()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    for i in range(args.steps):
+        starts[i].record(stream)
+        blk.replay()
+        ends[i].record(stream)
+    torch.cuda.synchronize()
+    times = sorted(s.elapsed_time(e) * 1e3 for s, e in zip(starts, ends))
+    us = times[len(times) // 2]
+    nbytes = blk.bytes_per_step(pos)
+    # one step's output vs the oracle (fp32, same folded e4m3 weights)
+    blk.step(x, pos)
+    torch.cuda.synchronize()
+    out = blk.out32.cpu().double()
+    ref = decode_step(x.cpu(), blk.effective_weights(), kc, vc, pos, heads=cfg.heads, kv_heads=cfg.n_kv, eps=cfg.eps,
+                      theta=cfg.rope_theta, dtype=torch.float32)[0].double()
+    rel = ((out - ref).abs().max() / ref.abs().max()).item()
+    return {"us": us, "tokens_per_s": cfg.batch / (us * 1e-6), "us_p10": times[max(0, len(times) // 10 - 1)],
+            "us_p90": times[min(len(times) - 1, 9 * len(times) // 10)],
+            "roofline": {"bound": "hbm", "achieved": nbytes / (us * 1e-6) / 1e9, "peak": 8000.0, "unit": "GB/s",
+                         "frac": nbytes / (us * 1e-6) / 1e9 / 8000.0, "bytes_per_step": nbytes},
+            "parity": {"max_rel_err": rel, "max_abs_err": (out - ref).abs().max().item(), "tolerance": 2e-2,
+                       "ok": rel < 2e-2, "against": "oracle.llama.decode_step fp32 on the folded e4m3 weights"},
+            "config": {"workload": "llama3-8b-block-decode-fp8", "batch": cfg.batch, "kv_len": pos,
+                       "d_model": cfg.hidden, "heads": cfg.heads, "kv_heads": cfg.n_kv, "ffn": cfg.intermediate,
+                       "weights": "e4m3, per-output-channel fp32 scales", "kv_cache": "bf16"}}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -115,6 +171,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-mamba", action="store_true", help="skip the Mamba-2 layer (config 1) line")
+    ap.add_argument("--no-decode", action="store_true", help="skip the fp8 decode-step (config 4) line")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU; --gpus must be 1 (see DESIGN.md for how the block would shard)"}))
@@ -163,6 +220,8 @@ def main() -> int:
     }
     if not args.no_mamba:
         line["mamba2_layer"] = bench_mamba_c2(args)
+    if not args.no_decode:
+        line["llama3_8b_decode_fp8"] = bench_decode_c5(args)
     if not args.no_cpu_baseline:
         log("cpu baseline: oracle fp32 forward of one sequence on the host")
         base, parity = cpu_baseline(model, cfg, x, out_gpu)

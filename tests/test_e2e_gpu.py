@@ -173,3 +173,49 @@ def test_graph_replays_match_eager(gpu, tmp_path, which):
         for g, r in zip(got, ref):
             assert torch.equal(g, r), (which, i)
         eager(x2 if i % 2 else x1)  # ordinary eager work between replays
+
+
+def _decode_case(cfg, pos, seed):
+    from targets.llama_block import build_llama_block
+
+    torch.manual_seed(seed)
+    m = build_llama_block(cfg, seed=seed)
+    sd = {k: v for k, v in m.state_dict().items() if not k.startswith(("rope", "attn_bias"))}
+    g = torch.Generator().manual_seed(seed + 1)
+    x = torch.randn(cfg.batch, cfg.hidden, generator=g).bfloat16()
+    kc = torch.randn(cfg.batch, cfg.seq, cfg.n_kv, cfg.head_dim, generator=g).bfloat16()
+    vc = torch.randn(cfg.batch, cfg.seq, cfg.n_kv, cfg.head_dim, generator=g).bfloat16()
+    return sd, x, kc, vc
+
+
+@pytest.mark.parametrize("which", ["small", "c5"])
+def test_decode_step_fp8_vs_oracle(gpu, which):
+    """Decode step with e4m3 weights: the block output and the cache entries it writes at ``pos``
+    against the oracle's decode step on the same (folded, dequantised) weights in fp32."""
+    from oracle.llama import decode_step
+    from targets.llama_block import LlamaBlockConfig, config_c5
+    from torch_helion.hip.decode import DecodeBlock
+
+    if which == "c5":
+        cfg, pos = config_c5(), 4096
+    else:
+        cfg, pos = LlamaBlockConfig(batch=4, seq=80, hidden=256, heads=4, kv_heads=2, intermediate=512, causal=True,
+                                    dtype=torch.bfloat16, rope_theta=500000.0), 77
+    announce(f"e2e decode fp8 {which} pos={pos}")
+    sd, x, kc, vc = _decode_case(cfg, pos, seed=3)
+    blk = DecodeBlock(sd, hidden=cfg.hidden, heads=cfg.heads, kv_heads=cfg.n_kv, intermediate=cfg.intermediate,
+                      eps=cfg.eps, rope_theta=cfg.rope_theta, batch=cfg.batch, max_len=cfg.seq, device=gpu)
+    blk.k_cache.copy_(kc.to(gpu))
+    blk.v_cache.copy_(vc.to(gpu))
+    blk.step(x.to(gpu), pos)
+    torch.cuda.synchronize()
+    out = blk.out32.cpu().double()
+    ref, kn, vn = decode_step(x, blk.effective_weights(), kc, vc, pos, heads=cfg.heads, kv_heads=cfg.n_kv,
+                              eps=cfg.eps, theta=cfg.rope_theta, dtype=torch.float32)
+    ref = ref.double()
+    rel = ((out - ref).abs().max() / ref.abs().max()).item()
+    assert rel < 2e-2, rel
+    assert (blk.k_cache[:, pos].float().cpu() - kn).abs().max().item() < 2e-2
+    assert (blk.v_cache[:, pos].float().cpu() - vn).abs().max().item() < 2e-2
+    # positions before pos are untouched
+    assert torch.equal(blk.k_cache[:, :pos].cpu(), kc[:, :pos])

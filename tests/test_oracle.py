@@ -170,3 +170,27 @@ def test_oracle_conv_matches_torch_conv1d():
     xb = x.reshape(bs, s, c).transpose(1, 2)
     ref = F.silu(F.conv1d(F.pad(xb, (k - 1, 0)), w.unsqueeze(1), groups=c)).transpose(1, 2).reshape(bs * s, c)
     assert torch.allclose(y, ref, atol=1e-12)
+
+
+def test_decode_step_matches_causal_prefill_row_by_row():
+    """Decoding tokens 0..S-1 one at a time, each against the cache of the earlier ones,
+    reproduces every row of the causal prefill block (GQA, RoPE), and a wrong cache position fails."""
+    from oracle.llama import block_forward, decode_step
+    from targets.llama_block import LlamaBlockConfig, build_llama_block
+
+    cfg = LlamaBlockConfig(batch=2, seq=12, hidden=64, heads=4, kv_heads=2, intermediate=96, causal=True,
+                           dtype=torch.float64, rope_theta=500000.0)
+    m = build_llama_block(cfg, seed=4)
+    x = m.example_inputs(seed=5)[0]
+    w = {k: v for k, v in m.state_dict().items() if not k.startswith(("rope", "attn_bias"))}
+    kw = dict(heads=cfg.heads, kv_heads=cfg.n_kv, eps=cfg.eps, theta=cfg.rope_theta)
+    ref = block_forward(x, w, causal=True, **kw)
+    hd = cfg.head_dim
+    kc = torch.zeros(cfg.batch, cfg.seq, cfg.n_kv, hd, dtype=torch.float64)
+    vc = torch.zeros_like(kc)
+    for t in range(cfg.seq):
+        out, kn, vn = decode_step(x[:, t], w, kc, vc, t, **kw)
+        assert (out - ref[:, t]).abs().max() < 1e-12, t
+        kc[:, t], vc[:, t] = kn, vn
+    bad, _, _ = decode_step(x[:, 5], w, kc, vc, 4, **kw)  # planted: cache position off by one
+    assert (bad - ref[:, 5]).abs().max() > 1e-3

@@ -178,3 +178,11 @@ def config_c1() -> LlamaBlockConfig:
 def config_c3() -> LlamaBlockConfig:
     return LlamaBlockConfig(batch=8, seq=2048, hidden=4096, heads=32, kv_heads=8, intermediate=14336, eps=1e-5,
                             rope_theta=500000.0, dtype=torch.bfloat16, causal=True)
+
+
+def config_c5() -> LlamaBlockConfig:
+    """BASELINE config 4 (C5): Llama-3-8B-shaped decode step, batch 64, KV cache 4096 per
+    sequence (the new token is position 4096), 32 q / 8 kv heads x 128, FFN 14336;
+    ``seq`` is the cache capacity including the new token."""
+    return LlamaBlockConfig(batch=64, seq=4097, hidden=4096, heads=32, kv_heads=8, intermediate=14336, eps=1e-5,
+                            rope_theta=500000.0, dtype=torch.bfloat16, causal=True)

@@ -1,0 +1,176 @@
+"""Decode step of a Llama block on the HIP backend: one new token per sequence,
+e4m3 weights with per-output-channel scales, a bf16 KV cache.
+
+The reference has no decode path (its models/llama_block.py:82-105 has no KV
+cache and its OpGraph no fp8 type); this runner is the decode configuration of
+the BASELINE (Llama-3-8B-shaped block, batch 64, cache 4096) built from the same
+kernel library. A step is six launches:
+
+  k0  th_gemm e4m3   q = rope_pos((x r) Wq'),       r = RMS row scale, Wq' = diag(g1) Wq
+  k1  th_gemm e4m3   k = rope_pos((x r) Wk'), v = (x r) Wv'  written straight into
+                     the caches at position ``pos`` (the output row stride is the
+                     cache's sequence stride)
+  k2  th_attention_decode over keys 0..pos
+  k3  th_gemm e4m3   x1 = x + attn Wo
+  k4  th_gemm e4m3   act = silu((x1 r2) Wg') * ((x1 r2) Wu'),  Wg' = diag(g2) Wg
+  k5  th_gemm e4m3   out = x1 + act Wd
+
+The norm gains are folded into the weights before quantisation (the same fold
+the prefill pipeline makes, reference optimizer/param_transforms.py:18-20), so
+the step computes exactly the block with weights ``effective_weights()``.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+
+from . import abi, ops
+
+_FP8 = torch.float8_e4m3fn
+_E4M3_MAX = 448.0
+
+
+def quantize_e4m3(w_kn: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Per-output-channel e4m3 quantisation of a [K, N] weight:
+    s[n] = max_k |w[k, n]| / 448, q = e4m3(w / s)."""
+    w = w_kn.float()
+    s = (w.abs().amax(0).clamp_min(1e-30) / _E4M3_MAX).float()
+    return (w / s).to(_FP8), s
+
+
+@dataclass
+class _Proj:
+    packed: torch.Tensor
+    scale: torch.Tensor   # [n_acc, N] fp32
+    n: int
+    k: int
+    n_acc: int
+
+
+class DecodeBlock:
+    """A Llama block's weights in e4m3 on the device, its KV cache and the step launches."""
+
+    def __init__(self, state_dict: dict[str, torch.Tensor], *, hidden: int, heads: int, kv_heads: int,
+                 intermediate: int, eps: float, rope_theta: float, batch: int, max_len: int,
+                 device: int | torch.device = 0) -> None:
+        self.device = torch.device("cuda", device) if isinstance(device, int) else torch.device(device)
+        if self.device.type != "cuda":
+            raise abi.HipBackendError("DecodeBlock", abi.TH_ERR_INVALID, f"device {device} is not a HIP device")
+        abi.init_device(self.device.index or 0)
+        self.D, self.H, self.Hkv, self.F = hidden, heads, kv_heads, intermediate
+        self.hd = hidden // heads
+        self.eps, self.theta = eps, rope_theta
+        self.B, self.max_len = batch, max_len
+        sd = {k: v.detach().float().cpu() for k, v in state_dict.items()}
+        g1, g2 = sd["input_norm.weight"], sd["post_norm.weight"]
+
+        def folded(name: str, gain: torch.Tensor | None) -> torch.Tensor:
+            w = sd[name].T.contiguous()                     # nn.Linear [out, in] -> [K, N]
+            return w * gain[:, None] if gain is not None else w
+
+        self._eff: dict[str, torch.Tensor] = {}
+
+        def proj(names: list[str], gain: torch.Tensor | None) -> _Proj:
+            qs = [quantize_e4m3(folded(n, gain)) for n in names]
+            for n, (q, s) in zip(names, qs):
+                self._eff[n] = (q.float() * s[None, :]).T.contiguous()   # [out, in], what the step multiplies by
+            k_, n_ = qs[0][0].shape
+            packed = ops.pack_rhs([q.to(self.device) for q, _ in qs], _FP8)
+            scale = torch.stack([s for _, s in qs]).to(self.device).contiguous()
+            return _Proj(packed, scale, n_, k_, len(names))
+
+        self.wq = proj(["attn.q_proj.weight"], g1)
+        self.wkv = proj(["attn.k_proj.weight", "attn.v_proj.weight"], g1)
+        self.wo = proj(["attn.o_proj.weight"], None)
+        self.wgu = proj(["mlp.gate_proj.weight", "mlp.up_proj.weight"], g2)
+        self.wd = proj(["mlp.down_proj.weight"], None)
+
+        dev, B = self.device, batch
+        bf = torch.bfloat16
+        self.k_cache = torch.zeros(B, max_len, kv_heads, self.hd, dtype=bf, device=dev)
+        self.v_cache = torch.zeros_like(self.k_cache)
+        self.q = torch.empty(B, heads * self.hd, dtype=bf, device=dev)
+        self.attn = torch.empty_like(self.q)
+        self.x1 = torch.empty(B, hidden, dtype=bf, device=dev)
+        self.x1_32 = torch.empty(B, hidden, device=dev)
+        self.act = torch.empty(B, intermediate, dtype=bf, device=dev)
+        self.out = torch.empty(B, hidden, dtype=bf, device=dev)
+        self.out32 = torch.empty(B, hidden, device=dev)
+        inv = 1.0 / (rope_theta ** (torch.arange(0, self.hd, 2, dtype=torch.float64) / self.hd))
+        ang = torch.outer(torch.arange(max_len, dtype=torch.float64), inv)
+        ang = torch.cat([ang, ang], -1)
+        self.cos = ang.cos().float().to(dev).contiguous()
+        self.sin = ang.sin().float().to(dev).contiguous()
+        ws = max(ops.gemm_workspace_bytes(B, p.n, p.k, p.n_acc, _FP8) for p in (self.wq, self.wkv, self.wo, self.wgu, self.wd))
+        self.gemm_ws = torch.empty(max(ws, 16), dtype=torch.uint8, device=dev)
+        self.graph: torch.cuda.CUDAGraph | None = None
+        aw = ops.attention_decode_workspace_bytes(B, heads, kv_heads, self.hd, max_len)
+        self.attn_ws = torch.empty(max(aw // 4, 1), device=dev)
+
+    # ------------------------------------------------------------------
+    def effective_weights(self) -> dict[str, torch.Tensor]:
+        """The weights the step multiplies by, as an fp32 state dict with unit norm
+        gains (the gains live inside the folded, dequantised projections)."""
+        w = dict(self._eff)
+        w["input_norm.weight"] = torch.ones(self.D)
+        w["post_norm.weight"] = torch.ones(self.D)
+        return w
+
+    def _gemm(self, p: _Proj, lhs: torch.Tensor, outs: list[ops.EpiSpec], **kw) -> None:
+        ops.gemm(ops.GemmCall(lhs.shape[0], p.n, p.k, p.n_acc, lhs, p.packed, outs, in_dtype=_FP8,
+                              rhs_scale=p.scale, workspace=self.gemm_ws, **kw))
+
+    def step(self, x: torch.Tensor, pos: int) -> torch.Tensor:
+        """One token per sequence at position ``pos`` (0 <= pos < max_len); x [batch, hidden]
+        bf16 on the device. Writes the new keys/values into the caches and returns the block
+        output [batch, hidden] (bf16; ``self.out32`` holds it in fp32)."""
+        if not 0 <= pos < self.max_len:
+            raise abi.HipBackendError("DecodeBlock.step", abi.TH_ERR_INVALID, f"pos {pos} outside the cache")
+        if x.dtype != torch.bfloat16 or tuple(x.shape) != (self.B, self.D):
+            raise abi.HipBackendError("DecodeBlock.step", abi.TH_ERR_INVALID, "x must be bf16 [batch, hidden]")
+        E = abi
+        norm = dict(sumsq=True, inv_k=1.0 / self.D, eps=self.eps)
+        rope = dict(rope_cos=self.cos[pos:pos + 1], rope_sin=self.sin[pos:pos + 1], rope_head_dim=self.hd,
+                    rope_period=1)
+        B, kvw = self.B, self.Hkv * self.hd
+        kslot = self.k_cache[:, pos].view(B, kvw)
+        vslot = self.v_cache[:, pos].view(B, kvw)
+        self._gemm(self.wq, x, [ops.EpiSpec(E.EPI_ROPE, self.q, a=0)], rscale_mask=0b1, **norm, **rope)
+        self._gemm(self.wkv, x, [ops.EpiSpec(E.EPI_ROPE, kslot, a=0), ops.EpiSpec(E.EPI_ACC, vslot, a=1)],
+                   rscale_mask=0b11, **norm, **rope)
+        ops.attention_decode(self.q, self.k_cache, self.v_cache, self.attn, scale=1.0 / math.sqrt(self.hd),
+                             fixed_len=pos + 1, workspace=self.attn_ws)
+        self._gemm(self.wo, self.attn, [ops.EpiSpec(E.EPI_ADD, self.x1, e=0), ops.EpiSpec(E.EPI_ADD, self.x1_32, e=0)],
+                   extras=[x])
+        self._gemm(self.wgu, self.x1, [ops.EpiSpec(E.EPI_SWIGLU, self.act, a=0, b=1)], rscale_mask=0b11, **norm)
+        self._gemm(self.wd, self.act, [ops.EpiSpec(E.EPI_ADD, self.out, e=0), ops.EpiSpec(E.EPI_ADD, self.out32, e=0)],
+                   extras=[self.x1_32])
+        return self.out
+
+    def capture(self, x: torch.Tensor, pos: int) -> None:
+        """Record ``step(x, pos)`` into a HIP graph (fixed input buffer and position);
+        ``replay()`` then re-runs it without host launch overhead."""
+        with torch.cuda.device(self.device):
+            torch.cuda.synchronize()
+            self.step(x, pos)
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                self.step(x, pos)
+            torch.cuda.synchronize()
+        self.graph = g
+
+    def replay(self) -> torch.Tensor:
+        self.graph.replay()
+        return self.out
+
+    def bytes_per_step(self, pos: int) -> int:
+        """HBM bytes a step must move: every weight byte and the cached keys/values it attends over."""
+        kv = 2 * self.B * (pos + 1) * self.Hkv * self.hd * 2
+        return self.weight_bytes() + kv
+
+    def weight_bytes(self) -> int:
+        return sum(p.n * p.k * p.n_acc for p in (self.wq, self.wkv, self.wo, self.wgu, self.wd))
