@@ -164,6 +164,51 @@ def bench_decode_c5(args) -> dict:
                        "weights": "e4m3, per-output-channel fp32 scales", "kv_cache": "bf16"}}
 
 
+def bench_mamba_c4(args) -> dict:
+    """Mamba-2 backbone: token ids -> embedding -> 24 layers -> final
+    RMSNorm -> tied LM head, bf16, B=8, L=2048, vocab 50280, through compile_model."""
+    import torch
+    from oracle.mamba import model_forward
+    from targets.mamba import build_mamba_model, config_c4
+    from torch_helion import CompileConfig, compile_model
+    from torch_helion.hip.bench import bench_program
+
+    log("Mamba-2 backbone, 24 layers + tied head (config 3)")
+    cfg = config_c4()
+    model = build_mamba_model(cfg, seed=0)
+    ids = model.example_inputs(seed=0)[0]
+    t0 = time.time()
+    res = compile_model(model, (ids,), CompileConfig(run_name="bench_mamba_c4", results_dir=REPO / "gpurun_out" / "results",
+                                                     backend="hip", device_check=False, reference_check=False,
+                                                     verify_passes=False, planner_mode="greedy", fp32_outputs=False))
+    log(f"compiled in {time.time() - t0:.1f} s: {len(res.program.kernels)} kernels")
+    dp = res.device_program
+    b = bench_program(dp, (ids,), res.hw, warmup=min(args.warmup, 3), reps=min(args.steps, 10))
+    us = b["us_median"]
+    by_kind: dict[str, float] = {}
+    for v in b["kernels"].values():
+        by_kind[v["kind"]] = by_kind.get(v["kind"], 0.0) + v["us"]
+    head_name = res.program.kernels[-1].name
+    head = b["kernels"][head_name]
+    # parity: logits of sequence 0's first tokens vs the float64 oracle on those tokens alone
+    prefix = 256
+    dp.run([ids])
+    torch.cuda.synchronize()
+    out = dp.outputs()[0].reshape(cfg.batch, cfg.seq, cfg.vocab)[0, :prefix].double().cpu()
+    ref = model_forward(ids[:1, :prefix], {k: v.detach() for k, v in model.state_dict().items()}, cfg)[0]
+    rel = ((out - ref).abs().max() / ref.abs().max()).item()
+    return {"us": us, "tokens_per_s": cfg.batch * cfg.seq / (us * 1e-6), "kernels": len(res.program.kernels),
+            "mfma_frac": b["total_flops"] / (us * 1e-6) / (res.hw.peak_tflops["bfloat16"] * 1e12),
+            "us_by_kind": {k: round(v, 1) for k, v in sorted(by_kind.items())},
+            "lm_head": {"kernel": head_name, "us": round(head["us"], 1), "mfma_frac": round(head["frac"], 4)},
+            "parity": {"max_rel_err": rel, "max_abs_err": (out - ref).abs().max().item(), "tolerance": 2e-2,
+                       "ok": rel < 2e-2, "against": f"oracle.mamba.model_forward float64, sequence 0, first {prefix} "
+                                                      "tokens (causal prefix), bf16 logits"},
+            "config": {"workload": "mamba2-backbone-lm", "batch": cfg.batch, "seq_len": cfg.seq, "layers": cfg.n_layers,
+                       "d_model": cfg.d_model, "heads": cfg.nheads, "head_dim": cfg.headdim, "d_state": cfg.d_state,
+                       "chunk": cfg.chunk, "vocab": cfg.vocab, "tied_head": True}}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -172,6 +217,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-mamba", action="store_true", help="skip the Mamba-2 layer (config 1) line")
     ap.add_argument("--no-decode", action="store_true", help="skip the fp8 decode-step (config 4) line")
+    ap.add_argument("--no-backbone", action="store_true", help="skip the Mamba-2 backbone (config 3) line")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU; --gpus must be 1 (see DESIGN.md for how the block would shard)"}))
@@ -222,6 +268,8 @@ def main() -> int:
         line["mamba2_layer"] = bench_mamba_c2(args)
     if not args.no_decode:
         line["llama3_8b_decode_fp8"] = bench_decode_c5(args)
+    if not args.no_backbone:
+        line["mamba2_backbone_lm"] = bench_mamba_c4(args)
     if not args.no_cpu_baseline:
         log("cpu baseline: oracle fp32 forward of one sequence on the host")
         base, parity = cpu_baseline(model, cfg, x, out_gpu)

@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define TH_ABI_VERSION 2
+#define TH_ABI_VERSION 3
 
 typedef enum th_status {
   TH_OK = 0,
@@ -271,6 +271,29 @@ typedef struct th_conv_desc {
 } th_conv_desc;
 
 int th_conv1d_causal(const th_conv_desc* desc, void* stream);
+
+/* ------------------------------------------------------- embedding kind
+ * Row gather of a token-embedding table (the `embedding` OpGraph op that
+ * the capture handler makes of aten.embedding; the reference's MambaModel
+ * has no embedding and takes float [B,S,D] hidden states,
+ * models/mamba.py:343-359):
+ *   out[t, :] = table[ids[t], :]
+ * An id outside [0, vocab) writes a row of zeros and, when n_invalid is
+ * given, adds 1 to *n_invalid (the caller zeroes it; torch raises instead).
+ */
+typedef struct th_embedding_desc {
+  int64_t tokens;                     /* number of ids */
+  int32_t dim, vocab;
+  int32_t dtype;                      /* TH_BF16 or TH_F32: table and out */
+  int32_t ids_dtype;                  /* TH_I64 or TH_I32 */
+  const void* table; int64_t ld_table;  /* [vocab, dim] */
+  const void* ids;                    /* [tokens], contiguous */
+  void* out; int64_t ld_out;          /* [tokens, dim] */
+  float* out32; int64_t ld_out32;     /* optional fp32 copy */
+  int32_t* n_invalid;                 /* optional device counter */
+} th_embedding_desc;
+
+int th_embedding(const th_embedding_desc* desc, void* stream);
 
 /* ------------------------------------------------- epilogue VM (fallback)
  * Evaluates an OpIR epilogue SSA (registered ops, reference:

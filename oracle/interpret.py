@@ -5,8 +5,10 @@ Restates the reference's codegen/interpret.py:18-77 (accumulators
 attention and scan kinds) with the op semantics of optimizer/evaluate.py:36-147,
 written independently of the product's interpreter and computing in float64
 by default. New kinds follow their defining formulas: causal / grouped-KV
-attention, ``ssd_chunked`` (the O(S) recurrence of oracle.mamba) and
-``conv1d`` (a direct sum over the kernel taps).
+attention, ``ssd_chunked`` (the O(S) recurrence of oracle.mamba),
+``conv1d`` (a direct sum over the kernel taps) and ``embedding`` (row
+indexing of the table: ``out[t] = table[ids[t]]``, what torch.nn.Embedding
+defines).
 
 ``storage="declared"`` rounds every kernel output to the dtype the Program
 declares for it, i.e. what a device that stores intermediates in their
@@ -140,6 +142,11 @@ def run_kernel(spec, env: dict[str, torch.Tensor], dtype=torch.float64) -> dict[
         vals["acc"] = ssd_chunked_program(*(args[r] for r in ("c", "b", "x", "dt", "A", "D")), spec.attrs)
     elif spec.kind == "conv1d":
         vals["acc"] = conv1d(args["x"], args["w"], spec.attrs)
+    elif spec.kind == "embedding":
+        ids = args["ids"].reshape(-1)
+        if ids.numel() and (int(ids.min()) < 0 or int(ids.max()) >= args["table"].shape[0]):
+            raise IndexError("token id outside the embedding table")
+        vals["out"] = args["table"][ids]
     else:
         raise ValueError(spec.kind)
     for a in spec.args:

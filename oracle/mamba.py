@@ -11,6 +11,11 @@
   in_proj split into z, xBC, dt; optional depthwise causal conv + SiLU on xBC;
   dt = softplus(dt + dt_bias); A = -exp(A_log); y = scan + D x; gated RMSNorm
   ``norm(y * silu(z))``; out_proj; residual; final RMSNorm for the backbone.
+* ``model_forward``: token ids -> rows of the embedding table -> backbone ->
+  logits against the same table (tied head, ``h E^T``). The reference's model
+  takes hidden states (models/mamba.py:343-359); the ids front end and the
+  tied head are the language-model form of that backbone. Pinned against the
+  eager ``nn.Embedding`` model, whose lookup and head are torch's own.
 """
 
 from __future__ import annotations
@@ -86,3 +91,25 @@ def backbone_forward(u: torch.Tensor, w: dict[str, torch.Tensor], cfg, dtype=tor
         pre = f"layers.{i}."
         u = u + mixer_forward(rms_norm(u, w[pre + "norm.weight"], cfg.eps), w, pre + "mixer.", cfg)
     return rms_norm(u, w["norm_f.weight"], cfg.eps)
+
+
+def model_forward(ids: torch.Tensor, w: dict[str, torch.Tensor], cfg, dtype=torch.float64,
+                  layers: int | None = None) -> torch.Tensor:
+    """Logits [b, s, vocab] for token ids [b, s]: ``backbone(E[ids]) @ E^T``.
+    ``layers`` keeps only the first layers (the model with fewer blocks)."""
+    table = w["embedding.weight"].to(dtype)
+    if ids.numel() and (int(ids.min()) < 0 or int(ids.max()) >= table.shape[0]):
+        raise IndexError("token id outside the embedding table")
+    u = table[ids.long()]
+    if layers is not None:
+        cfg = _with_layers(cfg, layers)
+    h = backbone_forward(u, w, cfg, dtype)
+    return h @ table.T
+
+
+def _with_layers(cfg, n: int):
+    import copy
+
+    c = copy.copy(cfg)
+    c.n_layers = n
+    return c

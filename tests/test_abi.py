@@ -45,7 +45,8 @@ def test_every_declared_symbol_is_exported_and_bound(lib):
 
 _STRUCTS = {
     "th_epi_out": "EpiOut", "th_gemm_desc": "GemmDesc", "th_rmsnorm_desc": "RmsNormDesc",
-    "th_attn_desc": "AttnDesc", "th_decode_desc": "DecodeDesc", "th_ssd_desc": "SsdDesc", "th_conv_desc": "ConvDesc", "th_vm_operand": "VmOperand", "th_vm_op": "VmOp", "th_vm_out": "VmOut",
+    "th_attn_desc": "AttnDesc", "th_decode_desc": "DecodeDesc", "th_ssd_desc": "SsdDesc", "th_conv_desc": "ConvDesc",
+    "th_embedding_desc": "EmbeddingDesc", "th_vm_operand": "VmOperand", "th_vm_op": "VmOp", "th_vm_out": "VmOut",
     "th_vm_desc": "VmDesc",
 }
 
@@ -117,7 +118,7 @@ def test_null_descriptors_are_rejected(lib):
     from torch_helion.hip import abi
 
     for fn in ("th_gemm", "th_rmsnorm", "th_attention_prefill", "th_attention_decode", "th_epilogue_vm", "th_ssd_chunked",
-               "th_conv1d_causal"):
+               "th_conv1d_causal", "th_embedding"):
         assert getattr(lib, fn)(None, None) == abi.TH_ERR_INVALID, fn
         assert "null descriptor" in abi.last_error(lib)
 
@@ -171,3 +172,25 @@ def test_fp8_gemm_validation(lib):
     assert lib.th_gemm_packed_bytes(256, 40, 1, abi.TH_F8E4M3) == 256 * 64  # K padded to 32-wide chunks
     assert lib.th_gemm_workspace_bytes(64, 4096, 4096, 1, abi.TH_BF16) == 0
     assert lib.th_gemm_workspace_bytes(64, 4096, 4096, 1, abi.TH_F8E4M3) > 0
+
+
+def test_embedding_validation(lib):
+    """Token ids are int64 or int32; strides cover the row; an empty batch is a no-op."""
+    from torch_helion.hip import abi
+
+    def desc(**over):
+        d = abi.EmbeddingDesc()
+        d.tokens, d.dim, d.vocab, d.dtype, d.ids_dtype = 16, 64, 100, abi.TH_BF16, abi.TH_I64
+        d.table, d.ld_table, d.ids, d.out, d.ld_out = 4096, 64, 8192, 12288, 64
+        for k, v in over.items():
+            setattr(d, k, v)
+        return d
+
+    for over, msg in (({"ids_dtype": abi.TH_F32}, "ids dtype"), ({"dtype": abi.TH_F16}, "dtype"),
+                      ({"ld_out": 32}, "row stride"), ({"vocab": 0}, "bad sizes"), ({"table": 0}, "null operand"),
+                      ({"out32": 4096, "ld_out32": 8}, "out32 row stride")):
+        d = desc(**over)
+        assert lib.th_embedding(C.byref(d), None) == abi.TH_ERR_INVALID, over
+        assert msg in abi.last_error(lib), (over, abi.last_error(lib))
+    d = desc(tokens=0, table=0, ids=0, out=0)
+    assert lib.th_embedding(C.byref(d), None) == abi.TH_OK

@@ -219,3 +219,57 @@ def test_decode_step_fp8_vs_oracle(gpu, which):
     assert (blk.v_cache[:, pos].float().cpu() - vn).abs().max().item() < 2e-2
     # positions before pos are untouched
     assert torch.equal(blk.k_cache[:, :pos].cpu(), kc[:, :pos])
+
+
+def _lm_check(res, model, cfg, ids, prefix: int, layers=None):
+    """Logits of the HIP program (fp32 copy) for sequence 0's first ``prefix`` tokens
+    against the oracle's model_forward in float64 on those tokens alone (the model is
+    causal, so a prefix of the output depends only on the same prefix of the input)."""
+    from oracle.mamba import model_forward
+
+    dp = res.device_program
+    dp.run([ids])
+    torch.cuda.synchronize()
+    out = dp.outputs(fp32=True)[0].reshape(cfg.batch, cfg.seq, cfg.vocab)[0, :prefix].double().cpu()
+    w = {k: v.detach() for k, v in model.state_dict().items()}
+    ref = model_forward(ids[:1, :prefix], w, cfg)[0]
+    return float((out - ref).abs().max() / ref.abs().max()), float((out - ref).abs().max())
+
+
+def test_mamba_lm_fp32_small(gpu, tmp_path):
+    """Token ids -> th_embedding -> 2 Mamba-2 layers -> tied head (vocab 1000, not a
+    multiple of 32) in fp32: 1e-4 relative to the oracle."""
+    import math
+
+    from targets.mamba import MambaConfig, build_mamba_model
+
+    announce("e2e mamba lm fp32 small")
+    cfg = MambaConfig(batch=2, seq=128, d_model=128, expand=2, headdim=32, d_state=32, chunk=64, n_layers=2, ngroups=1,
+                      use_conv=True, dtype=torch.float32, a_log_range=(0.0, math.log(16.0)), vocab=1000)
+    m = build_mamba_model(cfg, seed=0)
+    ids = m.example_inputs(seed=0)[0]
+    res = _compile(m, (ids,), tmp_path, "lm_fp32")
+    assert [l.entry for l in res.device_program.launches][0] == "th_embedding"
+    rel, _ = _lm_check(res, m, cfg, ids, cfg.seq)
+    assert rel < 1e-4, rel
+    with pytest.raises(IndexError):
+        res.device_program.set_inputs([ids.clone().fill_(cfg.vocab)])
+
+
+def test_mamba_lm_c4_shapes_two_layers(gpu, tmp_path):
+    """BASELINE config 3 (C4) at full width and length with 2 of its 24 layers and 2 of
+    its 8 sequences: d=1024, 32 heads x 64, N=128, chunk 256, vocab 50280 tied, bf16."""
+    from targets.mamba import build_mamba_model, config_c4
+    from torch_helion import CompileConfig, compile_model
+
+    announce("e2e mamba lm C4 shapes, 2 layers")
+    cfg = config_c4()
+    cfg.n_layers, cfg.batch = 2, 2
+    m = build_mamba_model(cfg, seed=0)
+    ids = m.example_inputs(seed=0)[0]
+    res = compile_model(m, (ids,), CompileConfig(run_name="lm_c4", results_dir=tmp_path, backend="hip",
+                                                 planner_mode="greedy", device_check=False))
+    kinds = [k.kind for k in res.program.kernels]
+    assert kinds[0] == "embedding" and kinds.count("ssd_chunked") == 2
+    rel, mx = _lm_check(res, m, cfg, ids, 384)
+    assert rel < 2e-2, (rel, mx)

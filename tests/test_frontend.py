@@ -192,6 +192,36 @@ def test_mamba_variants_compile(tmp_path, use_conv, ngroups):
     assert scan.attrs["ngroups"] == (ngroups or cfg.nheads)
 
 
+def test_token_id_model_compiles_with_embedding_and_tied_head(tmp_path):
+    """Token ids in, logits out: one embedding gather first, the tied head a GEMM of
+    width vocab last (with the final RMSNorm folded in), the activation dtype taken
+    from the table; the product interpreter matches the eager model and the oracle
+    interpreter (float64) matches the oracle's model_forward."""
+    import math
+
+    from oracle import interpret as oi
+    from oracle.mamba import model_forward
+    from targets.mamba import MambaConfig, build_mamba_model
+    from torch_helion import CompileConfig, compile_model
+
+    cfg = MambaConfig(batch=2, seq=64, d_model=64, expand=2, headdim=16, d_state=16, chunk=32, n_layers=2, ngroups=1,
+                      use_conv=True, dtype=torch.float32, a_log_range=(0.0, math.log(16.0)), vocab=1000)
+    m = build_mamba_model(cfg, seed=0)
+    x = m.example_inputs(seed=0)
+    res = compile_model(m, x, CompileConfig(run_name="lm", results_dir=tmp_path, backend="none", planner_mode="greedy"))
+    ks = res.program.kernels
+    assert [k.kind for k in ks].count("embedding") == 1 and ks[0].kind == "embedding"
+    assert ks[0].attrs == {"vocab": 1000, "dim": 64, "tokens": 128}
+    assert ks[-1].kind == "gemm" and ks[-1].grid["cols"] == 1000 and ks[-1].sumsq
+    assert res.program.tensors[ks[0].outputs[0].tensor].dtype == "float32"
+    assert res.reference_check["max_rel_err"] < 1e-5, res.reference_check
+    ora = oi.program_outputs(res.program, res.graph.params, list(x))[0]
+    ref = model_forward(x[0], dict(m.state_dict()), cfg)
+    assert oi.max_rel_err(ora, ref) < 1e-6  # folded constants are rounded to fp32
+    with pytest.raises(IndexError):
+        oi.program_outputs(res.program, res.graph.params, [x[0].clone().fill_(1000)])
+
+
 def test_compile_model_writes_results_layout(small_block, tmp_path):
     from torch_helion import CompileConfig, compile_model
 

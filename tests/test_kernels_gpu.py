@@ -497,3 +497,65 @@ def test_conv1d_causal(gpu, dtype):
         assert _rel(out, ref) < F32_REL
     else:
         assert _maxabs(out, ref) < BF16_TOL
+
+
+@pytest.mark.parametrize("dtype,ids_dtype,V,D,T", [
+    (torch.bfloat16, torch.int64, 50280, 1024, 16384),  # C4 lookup, 16-byte vector path
+    (torch.float32, torch.int32, 1000, 64, 333),
+    (torch.bfloat16, torch.int64, 77, 100, 129),         # 200-byte rows: element-wise path
+])
+def test_embedding_gather_exact(gpu, dtype, ids_dtype, V, D, T):
+    """out[t] = table[ids[t]] bit for bit (a copy), with and without the fp32 copy;
+    ids outside [0, V) give zero rows and are counted."""
+    from torch_helion.hip import ops
+
+    announce(f"embedding {dtype} ids {ids_dtype} V={V} D={D} T={T}")
+    g = torch.Generator().manual_seed(V + D + T)
+    table = torch.randn(V, D, generator=g).to(dtype)
+    ids = torch.randint(0, V, (T,), generator=g).to(ids_dtype)
+    ids[0], ids[-1] = 0, V - 1
+    td, idd = table.to(gpu), ids.to(gpu)
+    out = torch.full((T, D), float("nan"), dtype=dtype, device=gpu)
+    out32 = torch.full((T, D), float("nan"), device=gpu)
+    ops.embedding(td, idd, out, out32=out32)
+    torch.cuda.synchronize()
+    ref = table[ids.long()]
+    assert torch.equal(out.cpu(), ref)
+    assert torch.equal(out32.cpu(), ref.float())
+    bad = ids.clone()
+    bad[1], bad[T // 2] = -3, V
+    cnt = torch.zeros(1, dtype=torch.int32, device=gpu)
+    out.fill_(float("nan"))
+    ops.embedding(td, bad.to(gpu), out, n_invalid=cnt)
+    torch.cuda.synchronize()
+    got = out.cpu()
+    assert int(cnt.item()) == 2
+    assert torch.equal(got[1], torch.zeros(D, dtype=dtype)) and torch.equal(got[T // 2], torch.zeros(D, dtype=dtype))
+    keep = torch.ones(T, dtype=torch.bool)
+    keep[1] = keep[T // 2] = False
+    assert torch.equal(got[keep], ref[keep])
+
+
+def test_gemm_tied_lm_head_ragged_vocab(gpu):
+    """The C4 head: [T, 1024] x E^T [1024, 50280] (vocab not a multiple of 32) with the
+    final RMSNorm's row scale, bf16 and fp32 logits against a torch fp32 reference."""
+    from torch_helion.hip import abi, ops
+
+    M, N, K = 512, 50280, 1024
+    announce(f"gemm lm head M={M} N={N} K={K}")
+    g = torch.Generator().manual_seed(11)
+    h = torch.randn(M, K, generator=g).bfloat16()
+    table = (torch.randn(N, K, generator=g) * 0.02).bfloat16()
+    w = table.T.contiguous()
+    r = (h.float().pow(2).mean(-1, keepdim=True) + 1e-5).rsqrt()
+    ref = (h.float() @ w.float()) * r
+    hd = h.to(gpu)
+    packed = ops.pack_rhs([w.to(gpu)], torch.bfloat16)
+    o16 = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=gpu)
+    o32 = torch.full((M, N), float("nan"), device=gpu)
+    ops.gemm(ops.GemmCall(M, N, K, 1, hd, packed, [ops.EpiSpec(abi.EPI_ACC, o16), ops.EpiSpec(abi.EPI_ACC, o32)],
+                          sumsq=True, inv_k=1.0 / K, eps=1e-5, rscale_mask=0b1))
+    torch.cuda.synchronize()
+    assert _rel(o32, ref) < 1e-5
+    assert _maxabs(o16, ref) < BF16_TOL * max(1.0, float(ref.abs().max()))
+    assert not torch.isnan(o16).any()

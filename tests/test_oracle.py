@@ -137,6 +137,32 @@ def test_mamba_oracle_matches_module():
         assert (out - ref).abs().max() / ref.abs().max() < 1e-10, mode
 
 
+def test_mamba_oracle_model_forward_matches_embedding_module():
+    """Ids -> nn.Embedding rows -> blocks -> tied head, against the oracle (float64);
+    a wrong table orientation or a dropped final norm would fail this."""
+    from oracle.mamba import model_forward
+    from targets.mamba import MambaConfig, build_mamba_model
+
+    cfg = MambaConfig(batch=2, seq=24, d_model=32, expand=2, headdim=16, d_state=8, chunk=8, n_layers=2,
+                      ngroups=1, use_conv=True, dtype=torch.float64, a_log_range=(0.0, math.log(16.0)), vocab=97)
+    m = build_mamba_model(cfg, seed=5)
+    ids = m.example_inputs(seed=6)[0]
+    with torch.no_grad():
+        ref = m(ids)
+    out = model_forward(ids, dict(m.state_dict()), cfg)
+    assert out.shape == (2, 24, 97)
+    assert (out - ref).abs().max() / ref.abs().max() < 1e-10
+    # the first layers alone are the model with fewer blocks
+    cfg1 = MambaConfig(**{**cfg.__dict__, "n_layers": 1})
+    m1 = build_mamba_model(cfg1, seed=5)
+    m1.load_state_dict({k: v for k, v in m.state_dict().items() if not k.startswith("layers.1.")})
+    with torch.no_grad():
+        ref1 = m1(ids)
+    assert (model_forward(ids, dict(m.state_dict()), cfg, layers=1) - ref1).abs().max() < 1e-10
+    with pytest.raises(IndexError):
+        model_forward(ids.clone().fill_(-1), dict(m.state_dict()), cfg)
+
+
 def test_interpreters_agree_and_reproduce_reference_check(tmp_path):
     """The oracle interpreter (float64) and the product interpreter (float32) agree on
     the reference's default Llama program; the product one reproduces the recorded check."""

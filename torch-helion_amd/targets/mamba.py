@@ -252,4 +252,4 @@ def config_c2() -> MambaConfig:
 def config_c4() -> MambaConfig:
     return MambaConfig(batch=8, seq=2048, d_model=1024, expand=2, headdim=64, d_state=128, chunk=256, n_layers=24,
                        ngroups=1, d_conv=4, use_conv=True, dtype=torch.bfloat16, a_log_range=(0.0, math.log(16.0)),
-                       vocab=50280, mode="chunked")
+                       vocab=50280)

@@ -22,7 +22,7 @@ class CodegenError(RuntimeError):
 
 
 _ENTRY = {"gemm": "th_gemm", "attention": "th_attention_prefill", "ssd": "th_ssd_chunked",
-          "ssd_chunked": "th_ssd_chunked", "conv1d": "th_conv1d_causal"}
+          "ssd_chunked": "th_ssd_chunked", "conv1d": "th_conv1d_causal", "embedding": "th_embedding"}
 
 
 def launch_plan(spec: KernelSpec, program: Program) -> dict[str, Any]:

@@ -14,7 +14,7 @@ from ..optimizer.evaluate import eval_op
 from ..optimizer.opir import KernelSpec, Program
 
 _ROLES = {"ssd": ["c", "b", "x", "cum", "dt", "mask", "dskip"], "ssd_chunked": ["c", "b", "x", "dt", "A", "D"],
-          "conv1d": ["x", "w"]}
+          "conv1d": ["x", "w"], "embedding": ["table", "ids"]}
 
 
 def run_kernel(spec: KernelSpec, env: dict[str, torch.Tensor]) -> dict[str, torch.Tensor]:
@@ -30,6 +30,8 @@ def run_kernel(spec: KernelSpec, env: dict[str, torch.Tensor]) -> dict[str, torc
         return {spec.outputs[0].tensor: eval_op("attention", [args["q"], args["k"], args["v"]], spec.attrs)}
     elif spec.kind in _ROLES:
         vals["acc"] = eval_op(spec.kind, [args[r] for r in _ROLES[spec.kind]], spec.attrs)
+        if spec.kind == "embedding":
+            vals["out"] = vals.pop("acc").reshape(-1, spec.attrs["dim"])
     else:
         raise ValueError(spec.kind)
     for a in spec.args:

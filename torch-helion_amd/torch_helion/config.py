@@ -46,6 +46,7 @@ class CompileConfig:
     cpu_threads: int = 0                          # 0: all cores in the process affinity
     ssd_chunk: int = 0                            # 0: 64 for sequences up to 1024, else 256
     fuse_rope: bool = True
+    fp32_outputs: bool = True                     # producers of program outputs also write an fp32 copy
     cpu_flop_budget: float = 2e10                 # graphs above this skip CPU-side checks in "auto" mode
 
     @property

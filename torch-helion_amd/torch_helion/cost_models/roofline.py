@@ -150,6 +150,14 @@ def elementwise_cost(spec: KernelSpec, tensors: dict[str, TensorType], hw: Hardw
     return _compose(hw, flops, nbytes, 0.0, 0, dtype, {}, {})
 
 
+def gather_cost(spec: KernelSpec, tensors: dict[str, TensorType], hw: HardwareSpec) -> CostBreakdown:
+    """Embedding gather: only the looked-up rows of the table move (ids + rows in, rows out)."""
+    dtype = _dtype(spec, tensors)
+    out = tensors[spec.outputs[0].tensor]
+    nbytes = 2 * _bytes(out) + _bytes(tensors[spec.arg("ids").tensor])
+    return _compose(hw, 0.0, nbytes, 0.0, 0, dtype, {}, {})
+
+
 def kernel_cost(spec: KernelSpec, tensors: dict[str, TensorType], hw: HardwareSpec, tiles: dict[str, int] | None = None) -> CostBreakdown:
     if spec.kind == "gemm":
         return gemm_cost(spec, tensors, hw)
@@ -157,6 +165,8 @@ def kernel_cost(spec: KernelSpec, tensors: dict[str, TensorType], hw: HardwareSp
         return attention_cost(spec, tensors, hw)
     if spec.kind in ("ssd", "ssd_chunked"):
         return ssd_cost(spec, tensors, hw)
-    if spec.kind in ("conv1d", "embedding"):
+    if spec.kind == "conv1d":
         return elementwise_cost(spec, tensors, hw)
+    if spec.kind == "embedding":
+        return gather_cost(spec, tensors, hw)
     raise CostModelError(f"unknown kernel kind {spec.kind}")

@@ -13,7 +13,7 @@ from pathlib import Path
 
 from .build import LIB_PATH
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 # th_status
 TH_OK = 0
@@ -114,6 +114,14 @@ class ConvDesc(C.Structure):
     ]
 
 
+class EmbeddingDesc(C.Structure):
+    _fields_ = [
+        ("tokens", _i64), ("dim", _i32), ("vocab", _i32), ("dtype", _i32), ("ids_dtype", _i32),
+        ("table", _p), ("ld_table", _i64), ("ids", _p), ("out", _p), ("ld_out", _i64),
+        ("out32", _p), ("ld_out32", _i64), ("n_invalid", _p),
+    ]
+
+
 class VmOperand(C.Structure):
     _fields_ = [("ptr", _p), ("ld", _i64), ("dtype", _i32), ("column", _i32)]
 
@@ -153,6 +161,7 @@ SIGNATURES: dict[str, tuple] = {
     "th_ssd_workspace_bytes": (_i64, [_i32, _i32, _i32, _i32, _i32, _i32]),
     "th_ssd_chunked": (_i32, [C.POINTER(SsdDesc), _p]),
     "th_conv1d_causal": (_i32, [C.POINTER(ConvDesc), _p]),
+    "th_embedding": (_i32, [C.POINTER(EmbeddingDesc), _p]),
 }
 
 

@@ -17,7 +17,7 @@ import torch
 from . import abi
 
 _DT = {torch.float32: abi.TH_F32, torch.bfloat16: abi.TH_BF16, torch.float16: abi.TH_F16,
-       torch.float8_e4m3fn: abi.TH_F8E4M3}
+       torch.float8_e4m3fn: abi.TH_F8E4M3, torch.int32: abi.TH_I32, torch.int64: abi.TH_I64}
 
 
 def th_dtype(t: torch.Tensor | torch.dtype) -> int:
@@ -305,3 +305,31 @@ def conv1d_causal(x, w, out, *, batch: int, seq: int, activation: str | None, ou
     if out32 is not None:
         d.y32, d.ld_y32 = out32.data_ptr(), _row_major(out32, "conv y32")
     abi.check(lib.th_conv1d_causal(C.byref(d), _stream(x)), "th_conv1d_causal", kernel)
+
+
+def embedding(table: torch.Tensor, ids: torch.Tensor, out: torch.Tensor, *, out32: torch.Tensor | None = None,
+              n_invalid: torch.Tensor | None = None, kernel: str | None = None) -> None:
+    """out[t] = table[ids[t]] (th_embedding). Rows of ids outside [0, vocab) are
+    written as zeros and counted in ``n_invalid`` (an int32 device scalar) if given."""
+    lib = _lib(table)
+    if ids.dtype not in (torch.int64, torch.int32) or not ids.is_contiguous():
+        raise abi.HipBackendError("th_embedding", abi.TH_ERR_INVALID, "ids must be contiguous int64 or int32", kernel)
+    if out.dtype != table.dtype or out.shape[-1] != table.shape[1] or out.numel() != ids.numel() * table.shape[1]:
+        raise abi.HipBackendError("th_embedding", abi.TH_ERR_INVALID,
+                                  f"out {tuple(out.shape)} {out.dtype} does not match ids {tuple(ids.shape)} "
+                                  f"x table {tuple(table.shape)} {table.dtype}", kernel)
+    if n_invalid is not None and (n_invalid.dtype != torch.int32 or n_invalid.device != table.device):
+        raise abi.HipBackendError("th_embedding", abi.TH_ERR_INVALID, "n_invalid must be an int32 device tensor", kernel)
+    out2 = out.reshape(-1, table.shape[1]) if out.dim() != 2 else out
+    d = abi.EmbeddingDesc()
+    d.tokens, d.dim, d.vocab = ids.numel(), table.shape[1], table.shape[0]
+    d.dtype, d.ids_dtype = th_dtype(table), th_dtype(ids)
+    d.table, d.ld_table = table.data_ptr(), _row_major(table, "embedding table")
+    d.ids = ids.data_ptr()
+    d.out, d.ld_out = out2.data_ptr(), _row_major(out2, "embedding out")
+    if out32 is not None:
+        o32 = out32.reshape(-1, table.shape[1]) if out32.dim() != 2 else out32
+        d.out32, d.ld_out32 = o32.data_ptr(), _row_major(o32, "embedding out32")
+    if n_invalid is not None:
+        d.n_invalid = n_invalid.data_ptr()
+    abi.check(lib.th_embedding(C.byref(d), _stream(table)), "th_embedding", kernel)

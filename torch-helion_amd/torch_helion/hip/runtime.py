@@ -74,18 +74,26 @@ class DeviceProgram:
         # to the activation dtype only where a GEMM consumes it as its LHS.
         self.shadow: dict[str, torch.Tensor] = {}
         produced = {o.tensor for k in program.kernels for o in k.outputs}
+        # a gathered table row is exact in the table's dtype: no shadow needed
+        exact = {o.tensor for k in program.kernels if k.kind == "embedding" for o in k.outputs}
         for k in program.kernels:
             for a in k.args:
                 if (a.role == "extra" and a.tensor in produced and a.tensor not in self.shadow
-                        and self.buffers[a.tensor].dtype in (torch.bfloat16, torch.float16)):
+                        and a.tensor not in exact and self.buffers[a.tensor].dtype in (torch.bfloat16, torch.float16)):
                     self.shadow[a.tensor] = torch.empty(self.buffers[a.tensor].shape, dtype=torch.float32,
                                                         device=self.device)
         if fp32_outputs:
             # program outputs are also kept in fp32 (the epilogue computes them in
             # fp32; rounding to the declared dtype is only the storage step)
             for o in program.outputs:
-                if o in produced and o not in self.shadow and self.buffers[o].dtype in (torch.bfloat16, torch.float16):
+                if o in produced and o not in self.shadow and o not in exact and self.buffers[o].dtype in (torch.bfloat16, torch.float16):
                     self.shadow[o] = torch.empty(self.buffers[o].shape, dtype=torch.float32, device=self.device)
+        # program inputs read as token ids, with the size of the table they index
+        self._vocab: dict[str, int] = {}
+        for k in program.kernels:
+            if k.kind == "embedding" and k.arg("ids").tensor in program.inputs:
+                ids = k.arg("ids").tensor
+                self._vocab[ids] = min(self._vocab.get(ids, k.attrs["vocab"]), k.attrs["vocab"])
         for k in program.kernels:
             self.launches.extend(self._lower(k))
 
@@ -96,6 +104,11 @@ class DeviceProgram:
         for name in self.program.inputs:
             dst = self.buffers[name]
             src = inputs[name]
+            if name in self._vocab and src.numel():
+                lo, hi = int(src.min()), int(src.max())
+                if lo < 0 or hi >= self._vocab[name]:
+                    raise IndexError(f"input {name}: token id {lo if lo < 0 else hi} outside the embedding table "
+                                     f"[0, {self._vocab[name]})")
             dst.copy_(src.reshape(dst.shape).to(dst.dtype), non_blocking=True)
 
     def launch_all(self) -> None:
@@ -175,7 +188,24 @@ class DeviceProgram:
         if spec.kind == "conv1d":
             from .ssd import lower_conv1d
             return lower_conv1d(self, spec)
+        if spec.kind == "embedding":
+            return [self._lower_embedding(spec)]
         raise _err(spec.name, f"kernel kind {spec.kind!r} has no HIP kernel")
+
+    # embedding ------------------------------------------------------------
+    def _lower_embedding(self, spec: KernelSpec) -> Launch:
+        table = self.buffers[spec.arg("table").tensor]
+        ids = self.buffers[spec.arg("ids").tensor]
+        if table.dtype not in (torch.bfloat16, torch.float32):
+            raise _err(spec.name, f"embedding table dtype {table.dtype} has no kernel")
+        out = self.buffers[spec.outputs[0].tensor]
+        out32 = self.shadow.get(spec.outputs[0].tensor)
+        ids_flat = ids.reshape(-1)
+
+        def run() -> None:
+            ops.embedding(table, ids_flat, out, out32=out32, kernel=spec.name)
+
+        return Launch(spec.name, "embedding", run, "th_embedding", {"vocab": table.shape[0], "dim": table.shape[1]})
 
     # attention ------------------------------------------------------------
     def _lower_attention(self, spec: KernelSpec) -> Launch:

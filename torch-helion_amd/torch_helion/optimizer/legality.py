@@ -10,11 +10,13 @@ are the kernels' own:
 * attention: head_dim 64 or 128 (bf16), 16/32/64/128 (fp32); heads a
   multiple of kv_heads;
 * ssd / ssd_chunked: head_dim and state_dim multiples of 16, at most 128;
-* conv1d: kernel width at most 8.
+* conv1d: kernel width at most 8;
+* embedding: integer ids, a parameter table, no epilogue.
 """
 
 from __future__ import annotations
 
+import math
 from dataclasses import dataclass, field
 
 from ..capture.opgraph import TensorType
@@ -101,6 +103,15 @@ def check_kernel(spec: KernelSpec, tensors: dict[str, TensorType], report: Legal
     elif spec.kind == "conv1d":
         if spec.attrs["kernel"] > 8:
             rep.add(k, "kernel", f"conv width {spec.attrs['kernel']} > 8")
+    elif spec.kind == "embedding":
+        a = spec.attrs
+        table, ids = tensors[spec.arg("table").tensor], tensors[spec.arg("ids").tensor]
+        if ids.dtype not in ("int64", "int32"):
+            rep.add(k, "ids", f"token ids are {ids.dtype}, not int64/int32")
+        if table.shape != (a["vocab"], a["dim"]) or math.prod(ids.shape) != a["tokens"]:
+            rep.add(k, "shape", f"table {table.shape} / ids {ids.shape} do not match {a}")
+        if spec.epilogue:
+            rep.add(k, "epilogue", "an embedding gather hosts no epilogue")
     else:
         rep.add(k, "kind", f"unknown kernel kind {spec.kind}")
     return rep

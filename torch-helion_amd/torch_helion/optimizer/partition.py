@@ -2,9 +2,10 @@
 
 Anchors are reductions: a group of sibling GEMMs sharing one LHS and output
 width (the planner's grouping decides which siblings share a kernel), an
-``attention``, a scan (``ssd`` / ``ssd_chunked``), a ``conv1d``, or a
-stand-alone row sum of squares. Every other compute op joins the epilogue of
-the latest anchor whose output tile it fits; the RMS column chain
+``attention``, a scan (``ssd`` / ``ssd_chunked``), a ``conv1d``, an
+``embedding`` gather, or a stand-alone row sum of squares. Every other
+compute op joins the epilogue of the latest anchor whose output tile it
+fits (an embedding hosts no epilogue); the RMS column chain
 (``row_sumsq`` -> scalars) is cloned into each kernel that needs it. Values
 crossing kernels become DRAM tensors. Deterministic for a given grouping.
 """
@@ -64,6 +65,8 @@ def _tile_frame(k: _Kernel) -> tuple[int, int]:
         return (a["batch"] * a["seq"], a["heads"] * a["head_dim"])
     if k.spec.kind == "conv1d":
         return (a["batch"] * a["seq"], a["width"])
+    if k.spec.kind == "embedding":
+        return (a["tokens"], a["dim"])
     return (k.spec.grid["rows"], k.spec.grid["cols"])
 
 
@@ -162,6 +165,19 @@ def build_program(g: OpGraph, grouping: Grouping | None = None, name: str = "pro
             k = new_kernel(spec, n)
             k.owned[n.name] = "acc"
             owner[n.name] = k
+        elif n.op == "embedding":
+            table, ids = n.inputs
+            if g[table].kind not in ("param", "const"):
+                raise PartitionError(f"{n.name}: the embedding table must be a parameter")
+            vocab, dim = g[table].type.shape
+            spec = KernelSpec(name="embedding", kind="embedding",
+                              attrs={"vocab": vocab, "dim": dim, "tokens": n.type.shape[0]})
+            spec.args.append(KernelArg("table", table, "table"))
+            spec.args.append(KernelArg("ids", ids, "ids"))
+            spec.outputs.append(KernelOutput(n.name, "out"))
+            k = new_kernel(spec, n)
+            k.owned[n.name] = "out"
+            owner[n.name] = k
         elif n.op == "batch_matmul":
             raise PartitionError(f"{n.name}: stand-alone batch_matmul has no kernel template")
 
@@ -182,7 +198,8 @@ def build_program(g: OpGraph, grouping: Grouping | None = None, name: str = "pro
 
     # --- epilogues
     for n in g:
-        if n.kind != "compute" or n.op in ("matmul", "attention", "ssd", "ssd_chunked", "conv1d", "row_sumsq"):
+        if n.kind != "compute" or n.op in ("matmul", "attention", "ssd", "ssd_chunked", "conv1d", "embedding",
+                                               "row_sumsq"):
             continue
         if _column_source(g, n.name, memo) is not None:
             continue
@@ -207,12 +224,20 @@ def build_program(g: OpGraph, grouping: Grouping | None = None, name: str = "pro
         owner[n.name] = home
 
     # --- outputs: values read outside their kernel
+    users: dict[str, list[OpNode]] = {}
+    for n in g:
+        for i in n.inputs:
+            users.setdefault(i, []).append(n)
+    readers: dict[str, set[int]] = {}
+    for kk in kernels:
+        for a in kk.spec.args:
+            readers.setdefault(a.tensor, set()).add(id(kk))
     for value, k in list(owner.items()):
-        if k.spec.kind == "attention" or value not in k.owned:
+        if k.spec.kind in ("attention", "embedding") or value not in k.owned:
             continue
         needed = value in g.outputs or any(
-            u.name not in k.owned for u in g.users(value) if u.name in owner or u.op in ("attention", "matmul"))
-        needed = needed or any(a.tensor == value for kk in kernels if kk is not k for a in kk.spec.args)
+            u.name not in k.owned for u in users.get(value, ()) if u.name in owner or u.op in ("attention", "matmul"))
+        needed = needed or bool(readers.get(value, set()) - {id(k)})
         if needed and value not in k.spec.output_tensors():
             k.spec.outputs.append(KernelOutput(value, k.owned[value]))
 
@@ -273,17 +298,22 @@ def _clone_column(g: OpGraph, name: str, home: _Kernel, memo: dict) -> str:
 
 
 def _order_kernels(kernels: list[_Kernel]) -> list[_Kernel]:
+    """Topological order, earliest graph position first among the ready kernels
+    (kernels are compared by identity: two kernels may hold equal specs)."""
     produced = {o.tensor: k for k in kernels for o in k.spec.outputs}
     done: list[_Kernel] = []
+    done_ids: set[int] = set()
     remaining = sorted(kernels, key=lambda k: k.order_key)
     while remaining:
-        progressed = False
-        for k in list(remaining):
+        left: list[_Kernel] = []
+        for k in remaining:
             deps = [produced[a.tensor] for a in k.spec.args if a.tensor in produced and produced[a.tensor] is not k]
-            if all(d in done for d in deps):
+            if all(id(d) in done_ids for d in deps):
                 done.append(k)
-                remaining.remove(k)
-                progressed = True
-        if not progressed:
+                done_ids.add(id(k))
+            else:
+                left.append(k)
+        if len(left) == len(remaining):
             raise PartitionError("cyclic kernel dependencies")
+        remaining = left
     return done

@@ -783,7 +783,10 @@ def flatten_to_2d(g: OpGraph) -> int:
             node.attrs["shape"] = list(_twod(tuple(node.attrs["shape"])))
         node.type = TensorType(_twod(node.type.shape), node.type.dtype)
     float_inputs = [i for i in g.inputs if g[i].type.dtype not in ("int64", "int32")]
-    act = g.metadata.get("act_dtype") or (g[float_inputs[0]].type.dtype if float_inputs else "float16")
+    # a model fed token ids computes in its embedding table's dtype
+    tables = [g[n.inputs[0]].type.dtype for n in g if n.op == "embedding"]
+    act = g.metadata.get("act_dtype") or (g[float_inputs[0]].type.dtype if float_inputs else
+                                          tables[0] if tables else "float16")
     for node in g:
         if node.kind in ("param", "const", "input"):
             continue

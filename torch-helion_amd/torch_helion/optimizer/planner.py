@@ -7,6 +7,13 @@ kernel. ``exhaustive`` enumerates every set partition of each sibling set
 Each candidate is partitioned, checked for MI355X legality and costed with
 the roofline model (``us`` per kernel plus launch overhead); the cheapest
 legal candidate wins, ties broken by fewer kernels.
+
+When the product of the per-set choices exceeds ``max_candidates`` (a deep
+model: a 24-layer Mamba-2 has 48 sibling sets), the reference enumerates
+only the first 512 combinations, which never varies the early layers. Here
+such graphs are planned by coordinate descent instead: starting from the
+first option of every set, each set in turn takes whichever of its options
+lowers the program cost with the others held, so every set is decided.
 """
 
 from __future__ import annotations
@@ -68,37 +75,50 @@ def set_partitions(items: list[str]) -> list[list[list[str]]]:
     return out
 
 
-def enumerate_groupings(g: OpGraph, mode: str = "exhaustive", max_candidates: int = 512) -> list[Grouping]:
+MAX_CANDIDATES = 512
+
+
+def set_options(g: OpGraph, mode: str = "exhaustive") -> list[list[list[list[str]]]]:
+    """Per sibling set, the partitions of it the planner may choose from."""
     per_set = []
     for s in sibling_sets(g):
         if mode == "exhaustive" and len(s) <= 6:
             per_set.append(set_partitions(s))
         else:
             per_set.append([[list(s)], [[m] for m in s]] if len(s) > 1 else [[list(s)]])
+    return per_set
+
+
+def grouping_of(combo) -> Grouping:
+    grouping: Grouping = {}
+    gid = 0
+    for part in combo:
+        for block in part:
+            for m in block:
+                grouping[m] = gid
+            gid += 1
+    return grouping
+
+
+def enumerate_groupings(g: OpGraph, mode: str = "exhaustive", max_candidates: int = MAX_CANDIDATES) -> list[Grouping]:
     groupings: list[Grouping] = []
-    for combo in product(*per_set):
-        grouping: Grouping = {}
-        gid = 0
-        for part in combo:
-            for block in part:
-                for m in block:
-                    grouping[m] = gid
-                gid += 1
-        groupings.append(grouping)
+    for combo in product(*set_options(g, mode)):
+        groupings.append(grouping_of(combo))
         if len(groupings) >= max_candidates:
             break
     return groupings
 
 
 def kernel_signature(spec, tensors) -> str:
-    d = spec.to_dict()
-    for key in ("name", "tiles", "cost"):
-        d.pop(key, None)
-    d["shapes"] = {a.name: list(tensors[a.tensor].shape) for a in spec.args}
-    d["dtypes"] = {a.name: tensors[a.tensor].dtype for a in spec.args}
-    d["args"] = [[a.name, a.role, a.view] for a in spec.args]
-    d["outputs"] = [o.value for o in spec.outputs]
-    return json.dumps(d, sort_keys=True, default=str)
+    """Structural key of a kernel (its name aside) for cost memoisation."""
+    body = [(b.op, tuple(b.inputs), json.dumps(b.attrs, sort_keys=True, default=str)) for b in spec.epilogue]
+    key = (spec.kind, spec.k_extent, tuple(sorted(spec.grid.items())), spec.sumsq,
+           tuple((gm.acc, gm.rhs) for gm in spec.gemms), tuple(body),
+           json.dumps(spec.attrs, sort_keys=True, default=str),
+           tuple((a.name, a.role, tuple(a.view or ()), tuple(tensors[a.tensor].shape), tensors[a.tensor].dtype)
+                 for a in spec.args),
+           tuple(o.value for o in spec.outputs))
+    return repr(key)
 
 
 def cost_program(program: Program, hw: HardwareSpec, config=None, memo: dict[str, Any] | None = None) -> tuple[float, dict[str, float]]:
@@ -117,26 +137,52 @@ def cost_program(program: Program, hw: HardwareSpec, config=None, memo: dict[str
     return total, per
 
 
+def _evaluate(g: OpGraph, grouping: Grouping, index: int, hw: HardwareSpec, config, name: str,
+              memo: dict[str, Any]) -> Candidate:
+    try:
+        program = build_program(g, grouping, name=name)
+    except PartitionError as e:
+        return Candidate(index, grouping, None, False, float("inf"), error=str(e))
+    rep = check_program(program)
+    if not rep.ok:
+        return Candidate(index, grouping, program, False, float("inf"), violations=[str(v) for v in rep.violations])
+    try:
+        total, per = cost_program(program, hw, config, memo)
+    except CostModelError as e:
+        return Candidate(index, grouping, program, False, float("inf"), error=str(e))
+    return Candidate(index, grouping, program, True, total, per)
+
+
+def _better(a: Candidate, b: Candidate) -> bool:
+    if not a.legal:
+        return False
+    return not b.legal or (a.total_cycles, len(a.program.kernels)) < (b.total_cycles, len(b.program.kernels))
+
+
 def plan(g: OpGraph, hw: HardwareSpec, config, name: str = "program") -> PlanResult:
     mode = getattr(config, "planner_mode", "exhaustive")
     candidates: list[Candidate] = []
     memo: dict[str, Any] = {}
-    for i, grouping in enumerate(enumerate_groupings(g, mode)):
-        try:
-            program = build_program(g, grouping, name=name)
-        except PartitionError as e:
-            candidates.append(Candidate(i, grouping, None, False, float("inf"), error=str(e)))
-            continue
-        rep = check_program(program)
-        if not rep.ok:
-            candidates.append(Candidate(i, grouping, program, False, float("inf"), violations=[str(v) for v in rep.violations]))
-            continue
-        try:
-            total, per = cost_program(program, hw, config, memo)
-        except CostModelError as e:
-            candidates.append(Candidate(i, grouping, program, False, float("inf"), error=str(e)))
-            continue
-        candidates.append(Candidate(i, grouping, program, True, total, per))
+    options = set_options(g, mode)
+    n_combos = 1
+    for o in options:
+        n_combos *= len(o)
+    if n_combos <= MAX_CANDIDATES:
+        for i, grouping in enumerate(enumerate_groupings(g, mode)):
+            candidates.append(_evaluate(g, grouping, i, hw, config, name, memo))
+    else:
+        choice = [0] * len(options)
+        cur = _evaluate(g, grouping_of([o[0] for o in options]), 0, hw, config, name, memo)
+        candidates.append(cur)
+        for si, opts in enumerate(options):
+            for oi in range(1, len(opts)):
+                trial = list(choice)
+                trial[si] = oi
+                c = _evaluate(g, grouping_of([o[j] for o, j in zip(options, trial)]), len(candidates), hw, config,
+                              name, memo)
+                candidates.append(c)
+                if _better(c, cur):
+                    cur, choice = c, trial
     legal = [c for c in candidates if c.legal]
     if not legal:
         details = "\n".join(f"  candidate {c.index}: {c.error or c.violations}" for c in candidates[:10])
