@@ -423,6 +423,8 @@ def _ssd_case(bs, s, h, p, n, g, dtype, seed):
     # bf16 runs on the MFMA path: ragged length, groups, N=32, N=128 with 256-row chunks, 128- and 32-row chunks
     (1, 200, 4, 32, 32, 2, 64, torch.bfloat16), (2, 512, 2, 64, 128, 1, 256, torch.bfloat16),
     (2, 300, 4, 64, 64, 1, 128, torch.bfloat16), (1, 100, 2, 64, 64, 1, 32, torch.bfloat16),
+    (1, 300, 2, 128, 128, 1, 256, torch.bfloat16),   # 4 p-tiles per unit, ragged last chunk
+    (2, 2048, 4, 64, 128, 1, 256, torch.bfloat16),   # C4 head shape and length (4 of its 32 heads)
 ])
 def test_ssd_chunked_vs_recurrence(gpu, bs, s, h, p, n, g, chunk, dtype):
     from oracle.mamba import ssd_chunked_program
@@ -479,20 +481,28 @@ def test_ssd_reference_form_padded_cum(gpu, dtype):
         assert _maxabs(out, ref) < BF16_TOL
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_conv1d_causal(gpu, dtype):
+@pytest.mark.parametrize("dtype,bs,s,c,k,col0", [
+    (torch.float32, 2, 300, 1152, 4, 0),
+    (torch.bfloat16, 2, 300, 1152, 4, 0),     # 16-byte vector path, ragged last token run
+    (torch.bfloat16, 3, 17, 128, 4, 128),     # input is a column slice of a wider tensor (row stride 384)
+    (torch.bfloat16, 2, 40, 64, 3, 0),        # kernel width 3: element-wise path
+])
+def test_conv1d_causal(gpu, dtype, bs, s, c, k, col0):
     from oracle.interpret import conv1d
     from torch_helion.hip import ops
 
-    announce(f"conv1d {dtype}")
-    bs, s, c, k = 2, 300, 1152, 4
-    gen = torch.Generator().manual_seed(5)
-    x = torch.randn(bs * s, c, generator=gen).to(dtype)
+    announce(f"conv1d {dtype} bs={bs} s={s} c={c} k={k} col0={col0}")
+    gen = torch.Generator().manual_seed(5 + c + k)
+    wide = torch.randn(bs * s, c + 2 * col0, generator=gen).to(dtype)
+    x = wide[:, col0:col0 + c]
     w = torch.randn(c, k, generator=gen) * 0.3
     ref = conv1d(x.double(), w.double(), {"batch": bs, "seq": s, "activation": "silu"})
+    xd = wide.to(gpu)[:, col0:col0 + c]
     out = torch.empty(bs * s, c, dtype=dtype, device=gpu)
-    ops.conv1d_causal(x.to(gpu), w.to(gpu), out, batch=bs, seq=s, activation="silu")
+    out32 = torch.empty(bs * s, c, device=gpu)
+    ops.conv1d_causal(xd, w.to(gpu), out, batch=bs, seq=s, activation="silu", out32=out32)
     torch.cuda.synchronize()
+    assert _rel(out32, ref) < F32_REL
     if dtype == torch.float32:
         assert _rel(out, ref) < F32_REL
     else:

@@ -38,6 +38,7 @@ struct SsdK {
   float* y32; int64_t ldy32;
   float* states;  // [B][H][nc][P*N]
   float* tot;     // [B][H][nc]
+  int vec_epi;    // bf16 y (and gate), no dskip, 16-byte aligned rows: vector epilogue
 };
 
 // Running sum of dA (or the given cum re-based) for chunk ``c`` into cl[0..Q),
@@ -264,213 +265,453 @@ __global__ void __launch_bounds__(256) ssd_out_kernel(SsdK p) {
 
 // ------------------------------------------------------ bf16 MFMA scan path
 // Same three-step scan with every product on v_mfma_f32_32x32x16_bf16 (bf16
-// operands, fp32 accumulation). Operand layouts of the 32x32x16 MFMA, lane l:
-//   A (32 x 16): row l%32, k = 8*(l/32) .. +8      B (16 x 32): col l%32, same k
-//   C (32 x 32): register r holds row 8*(r/4) + 4*(l/32) + r%4, col l%32.
-// The computed operands w_l x_l (chunk states), M = (C B^T) o L and the carried
-// state H are fp32; each enters the MFMA as hi + lo, two bf16 parts with
-// hi = bf16(v), lo = bf16(v - hi), so they carry ~16 mantissa bits. Inputs x,
-// B, C are bf16 already; all sums are fp32.
+// operands, fp32 accumulation). Operand layouts of the 32x32x16 MFMA, lane l,
+// g = l/32:
+//   A (32 x 16): row l%32, k = 8g .. 8g+8       B (16 x 32): col l%32, same k
+//   C (32 x 32): register r holds row 8*(r/4) + 4g + r%4, col l%32.
+// A and B fragments have the same shape, so a C result read lane-wise is, as
+// it stands, the A or B operand of a next product whose k index runs over its
+// rows: registers 0..7 are k-step 0 and 8..15 k-step 1, with the k order
+// row(r) of the C layout. Both operands of such a product must come out of a
+// C layout (or be stored in that order) so their k orders agree.
+//
+// Token-major tiles (32 tokens x 32 columns of x or B) become operands with k
+// over tokens through an identity product: D = X I copies X exactly (bf16 in,
+// one nonzero product per fp32 sum) into the C layout, lane = column,
+// register = token. Nothing is transposed through LDS.
+//
+// Computed fp32 operands (w_l x_l, the masked decay products and the carried
+// state) enter as hi + lo, hi = bf16(v), lo = bf16(v - hi), ~16 mantissa bits;
+// x, B, C are bf16 already.
 
-__device__ __forceinline__ bf16x8_t pack8_bf16(const float* v) {
-  uint4 w;
-  w.x = (uint32_t)f32_to_bf16(v[0]) | ((uint32_t)f32_to_bf16(v[1]) << 16);
-  w.y = (uint32_t)f32_to_bf16(v[2]) | ((uint32_t)f32_to_bf16(v[3]) << 16);
-  w.z = (uint32_t)f32_to_bf16(v[4]) | ((uint32_t)f32_to_bf16(v[5]) << 16);
-  w.w = (uint32_t)f32_to_bf16(v[6]) | ((uint32_t)f32_to_bf16(v[7]) << 16);
+typedef __attribute__((ext_vector_type(2))) float f32x2_t;
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
+
+// two fp32 -> packed bf16 pair, round to nearest even (v_cvt_pk_bf16_f32)
+__device__ __forceinline__ uint32_t pk_bf16(float a, float b) {
+  const f32x2_t v = {a, b};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
+}
+
+__device__ __forceinline__ bf16x8_t pk8(const float* v) {
+  const uint4 w = make_uint4(pk_bf16(v[0], v[1]), pk_bf16(v[2], v[3]), pk_bf16(v[4], v[5]), pk_bf16(v[6], v[7]));
   return __builtin_bit_cast(bf16x8_t, w);
 }
 
-__device__ __forceinline__ void split8_bf16(const float* v, bf16x8_t& hi, bf16x8_t& lo) {
-  float h[8], l[8];
+__device__ __forceinline__ void unpk8(const uint4& w, float* f) {
+  const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const uint16_t hb = f32_to_bf16(v[i]);
-    h[i] = bf16_to_f32(hb);
-    l[i] = v[i] - h[i];
+  for (int q = 0; q < 4; ++q) {
+    f[2 * q] = __uint_as_float(ws[q] << 16);
+    f[2 * q + 1] = __uint_as_float(ws[q] & 0xffff0000u);
   }
-  hi = pack8_bf16(h);
-  lo = pack8_bf16(l);
 }
 
+__device__ __forceinline__ void pk8_split(const float* v, bf16x8_t& hi, bf16x8_t& lo) {
+  const uint4 h = make_uint4(pk_bf16(v[0], v[1]), pk_bf16(v[2], v[3]), pk_bf16(v[4], v[5]), pk_bf16(v[6], v[7]));
+  float f[8], r[8];
+  unpk8(h, f);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) r[i] = v[i] - f[i];
+  hi = __builtin_bit_cast(bf16x8_t, h);
+  lo = pk8(r);
+}
+
+// Branch-free guarded load: out-of-range lanes read element 0 (always valid)
+// and return zeros, so a batch of loads issues back to back.
 __device__ __forceinline__ bf16x8_t ldg_bf16x8(const void* base, int64_t elem, bool ok) {
-  if (!ok) return __builtin_bit_cast(bf16x8_t, make_uint4(0, 0, 0, 0));
-  return *(const bf16x8_t*)((const uint16_t*)base + elem);
+  const uint4 v = *(const uint4*)((const uint16_t*)base + (ok ? elem : 0));
+  const uint4 z = make_uint4(0, 0, 0, 0);
+  return __builtin_bit_cast(bf16x8_t, ok ? v : z);
 }
 
 __device__ __forceinline__ int crow_of(int r, int lane) { return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3); }
 
-// Token-major bf16 rows [tok0 + l, col0 .. col0 + 8*C8) of chunk rows l < Q into
-// an LDS matrix dst[col][l] (row stride QS), each value times wl[l] (or 1).
-__device__ void stage_transposed(const void* src, int64_t ld, int64_t tok0, int64_t col0, int C8, int Q, int rows,
-                                 const float* wl, uint16_t* dst, int QS, uint16_t* dst_lo = nullptr) {
-  for (int e = threadIdx.x; e < Q * C8; e += 256) {
-    const int l = e / C8, c8 = e - l * C8;
-    uint4 raw = make_uint4(0, 0, 0, 0);
-    if (l < rows) raw = *(const uint4*)((const uint16_t*)src + (tok0 + l) * ld + col0 + c8 * 8);
-    const uint32_t ws[4] = {raw.x, raw.y, raw.z, raw.w};
-    uint16_t* d = dst + (c8 * 8) * QS + l;
-    if (wl) {
-      const float w = wl[l];
-      uint16_t* dl = dst_lo + (c8 * 8) * QS + l;
+// B operand of the identity product for k-step kk: 1.0 at k = column (lane % 32).
+__device__ __forceinline__ bf16x8_t eye_frag(int lane, int kk) {
+  const int j = (lane & 31) - 16 * kk - 8 * (lane >> 5);
+  uint32_t w[4];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const float v = __uint_as_float((i & 1) ? (ws[i >> 1] & 0xffff0000u) : (ws[i >> 1] << 16)) * w;
-        const uint16_t hb = f32_to_bf16(v);
-        d[i * QS] = hb;
-        dl[i * QS] = f32_to_bf16(v - bf16_to_f32(hb));
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        d[(2 * i) * QS] = (uint16_t)(ws[i] & 0xffffu);
-        d[(2 * i + 1) * QS] = (uint16_t)(ws[i] >> 16);
-      }
-    }
-  }
+  for (int q = 0; q < 4; ++q) w[q] = (j == 2 * q ? 0x3F80u : 0u) | (j == 2 * q + 1 ? 0x3F800000u : 0u);
+  return __builtin_bit_cast(bf16x8_t, make_uint4(w[0], w[1], w[2], w[3]));
 }
 
-// S_c[p][n] = sum_l (w_l x_l[p]) B_l[n],  w_l = dt_l exp(cl_last - cl_l).
-__global__ void __launch_bounds__(256) ssd_state_mfma_kernel(SsdK p) {
-  extern __shared__ float sm[];
-  float* cl = sm;          // 256
-  float* dts = cl + 256;   // 256
-  float* tmp = dts + 256;  // 512
-  const int Q = p.Q, P = p.P, N = p.N, QS = Q + 8;
-  uint16_t* xt = (uint16_t*)(tmp + 512);  // [P][QS]  w_l x_l (hi part), transposed
-  uint16_t* xl = xt + P * QS;             // [P][QS]  its lo part
-  uint16_t* bt = xl + P * QS;             // [N][QS]  B_l, transposed
+// 32 rows (lane%32) x 32 columns, given as the two 16-column A fragments -> C layout.
+__device__ __forceinline__ f32x16_t relayout(bf16x8_t a0, bf16x8_t a1, bf16x8_t e0, bf16x8_t e1) {
+  f32x16_t d;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) d[r] = 0.f;
+  d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, e0, d, 0, 0, 0);
+  d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, e1, d, 0, 0, 0);
+  return d;
+}
+
+// S_c[p][n] = sum_l (w_l x_l[p]) B_l[n],  w_l = dt_l exp(cl_last - cl_l)  (exponent <= 0).
+// One workgroup per (chunk, head, batch), no LDS staging: wave w owns p-tile
+// w % PT and n-tiles w / PT + j * (4 / PT), j < NTW, and walks the chunk in
+// 32-token blocks, each x / B block moved into operand order by relayout().
+template <int NTW>
+__global__ void __launch_bounds__(256) ssd_state2_kernel(SsdK p) {
+  __shared__ float cl[256], dts[256], tmp[512], wl[256];
   const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z, tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int g = h / p.hpg;
+  const int g = h / p.hpg, gl = lane >> 5, r32 = lane & 31;
   chunk_running_sum(p, b, h, c, cl, dts, tmp);
-  const int t0 = c * Q;
-  const int rows = min(Q, p.S - t0);
+  const int Q = p.Q, t0 = c * Q, rows = min(Q, p.S - t0);
   const float last = cl[Q - 1];
-  if (tid < Q) tmp[tid] = dts[tid] * __expf(last - cl[tid]);  // w_l (0 past the sequence end: dt = 0)
+  if (tid < Q) wl[tid] = dts[tid] * __expf(last - cl[tid]);
   __syncthreads();
+  const int PT = p.P >> 5, NT = p.N >> 5, WPP = 4 / PT;
+  const int pt = wave % PT, nt0 = wave / PT;
   const int64_t tok0 = (int64_t)b * p.S + t0;
-  stage_transposed(p.x, p.ldx, tok0, (int64_t)h * P, P >> 3, Q, rows, tmp, xt, QS, xl);
-  stage_transposed(p.b, p.ldb, tok0, (int64_t)g * N, N >> 3, Q, rows, nullptr, bt, QS);
-  __syncthreads();
-  const int TN = N >> 5;
-  float* st = p.states + (((int64_t)b * p.H + h) * p.nc + c) * (int64_t)(P * N);
-  for (int tile = wave; tile < (P >> 5) * TN; tile += 4) {
-    const int ti = tile / TN, tj = tile - ti * TN;
-    f32x16_t acc;
+  const int64_t xcol = (int64_t)h * p.P + pt * 32 + 8 * gl, bcol = (int64_t)g * p.N + 8 * gl;
+  const bf16x8_t e0 = eye_frag(lane, 0), e1 = eye_frag(lane, 1);
+  f32x16_t acc[NTW];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) acc[r] = 0.f;
-    const uint16_t* ar = xt + (ti * 32 + (lane & 31)) * QS + 8 * (lane >> 5);
-    const uint16_t* arl = ar + P * QS;
-    const uint16_t* br = bt + (tj * 32 + (lane & 31)) * QS + 8 * (lane >> 5);
-    for (int k0 = 0; k0 < Q; k0 += 16) {
-      const bf16x8_t bv = *(const bf16x8_t*)(br + k0);
-      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(*(const bf16x8_t*)(ar + k0), bv, acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(*(const bf16x8_t*)(arl + k0), bv, acc, 0, 0, 0);
+  for (int j = 0; j < NTW; ++j)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[j][r] = 0.f;
+  const int nsb = (rows + 31) >> 5;
+  struct Blk {
+    bf16x8_t xa0, xa1, ba[NTW][2];
+  };
+  auto load_blk = [&](Blk& k2, int sb) {
+    const int l = sb * 32 + r32;
+    const bool ok = sb < nsb && l < rows;
+    const int64_t tok = tok0 + l;
+    k2.xa0 = ldg_bf16x8(p.x, tok * p.ldx + xcol, ok);
+    k2.xa1 = ldg_bf16x8(p.x, tok * p.ldx + xcol + 16, ok);
+#pragma unroll
+    for (int j = 0; j < NTW; ++j) {
+      const int nt = nt0 + j * WPP;
+      k2.ba[j][0] = ldg_bf16x8(p.b, tok * p.ldb + bcol + nt * 32, ok && nt < NT);
+      k2.ba[j][1] = ldg_bf16x8(p.b, tok * p.ldb + bcol + nt * 32 + 16, ok && nt < NT);
     }
+  };
+  auto compute_blk = [&](const Blk& k2, int sb) {
+    const f32x16_t xr = relayout(k2.xa0, k2.xa1, e0, e1);
+    float v[16];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) st[(int64_t)(ti * 32 + crow_of(r, lane)) * N + tj * 32 + (lane & 31)] = acc[r];
+    for (int q = 0; q < 4; ++q) {
+      const float4 w4 = *(const float4*)&wl[sb * 32 + 8 * q + 4 * gl];
+      v[4 * q] = xr[4 * q] * w4.x;
+      v[4 * q + 1] = xr[4 * q + 1] * w4.y;
+      v[4 * q + 2] = xr[4 * q + 2] * w4.z;
+      v[4 * q + 3] = xr[4 * q + 3] * w4.w;
+    }
+    bf16x8_t xh0, xl0, xh1, xl1;
+    pk8_split(v, xh0, xl0);
+    pk8_split(v + 8, xh1, xl1);
+#pragma unroll
+    for (int j = 0; j < NTW; ++j) {
+      if (nt0 + j * WPP >= NT) continue;
+      const f32x16_t br = relayout(k2.ba[j][0], k2.ba[j][1], e0, e1);
+      float bv[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) bv[r] = br[r];
+      const bf16x8_t bb0 = pk8(bv), bb1 = pk8(bv + 8);
+      acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xh0, bb0, acc[j], 0, 0, 0);
+      acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xl0, bb0, acc[j], 0, 0, 0);
+      acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xh1, bb1, acc[j], 0, 0, 0);
+      acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xl1, bb1, acc[j], 0, 0, 0);
+    }
+  };
+  // two buffers: the next token block's loads are in flight while this one computes
+  Blk k0, k1;
+  load_blk(k0, 0);
+  for (int sb = 0; sb < nsb; sb += 2) {
+    load_blk(k1, sb + 1);
+    compute_blk(k0, sb);
+    if (sb + 1 >= nsb) break;
+    load_blk(k0, sb + 2);
+    compute_blk(k1, sb + 1);
+  }
+  float* st = p.states + (((int64_t)b * p.H + h) * p.nc + c) * (int64_t)(p.P * p.N);
+#pragma unroll
+  for (int j = 0; j < NTW; ++j) {
+    const int nt = nt0 + j * WPP;
+    if (nt >= NT) continue;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) st[(int64_t)(pt * 32 + crow_of(r, lane)) * p.N + nt * 32 + r32] = acc[j][r];
   }
   if (tid == 0) p.tot[((int64_t)b * p.H + h) * p.nc + c] = last;
 }
 
-// One workgroup per chunk; each wave takes 32x32 output tiles (32 rows t,
-// 32 columns p):
-//   y = exp(cl_t) C_t H^T + sum_{s<=t} [(C_t . B_s) exp(cl_t - cl_s) dt_s] x_s + D x_t, times gate,
-// where H is the state entering the chunk (the carry kernel's output).
-template <int KS>  // state_dim / 16
-__global__ void __launch_bounds__(256) ssd_out_mfma_kernel(SsdK p) {
+// H_0 = 0, H_{c+1} = exp(tot_c) H_c + S_c, written for c >= 1 as the hi/lo bf16
+// B fragments of the out kernel's state term: fragment (pt, ks, lane) is
+// H[pt*32 + lane%32][16 ks + 8 (lane/32) + j], j < 8, hi (16 bytes) then lo.
+// One thread per (p, 8 consecutive n), sequential over the chunks.
+__global__ void __launch_bounds__(256) ssd_carry2_kernel(SsdK p, uint4* hf) {
+  const int h = blockIdx.y, b = blockIdx.z;
+  const int N8 = p.N >> 3, KS = p.N >> 4, PN = p.P * p.N;
+  const int e = blockIdx.x * 256 + threadIdx.x;
+  if (e >= p.P * N8) return;
+  const int pp = e / N8, n8 = e - pp * N8;
+  const int frag = ((pp >> 5) * KS + (n8 >> 1)) * 64 + (pp & 31) + 32 * (n8 & 1);
+  const int64_t bh = (int64_t)b * p.H + h;
+  const float* st = p.states + bh * p.nc * PN + (int64_t)pp * p.N + n8 * 8;
+  uint4* out = hf + bh * p.nc * (PN / 4) + 2 * frag;
+  const float* tot = p.tot + bh * p.nc;
+  float carry[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) carry[i] = 0.f;
+  // the loads of up to 8 chunks are issued together; the recurrence then runs on registers
+  for (int c0 = 0; c0 + 1 < p.nc; c0 += 8) {
+    float4 sv[8][2];
+    float dec[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int c = min(c0 + k, p.nc - 2);
+      sv[k][0] = *(const float4*)(st + (int64_t)c * PN);
+      sv[k][1] = *(const float4*)(st + (int64_t)c * PN + 4);
+      dec[k] = tot[c];
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int c = c0 + k;
+      if (c + 1 >= p.nc) break;
+      const float e = c == 0 ? 0.f : __expf(dec[k]);
+      const float s8[8] = {sv[k][0].x, sv[k][0].y, sv[k][0].z, sv[k][0].w,
+                           sv[k][1].x, sv[k][1].y, sv[k][1].z, sv[k][1].w};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) carry[i] = carry[i] * e + s8[i];
+      bf16x8_t hi, lo;
+      pk8_split(carry, hi, lo);
+      uint4* o = out + (int64_t)(c + 1) * (PN / 4);
+      o[0] = __builtin_bit_cast(uint4, hi);
+      o[1] = __builtin_bit_cast(uint4, lo);
+    }
+  }
+}
+
+// One workgroup per (chunk, head, batch):
+//   y_t = exp(cl_t) C_t H^T + sum_{s<=t} (C_t . B_s) exp(cl_t - cl_s) dt_s x_s + D x_t, times gate.
+// x of the chunk is staged once in LDS as B fragments (relayout()). A unit is
+// a 32-row t-block with NPT p-tiles; for each s-block s <= t the wave forms
+// G^T = B_s C_t^T on the MFMA (lane = t, registers = s in C order), weighs it
+// element-wise with the decay (every exponent a difference cl_t - cl_s <= 0,
+// in base 2) and uses it directly as the A operand of the product with x.
+// Full chunks load without guards; only the diagonal s-block is masked. The
+// result goes out through a per-wave LDS tile as 16-byte rows (gate in, y out).
+constexpr int kEpiStride = 36;  // floats per row of the per-wave 32 x 32 output tile
+
+template <int KS, int NPT>  // KS = state_dim / 16, NPT = p-tiles per unit
+__global__ void __launch_bounds__(256, 2) ssd_out2_kernel(SsdK p, const uint4* hf) {
   extern __shared__ float sm[];
-  float* cl = sm;
+  float* cl = sm;          // running sum of dA, in log2 units after set-up
   float* dts = cl + 256;
   float* tmp = dts + 256;
-  const int Q = p.Q, P = p.P, N = KS * 16, QS = Q + 8;
-  constexpr int MS = 40;                  // M scratch row stride (bf16)
-  uint16_t* xt = (uint16_t*)(tmp + 512);  // [P][QS] x transposed
-  uint16_t* ms = xt + P * QS;             // per wave [32][MS]
+  float* epi = tmp + 512;  // [4 waves][32][kEpiStride]
+  uint4* xs = (uint4*)(epi + 4 * 32 * kEpiStride);  // [Q/32][2][PT][64] B fragments of x
   const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z, tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int g = h / p.hpg;
+  const int g = h / p.hpg, gl = lane >> 5, r32 = lane & 31;
   chunk_running_sum(p, b, h, c, cl, dts, tmp);
-  const int t0 = c * Q;
-  const int rows = min(Q, p.S - t0);
+  const int Q = p.Q, t0 = c * Q, rows = min(Q, p.S - t0);
+  if (tid < Q) cl[tid] *= 1.4426950408889634f;
+  const int PT = p.P >> 5;
   const int64_t tok0 = (int64_t)b * p.S + t0;
-  stage_transposed(p.x, p.ldx, tok0, (int64_t)h * P, P >> 3, Q, rows, nullptr, xt, QS);
+  const int ntb = (rows + 31) >> 5;
+  const bool full = rows == Q;
+  {
+    // this wave's x tiles (at most 8): every load issued before the first relayout
+    const bf16x8_t e0 = eye_frag(lane, 0), e1 = eye_frag(lane, 1);
+    bf16x8_t xa[8][2];
+#pragma unroll
+    for (int k2 = 0; k2 < 8; ++k2) {
+      const int u = wave + 4 * k2;
+      const int sb = u / PT, pt = u - sb * PT;
+      const int l = sb * 32 + r32;
+      const bool ok = u < ntb * PT && l < rows;
+      const int64_t at = (tok0 + l) * p.ldx + (int64_t)h * p.P + pt * 32 + 8 * gl;
+      xa[k2][0] = ldg_bf16x8(p.x, at, ok);
+      xa[k2][1] = ldg_bf16x8(p.x, at + 16, ok);
+    }
+#pragma unroll
+    for (int k2 = 0; k2 < 8; ++k2) {
+      const int u = wave + 4 * k2;
+      if (u >= ntb * PT) break;
+      const int sb = u / PT, pt = u - sb * PT;
+      const f32x16_t d = relayout(xa[k2][0], xa[k2][1], e0, e1);
+      float v[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) v[r] = d[r];
+      xs[((sb * 2 + 0) * PT + pt) * 64 + lane] = __builtin_bit_cast(uint4, pk8(v));
+      xs[((sb * 2 + 1) * PT + pt) * 64 + lane] = __builtin_bit_cast(uint4, pk8(v + 8));
+    }
+  }
   __syncthreads();
-  uint16_t* msw = ms + wave * 2 * 32 * MS;  // hi tile, then lo tile
-  uint16_t* msl = msw + 32 * MS;
-  const float* H = p.states + (((int64_t)b * p.H + h) * p.nc + c) * (int64_t)(P * N);
-  const int TP = P >> 5, ntb = (rows + 31) >> 5;
-  const int64_t ccol = (int64_t)g * N + 8 * (lane >> 5);
-  for (int unit = wave; unit < ntb * TP; unit += 4) {
-    const int tb = unit / TP, pt = unit - tb * TP;
-    const int trow = tb * 32 + (lane & 31);
+  const int PG = PT / NPT, U = ntb * PG;
+  const uint4* hfc = hf + (((int64_t)b * p.H + h) * p.nc + c) * (int64_t)(p.P * p.N / 4);
+  const int64_t ccol = (int64_t)g * p.N + 8 * gl;
+  const float dh = p.D ? p.D[h] : 0.f;
+  float* ep = epi + wave * 32 * kEpiStride;
+  for (int i = 0; i < U; ++i) {
+    // units by decreasing work, dealt to the waves in snake order
+    int w = i & 3;
+    if ((i >> 2) & 1) w = 3 - w;
+    if (w != wave) continue;
+    const int tb = ntb - 1 - i / PG, pg = i % PG;
+    const int t = tb * 32 + r32;
     bf16x8_t cf[KS];
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) cf[ks] = ldg_bf16x8(p.c, (tok0 + trow) * p.ldc + ccol + ks * 16, trow < rows);
-    f32x16_t acc;
+    for (int ks = 0; ks < KS; ++ks) cf[ks] = ldg_bf16x8(p.c, (tok0 + t) * p.ldc + ccol + ks * 16, t < rows);
+    f32x16_t acc[NPT];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+    for (int j = 0; j < NPT; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[j][r] = 0.f;
     if (c > 0) {
-      const float* hr = H + (int64_t)(pt * 32 + (lane & 31)) * N + 8 * (lane >> 5);
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        const float4 h0 = *(const float4*)(hr + ks * 16), h1 = *(const float4*)(hr + ks * 16 + 4);
-        const float hv[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
-        bf16x8_t hh, hl;
-        split8_bf16(hv, hh, hl);
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(cf[ks], hh, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(cf[ks], hl, acc, 0, 0, 0);
+      for (int j = 0; j < NPT; ++j) {
+        const int pt = pg * NPT + j;
+        uint4 hfr[KS][2];
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          const uint4* f = hfc + 2 * ((pt * KS + ks) * 64 + lane);
+          hfr[ks][0] = f[0];
+          hfr[ks][1] = f[1];
+        }
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(cf[ks], __builtin_bit_cast(bf16x8_t, hfr[ks][0]), acc[j], 0, 0, 0);
+          acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(cf[ks], __builtin_bit_cast(bf16x8_t, hfr[ks][1]), acc[j], 0, 0, 0);
+        }
       }
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc[r] *= __expf(cl[tb * 32 + crow_of(r, lane)]);
+      for (int q = 0; q < 4; ++q) {
+        const float4 c4 = *(const float4*)&cl[tb * 32 + 8 * q + 4 * gl];
+        const float ex[4] = {exp2f(c4.x), exp2f(c4.y), exp2f(c4.z), exp2f(c4.w)};
+#pragma unroll
+        for (int j = 0; j < NPT; ++j)
+#pragma unroll
+          for (int i2 = 0; i2 < 4; ++i2) acc[j][4 * q + i2] *= ex[i2];
+      }
     }
-    for (int sb = 0; sb <= tb; ++sb) {
-      const int srow = sb * 32 + (lane & 31);
-      f32x16_t gacc;
+    const float clt = cl[t];
+    // one s-block: G^T = B_s C_t^T, decay-weighted and (diagonal block) masked, times x_s
+    auto sblock = [&](const bf16x8_t* bfr, int sb) {
+      f32x16_t gt;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) gacc[r] = 0.f;
+      for (int r = 0; r < 16; ++r) gt[r] = 0.f;
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks)
-        gacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-            cf[ks], ldg_bf16x8(p.b, (tok0 + srow) * p.ldb + ccol + ks * 16, srow < rows), gacc, 0, 0, 0);
-      // M[t][s] = G o L, written to this wave's scratch as bf16 (A-operand layout on read)
+      for (int ks = 0; ks < KS; ++ks) gt = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[ks], cf[ks], gt, 0, 0, 0);
+      float m[16];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int tr = crow_of(r, lane), t = tb * 32 + tr;
-        const float m = (srow <= t && srow < rows) ? gacc[r] * __expf(cl[t] - cl[srow]) * dts[srow] : 0.f;
-        const uint16_t mh = f32_to_bf16(m);
-        msw[tr * MS + (lane & 31)] = mh;
-        msl[tr * MS + (lane & 31)] = f32_to_bf16(m - bf16_to_f32(mh));
+      for (int q = 0; q < 4; ++q) {
+        const int s0 = sb * 32 + 8 * q + 4 * gl;
+        const float4 c4 = *(const float4*)&cl[s0];
+        const float4 d4 = *(const float4*)&dts[s0];
+        const float cs[4] = {c4.x, c4.y, c4.z, c4.w}, ds[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+        for (int i2 = 0; i2 < 4; ++i2) m[4 * q + i2] = gt[4 * q + i2] * exp2f(clt - cs[i2]) * ds[i2];
       }
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      if (sb == tb) {
 #pragma unroll
-      for (int k2 = 0; k2 < 2; ++k2) {
-        const int mo = (lane & 31) * MS + k2 * 16 + 8 * (lane >> 5);
-        const bf16x8_t bx = *(const bf16x8_t*)(xt + (pt * 32 + (lane & 31)) * QS + sb * 32 + k2 * 16 + 8 * (lane >> 5));
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(*(const bf16x8_t*)(msw + mo), bx, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(*(const bf16x8_t*)(msl + mo), bx, acc, 0, 0, 0);
+        for (int r = 0; r < 16; ++r) m[r] = tb * 32 + crow_of(r, lane) <= t ? m[r] : 0.f;
       }
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      bf16x8_t mh0, ml0, mh1, ml1;
+      pk8_split(m, mh0, ml0);
+      pk8_split(m + 8, mh1, ml1);
+#pragma unroll
+      for (int j = 0; j < NPT; ++j) {
+        const int pt = pg * NPT + j;
+        const bf16x8_t x0 = __builtin_bit_cast(bf16x8_t, xs[((sb * 2 + 0) * PT + pt) * 64 + lane]);
+        const bf16x8_t x1 = __builtin_bit_cast(bf16x8_t, xs[((sb * 2 + 1) * PT + pt) * 64 + lane]);
+        acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(mh0, x0, acc[j], 0, 0, 0);
+        acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ml0, x0, acc[j], 0, 0, 0);
+        acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(mh1, x1, acc[j], 0, 0, 0);
+        acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ml1, x1, acc[j], 0, 0, 0);
+      }
+    };
+    auto load_b = [&](bf16x8_t* bfr, int sb) {
+      const int sr = sb * 32 + r32;
+      const int64_t at = (tok0 + sr) * p.ldb + ccol;
+      if (full) {
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) bfr[ks] = *(const bf16x8_t*)((const uint16_t*)p.b + at + ks * 16);
+      } else {
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) bfr[ks] = ldg_bf16x8(p.b, at + ks * 16, sr < rows);
+      }
+    };
+    // two buffers: the next s-block's B rows are in flight while this one computes
+    bf16x8_t b0[KS], b1[KS];
+    load_b(b0, 0);
+    for (int sb = 0; sb <= tb; sb += 2) {
+      if (sb + 1 <= tb) load_b(b1, sb + 1);
+      sblock(b0, sb);
+      if (sb + 1 > tb) break;
+      if (sb + 2 <= tb) load_b(b0, sb + 2);
+      sblock(b1, sb + 1);
     }
-    const int pp = pt * 32 + (lane & 31);
-    const int64_t col = (int64_t)h * P + pp;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int t = tb * 32 + crow_of(r, lane);
-      if (t >= rows) continue;
-      const int64_t tok = tok0 + t;
-      const float xv = load_elem(p.x, tok * p.ldx + col, p.dtype);
-      float v = acc[r];
-      if (p.dskip) v += xv * load_elem(p.dskip, tok * p.lddskip + col, p.dtype);
-      else if (p.D) v += xv * p.D[h];
-      if (p.gate) v *= load_elem(p.gate, tok * p.ldgate + col, p.gdt);
-      store_elem(p.y, tok * p.ldy + col, p.ydt, v);
-      if (p.y32) p.y32[tok * p.ldy32 + col] = v;
+    for (int j = 0; j < NPT; ++j) {
+      const int pt = pg * NPT + j;
+      float xv[16];
+      unpk8(xs[((tb * 2 + 0) * PT + pt) * 64 + lane], xv);
+      unpk8(xs[((tb * 2 + 1) * PT + pt) * 64 + lane], xv + 8);
+      const int64_t col = (int64_t)h * p.P + pt * 32 + r32;
+      if (p.vec_epi) {
+        // C layout -> row-major tile in LDS -> 16 columns of one row per lane
+#pragma unroll
+        for (int r = 0; r < 16; ++r) ep[crow_of(r, lane) * kEpiStride + r32] = acc[j][r] + xv[r] * dh;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        const int row = lane >> 1, c0 = 16 * (lane & 1);
+        float v[16];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float4 f = *(const float4*)&ep[row * kEpiStride + c0 + 4 * q];
+          v[4 * q] = f.x; v[4 * q + 1] = f.y; v[4 * q + 2] = f.z; v[4 * q + 3] = f.w;
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        const int tr = tb * 32 + row;
+        const bool ok = tr < rows;
+        const int64_t tok = tok0 + (ok ? tr : 0);
+        const int64_t oc = (int64_t)h * p.P + pt * 32 + c0;
+        if (p.gate) {
+          const uint4* gp = (const uint4*)((const uint16_t*)p.gate + tok * p.ldgate + oc);
+          float gv[16];
+          unpk8(gp[0], gv);
+          unpk8(gp[1], gv + 8);
+#pragma unroll
+          for (int k2 = 0; k2 < 16; ++k2) v[k2] *= gv[k2];
+        }
+        if (ok) {
+          uint4* yp = (uint4*)((uint16_t*)p.y + tok * p.ldy + oc);
+          yp[0] = __builtin_bit_cast(uint4, pk8(v));
+          yp[1] = __builtin_bit_cast(uint4, pk8(v + 8));
+          if (p.y32) {
+            float4* y4 = (float4*)(p.y32 + tok * p.ldy32 + oc);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) y4[q] = make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
+          }
+        }
+      } else {
+        // general dtypes / full D: every load of the 16 rows issues before any is used
+        float dv[16], gv[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int tr = tb * 32 + crow_of(r, lane);
+          const int64_t tok = tok0 + (tr < rows ? tr : 0);
+          dv[r] = p.dskip ? load_elem(p.dskip, tok * p.lddskip + col, p.dtype) : dh;
+          gv[r] = p.gate ? load_elem(p.gate, tok * p.ldgate + col, p.gdt) : 1.f;
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int tr = tb * 32 + crow_of(r, lane);
+          const float v = (acc[j][r] + xv[r] * dv[r]) * gv[r];
+          if (tr < rows) {
+            const int64_t tok = tok0 + tr;
+            store_elem(p.y, tok * p.ldy + col, p.ydt, v);
+            if (p.y32) p.y32[tok * p.ldy32 + col] = v;
+          }
+        }
+      }
     }
   }
 }
@@ -500,9 +741,82 @@ __global__ void __launch_bounds__(256) conv1d_causal_kernel(ConvK p) {
   if (p.y32) p.y32[tok * p.ldy32 + ch] = acc;
 }
 
+// bf16 input, 8 channels (one 16-byte vector) x TT consecutive tokens of one
+// sequence per thread: the TT + K - 1 input rows the run needs are loaded
+// up front (the K - 1 rows before the run come from L2 for every run but the
+// first of a sequence), the taps slide over registers, and every access is a
+// 16-byte vector (32 bytes for fp32 outputs). Consecutive lanes take
+// consecutive channel groups, so a wave reads whole 1 KiB row segments.
+template <int K, int TT>
+__global__ void __launch_bounds__(256) conv1d_vec_kernel(ConvK p, int cg, int runs) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int g = (int)(idx % cg);
+  const int64_t r = idx / cg;  // run over (sequence, token block)
+  if (r >= (int64_t)p.B * runs) return;
+  const int bseq = (int)(r / runs);
+  const int t0 = (int)(r - (int64_t)bseq * runs) * TT;
+  const int ch = g * 8;
+  float w[8][K];
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+#pragma unroll
+    for (int j = 0; j < K; ++j) w[c][j] = p.w[(int64_t)(ch + c) * K + j];
+  }
+  const int64_t base = (int64_t)bseq * p.S;
+  uint4 rows[TT + K - 1];
+#pragma unroll
+  for (int i = 0; i < TT + K - 1; ++i) {
+    const int t = t0 - (K - 1) + i;
+    rows[i] = (t >= 0 && t < p.S) ? *(const uint4*)((const uint16_t*)p.x + (base + t) * p.ldx + ch)
+                                  : make_uint4(0, 0, 0, 0);
+  }
+  auto unpack = [](const uint4& v, float* f) {
+    const uint32_t ws[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      f[2 * q] = __uint_as_float(ws[q] << 16);
+      f[2 * q + 1] = __uint_as_float(ws[q] & 0xffff0000u);
+    }
+  };
+#pragma unroll
+  for (int i = 0; i < TT; ++i) {
+    const int t = t0 + i;
+    if (t >= p.S) break;
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < K; ++j) {
+      float f[8];
+      unpack(rows[i + j], f);
+#pragma unroll
+      for (int c = 0; c < 8; ++c) acc[c] += w[c][j] * f[c];
+    }
+    if (p.act == 1) {
+#pragma unroll
+      for (int c = 0; c < 8; ++c) acc[c] = acc[c] * sigmoidf_(acc[c]);
+    }
+    const int64_t tok = base + t;
+    if (p.ydt == TH_BF16) {
+      uint4 o;
+      o.x = (uint32_t)f32_to_bf16(acc[0]) | ((uint32_t)f32_to_bf16(acc[1]) << 16);
+      o.y = (uint32_t)f32_to_bf16(acc[2]) | ((uint32_t)f32_to_bf16(acc[3]) << 16);
+      o.z = (uint32_t)f32_to_bf16(acc[4]) | ((uint32_t)f32_to_bf16(acc[5]) << 16);
+      o.w = (uint32_t)f32_to_bf16(acc[6]) | ((uint32_t)f32_to_bf16(acc[7]) << 16);
+      *(uint4*)((uint16_t*)p.y + tok * p.ldy + ch) = o;
+    } else {
+      float* yo = (float*)p.y + tok * p.ldy + ch;
+      *(float4*)yo = make_float4(acc[0], acc[1], acc[2], acc[3]);
+      *(float4*)(yo + 4) = make_float4(acc[4], acc[5], acc[6], acc[7]);
+    }
+    if (p.y32) {
+      float* yo = p.y32 + tok * p.ldy32 + ch;
+      *(float4*)yo = make_float4(acc[0], acc[1], acc[2], acc[3]);
+      *(float4*)(yo + 4) = make_float4(acc[4], acc[5], acc[6], acc[7]);
+    }
+  }
+}
+
 static size_t state_lds(int P, int N) { return (size_t)(256 * 4 + 32 * P + 32 * N) * 4; }
-static size_t state_mfma_lds(int Q, int P, int N) { return 1024 * 4 + (size_t)(2 * P + N) * (Q + 8) * 2; }
-static size_t out_mfma_lds(int Q, int P) { return 1024 * 4 + (size_t)P * (Q + 8) * 2 + 4 * 2 * 32 * 40 * 2; }
+static size_t out2_lds(int Q, int P) { return 1024 * 4 + 4 * 32 * kEpiStride * 4 + (size_t)Q * P * 2; }
 static size_t out_lds(int RB, int P, int N) {
   const size_t intra = (size_t)RB * (N + 1) + (size_t)RB * (P + 1) + (size_t)RB * (RB + 1);
   const size_t inter = (size_t)P * (N + 1);
@@ -514,9 +828,10 @@ constexpr size_t kMaxLds = 163840;  // 160 KiB per workgroup on gfx950
 // Raise the dynamic-LDS limit of the scan kernels once per device (th_init),
 // so that launching them needs no attribute call (and can be graph-captured).
 int ssd_init_device() {
-  const void* fns[] = {(const void*)ssd_state_kernel, (const void*)ssd_out_kernel, (const void*)ssd_state_mfma_kernel,
-                       (const void*)ssd_out_mfma_kernel<2>, (const void*)ssd_out_mfma_kernel<4>,
-                       (const void*)ssd_out_mfma_kernel<8>};
+  const void* fns[] = {(const void*)ssd_state_kernel,          (const void*)ssd_out_kernel,
+                       (const void*)ssd_out2_kernel<2, 1>,      (const void*)ssd_out2_kernel<4, 1>,
+                       (const void*)ssd_out2_kernel<8, 1>,      (const void*)ssd_out2_kernel<2, 2>,
+                       (const void*)ssd_out2_kernel<4, 2>,      (const void*)ssd_out2_kernel<8, 2>};
   for (const void* f : fns) TH_CHECK_HIP(hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxLds));
   return TH_OK;
 }
@@ -534,11 +849,16 @@ static bool ssd_force_valu() {
 
 using namespace th;
 
+// Workspace: chunk states S [B][H][nc][P*N] fp32, chunk totals [B][H][nc]
+// (padded to 4 floats), then the carried states as MFMA fragments (4 bytes
+// per element, the MFMA path only).
+static int64_t ssd_tot_floats(int64_t bhc) { return (bhc + 3) / 4 * 4; }
+
 extern "C" int64_t th_ssd_workspace_bytes(int32_t batch, int32_t seq, int32_t heads, int32_t head_dim,
                                           int32_t state_dim, int32_t chunk) {
   if (batch <= 0 || seq <= 0 || heads <= 0 || head_dim <= 0 || state_dim <= 0 || chunk <= 0) return -1;
-  const int64_t nc = cdiv(seq, chunk);
-  return (int64_t)batch * heads * nc * ((int64_t)head_dim * state_dim + 1) * 4;
+  const int64_t bhc = (int64_t)batch * heads * cdiv(seq, chunk);
+  return (2 * bhc * head_dim * state_dim + ssd_tot_floats(bhc)) * 4;
 }
 
 extern "C" int th_ssd_chunked(const th_ssd_desc* d, void* stream) {
@@ -575,27 +895,50 @@ extern "C" int th_ssd_chunked(const th_ssd_desc* d, void* stream) {
   k.dt = d->dt; k.lddt = d->ld_dt; k.cum = d->cum; k.ldcum = d->ld_cum; k.A = d->A; k.D = d->D;
   k.dskip = d->dskip; k.lddskip = d->ld_dskip; k.gate = d->gate; k.ldgate = d->ld_gate; k.gdt = d->gate_dtype;
   k.y = d->y; k.ldy = d->ld_y; k.ydt = d->y_dtype; k.y32 = d->y32; k.ldy32 = d->ld_y32;
+  {
+    auto a16 = [](const void* q) { return ((uintptr_t)q & 15) == 0; };
+    k.vec_epi = d->y_dtype == TH_BF16 && d->ld_y % 8 == 0 && a16(d->y) && !d->dskip &&
+                (!d->gate || (d->gate_dtype == TH_BF16 && d->ld_gate % 8 == 0 && a16(d->gate))) &&
+                (!d->y32 || (d->ld_y32 % 4 == 0 && a16(d->y32))) && d->head_dim % 32 == 0;
+  }
   k.states = d->workspace;
   k.tot = d->workspace + (int64_t)k.B * k.H * k.nc * k.P * k.N;
   hipStream_t s = (hipStream_t)stream;
-  // MFMA path: bf16 operands, 32-multiple tiles, 16-byte aligned rows.
+  // MFMA path: bf16 operands, 32-wide p / n tiles, 16-byte aligned rows.
   auto al16 = [](const void* q) { return ((uintptr_t)q & 15) == 0; };
-  const bool mfma = d->dtype == TH_BF16 && k.P % 32 == 0 && k.P <= 128 && (k.N == 32 || k.N == 64 || k.N == 128) &&
-                    k.Q % 32 == 0 && d->ld_x % 8 == 0 && d->ld_b % 8 == 0 && d->ld_c % 8 == 0 && al16(d->x) &&
-                    al16(d->b) && al16(d->c) && state_mfma_lds(k.Q, k.P, k.N) <= kMaxLds &&
-                    out_mfma_lds(k.Q, k.P) <= kMaxLds && !ssd_force_valu();
+  const bool mfma = d->dtype == TH_BF16 && (k.P == 32 || k.P == 64 || k.P == 128) &&
+                    (k.N == 32 || k.N == 64 || k.N == 128) && k.Q % 32 == 0 && d->ld_x % 8 == 0 &&
+                    d->ld_b % 8 == 0 && d->ld_c % 8 == 0 && al16(d->x) && al16(d->b) && al16(d->c) &&
+                    out2_lds(k.Q, k.P) <= kMaxLds && !ssd_force_valu();
   if (mfma) {
-    const size_t l1 = state_mfma_lds(k.Q, k.P, k.N), l3 = out_mfma_lds(k.Q, k.P);
-    hipLaunchKernelGGL(ssd_state_mfma_kernel, dim3(k.nc, k.H, k.B), dim3(256), l1, s, k);
+    const int64_t bhc = (int64_t)k.B * k.H * k.nc;
+    uint4* hf = (uint4*)(d->workspace + bhc * k.P * k.N + ssd_tot_floats(bhc));
+    const int PT = k.P / 32, NT = k.N / 32;
+    const int ntw = (NT * PT + 3) / 4;
+    const dim3 grid(k.nc, k.H, k.B);
+    if (ntw == 1) hipLaunchKernelGGL(ssd_state2_kernel<1>, grid, dim3(256), 0, s, k);
+    else if (ntw == 2) hipLaunchKernelGGL(ssd_state2_kernel<2>, grid, dim3(256), 0, s, k);
+    else hipLaunchKernelGGL(ssd_state2_kernel<4>, grid, dim3(256), 0, s, k);
     TH_CHECK_LAUNCH();
-    hipLaunchKernelGGL(ssd_carry_kernel, dim3((unsigned)cdiv(k.P * k.N, 256), k.H, k.B), dim3(256), 0, s, k);
-    TH_CHECK_LAUNCH();
-    if (k.N == 32)
-      hipLaunchKernelGGL(ssd_out_mfma_kernel<2>, dim3(k.nc, k.H, k.B), dim3(256), l3, s, k);
-    else if (k.N == 64)
-      hipLaunchKernelGGL(ssd_out_mfma_kernel<4>, dim3(k.nc, k.H, k.B), dim3(256), l3, s, k);
-    else
-      hipLaunchKernelGGL(ssd_out_mfma_kernel<8>, dim3(k.nc, k.H, k.B), dim3(256), l3, s, k);
+    if (k.nc > 1) {
+      hipLaunchKernelGGL(ssd_carry2_kernel, dim3((unsigned)cdiv(k.P * k.N / 8, 256), k.H, k.B), dim3(256), 0, s, k, hf);
+      TH_CHECK_LAUNCH();
+    }
+    const size_t l3 = out2_lds(k.Q, k.P);
+    // a full 8-block chunk gives every wave two t-blocks: share each G^T tile over
+    // two p-tiles (more accumulators would not fit two waves per SIMD)
+    const int npt = k.Q / 32 >= 8 ? std::min(PT, 2) : 1;
+#define TH_SSD_OUT2(KS_, NPT_) hipLaunchKernelGGL((ssd_out2_kernel<KS_, NPT_>), grid, dim3(256), l3, s, k, (const uint4*)hf)
+#define TH_SSD_OUT2_KS(NPT_)                \
+  do {                                      \
+    if (k.N == 32) TH_SSD_OUT2(2, NPT_);    \
+    else if (k.N == 64) TH_SSD_OUT2(4, NPT_); \
+    else TH_SSD_OUT2(8, NPT_);              \
+  } while (0)
+    if (npt == 1) TH_SSD_OUT2_KS(1);
+    else TH_SSD_OUT2_KS(2);
+#undef TH_SSD_OUT2_KS
+#undef TH_SSD_OUT2
     TH_CHECK_LAUNCH();
     return TH_OK;
   }
@@ -627,8 +970,20 @@ extern "C" int th_conv1d_causal(const th_conv_desc* d, void* stream) {
   k.B = d->batch; k.S = d->seq; k.W = d->width; k.K = d->kernel; k.act = d->activation;
   k.xdt = d->x_dtype; k.ydt = d->y_dtype; k.x = d->x; k.ldx = d->ld_x; k.w = d->w;
   k.y = d->y; k.ldy = d->ld_y; k.y32 = d->y32; k.ldy32 = d->ld_y32;
-  hipLaunchKernelGGL(conv1d_causal_kernel, dim3((unsigned)((int64_t)k.B * k.S), (unsigned)cdiv(k.W, 256)), dim3(256), 0,
-                     (hipStream_t)stream, k);
+  auto al16 = [](const void* q) { return q == nullptr || ((uintptr_t)q & 15) == 0; };
+  const bool vec = k.K == 4 && k.xdt == TH_BF16 && k.W % 8 == 0 && k.ldx % 8 == 0 && k.ldy % 8 == 0 &&
+                   (!k.y32 || k.ldy32 % 4 == 0) && al16(k.x) && al16(k.y) && al16(k.y32);
+  if (vec) {
+    constexpr int TT = 16;
+    const int cg = k.W / 8;
+    const int runs = (int)cdiv(k.S, TT);
+    const int64_t threads = (int64_t)cg * k.B * runs;
+    hipLaunchKernelGGL((conv1d_vec_kernel<4, TT>), dim3((unsigned)cdiv(threads, 256)), dim3(256), 0,
+                       (hipStream_t)stream, k, cg, runs);
+  } else {
+    hipLaunchKernelGGL(conv1d_causal_kernel, dim3((unsigned)((int64_t)k.B * k.S), (unsigned)cdiv(k.W, 256)), dim3(256),
+                       0, (hipStream_t)stream, k);
+  }
   TH_CHECK_LAUNCH();
   return TH_OK;
 }
