@@ -83,6 +83,146 @@ __device__ __forceinline__ void store4(void* p, int64_t off, int dtype, bool vec
   for (int q = 0; q < 4 && q < valid; ++q) store_elem(p, off + q, dtype, t[q]);
 }
 
+// 8 consecutive elements (one 16-byte bf16 or two 16-byte fp32 accesses when
+// vec8, element by element for a ragged end or unaligned rows).
+__device__ __forceinline__ void load8(const void* p, int64_t off, int dtype, bool vec8, int valid, float* v) {
+  if (vec8 && valid >= 8) {
+    if (dtype == TH_BF16) {
+      const uint4 w = *(const uint4*)((const uint16_t*)p + off);
+      const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        v[2 * q] = __uint_as_float(ws[q] << 16);
+        v[2 * q + 1] = __uint_as_float(ws[q] & 0xffff0000u);
+      }
+    } else {
+      const float4 a = *(const float4*)((const float*)p + off), b = *(const float4*)((const float*)p + off + 4);
+      v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    }
+    return;
+  }
+#pragma unroll
+  for (int q = 0; q < 8; ++q) v[q] = q < valid ? load_elem(p, off + q, dtype) : 0.f;
+}
+
+__device__ __forceinline__ void store8(void* p, int64_t off, int dtype, bool vec8, int valid, const float* v) {
+  if (vec8 && valid >= 8) {
+    if (dtype == TH_BF16) {
+      uint4 w;
+      w.x = (uint32_t)f32_to_bf16(v[0]) | ((uint32_t)f32_to_bf16(v[1]) << 16);
+      w.y = (uint32_t)f32_to_bf16(v[2]) | ((uint32_t)f32_to_bf16(v[3]) << 16);
+      w.z = (uint32_t)f32_to_bf16(v[4]) | ((uint32_t)f32_to_bf16(v[5]) << 16);
+      w.w = (uint32_t)f32_to_bf16(v[6]) | ((uint32_t)f32_to_bf16(v[7]) << 16);
+      *(uint4*)((uint16_t*)p + off) = w;
+    } else {
+      *(float4*)((float*)p + off) = make_float4(v[0], v[1], v[2], v[3]);
+      *(float4*)((float*)p + off + 4) = make_float4(v[4], v[5], v[6], v[7]);
+    }
+    return;
+  }
+#pragma unroll
+  for (int q = 0; q < 8; ++q)
+    if (q < valid) store_elem(p, off + q, dtype, v[q]);
+}
+
+// One output op over a 16-row slice of the per-wave epilogue (persistent
+// kernel). Lane l takes columns c8 .. c8+8 (c8 = 8 (l % q8), q8 = hbn / 8
+// octets per row) of rows r_l + pass * rp, pass < np. The op is a template
+// argument, so each output runs one straight loop; every global operand of
+// the slice (extra rows, RoPE table rows) is loaded before the first use.
+template <int OP, bool SUMSQ>
+__device__ __forceinline__ void epi_slice(const GemmK& p, const EpiOutK& eo, const float* wsl, int ws, int hbn,
+                                          const float* rsrow, int64_t row0, int64_t col_w, int r_l, int c8, int np,
+                                          int rp) {
+  constexpr bool USES_E = OP == TH_EPI_ADD || OP == TH_EPI_SOFTPLUS_ADD || OP == TH_EPI_MUL;
+  constexpr bool USES_T = OP == TH_EPI_ROPE || OP == TH_EPI_ROPE_PAIR;
+  const int ia = eo.a, ib = eo.b;
+  const bool sa = SUMSQ && ((p.rscale_mask >> ia) & 1u);
+  const bool sb = SUMSQ && ib >= 0 && ((p.rscale_mask >> ib) & 1u);
+  const int64_t gn = col_w + c8;
+  const int valid = (int)min((int64_t)8, p.N - gn);
+  float xe[4][8], ye[4][8];
+  if constexpr (USES_E || USES_T) {
+#pragma unroll
+    for (int ps = 0; ps < 4; ++ps) {
+      const int64_t gm = row0 + r_l + ps * rp;
+      if (ps >= np || gm >= p.M || valid <= 0) continue;
+      if constexpr (USES_E) {
+        const int e = eo.e;
+        load8(p.extra[e], gm * p.ld_extra[e] + gn, p.extra_dtype[e], p.extra_vec8[e] != 0, valid, xe[ps]);
+      } else {
+        // head_dim is a multiple of 8, so the octet lies inside one head
+        const int64_t toff = (int64_t)((int)gm % p.period) * p.hd + (int)gn % p.hd;
+        const float4 c0 = *(const float4*)(p.rcos + toff), c1 = *(const float4*)(p.rcos + toff + 4);
+        const float4 s0 = *(const float4*)(p.rsin + toff), s1 = *(const float4*)(p.rsin + toff + 4);
+        xe[ps][0] = c0.x; xe[ps][1] = c0.y; xe[ps][2] = c0.z; xe[ps][3] = c0.w;
+        xe[ps][4] = c1.x; xe[ps][5] = c1.y; xe[ps][6] = c1.z; xe[ps][7] = c1.w;
+        ye[ps][0] = s0.x; ye[ps][1] = s0.y; ye[ps][2] = s0.z; ye[ps][3] = s0.w;
+        ye[ps][4] = s1.x; ye[ps][5] = s1.y; ye[ps][6] = s1.z; ye[ps][7] = s1.w;
+      }
+    }
+  }
+#pragma unroll
+  for (int ps = 0; ps < 4; ++ps) {
+    const int r16 = r_l + ps * rp;
+    const int64_t gm = row0 + r16;
+    if (ps >= np || gm >= p.M || valid <= 0) continue;
+    const float rr = SUMSQ ? rsrow[r16] : 1.f;
+    const float* srow = wsl + r16 * ws;
+    float a[8], v[8];
+    {
+      const float4 a0 = *(const float4*)(srow + ia * hbn + c8), a1 = *(const float4*)(srow + ia * hbn + c8 + 4);
+      a[0] = a0.x; a[1] = a0.y; a[2] = a0.z; a[3] = a0.w; a[4] = a1.x; a[5] = a1.y; a[6] = a1.z; a[7] = a1.w;
+    }
+    if (sa) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) a[i] *= rr;
+    }
+    if constexpr (OP == TH_EPI_ACC) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = a[i];
+    } else if constexpr (OP == TH_EPI_SILU) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = a[i] * sigmoidf_(a[i]);
+    } else if constexpr (OP == TH_EPI_SWIGLU) {
+      const float4 b0 = *(const float4*)(srow + ib * hbn + c8), b1 = *(const float4*)(srow + ib * hbn + c8 + 4);
+      float bb[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = a[i] * sigmoidf_(a[i]) * (sb ? bb[i] * rr : bb[i]);
+    } else if constexpr (OP == TH_EPI_ROPE || OP == TH_EPI_ROPE_PAIR) {
+      float rot[8];
+      if constexpr (OP == TH_EPI_ROPE) {
+        // partner column within the head, per quad (half a head is a multiple of 4)
+        const int half = p.hd >> 1;
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          const int within = (int)((gn + 4 * q) % p.hd);
+          const int pc = within < half ? c8 + 4 * q + half : c8 + 4 * q - half;
+          const float sg = within < half ? -1.f : 1.f;
+          const float4 r4 = *(const float4*)(srow + ia * hbn + pc);
+          const float s2 = sa ? sg * rr : sg;
+          rot[4 * q] = r4.x * s2; rot[4 * q + 1] = r4.y * s2; rot[4 * q + 2] = r4.z * s2; rot[4 * q + 3] = r4.w * s2;
+        }
+      } else {
+        const float4 b0 = *(const float4*)(srow + ib * hbn + c8), b1 = *(const float4*)(srow + ib * hbn + c8 + 4);
+        const float bb[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) rot[i] = sb ? bb[i] * rr : bb[i];
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = a[i] * xe[ps][i] + rot[i] * ye[ps][i];
+    } else {  // ADD, SOFTPLUS_ADD, MUL
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        if constexpr (OP == TH_EPI_MUL) v[i] = a[i] * xe[ps][i];
+        else if constexpr (OP == TH_EPI_ADD) v[i] = a[i] + xe[ps][i];
+        else v[i] = softplusf_(a[i] + xe[ps][i]);
+      }
+    }
+    store8(eo.ptr, gm * eo.ld + gn, eo.dtype, eo.vec8 != 0, valid, v);
+  }
+}
+
 // Evaluate every output op for the `rows` slab rows staged in LDS.
 // slab[r * srow + i * bn + j] = acc_i(row0 + r, tile_n * bn + j).
 __device__ void epilogue_slab(const GemmK& p, const float* slab, int srow, int rows,
@@ -758,113 +898,24 @@ __global__ void __launch_bounds__(256, 1) gemm_bf16_pk_kernel(GemmK p) {
 
         const int64_t row0 = row_w + t * 32 + h * 16;
         const float* rsrow = rsx + wm * WM + t * 32 + h * 16;
-        const int nu = 1 << (qlog - 2);  // units per lane: 16 rows x hbn/4 quads / 64 lanes (2, 4 or 8)
+        const int q8log = qlog - 1;  // octets per row = hbn / 8 (4, 8 or 16)
+        const int r_l = lane >> q8log, c8 = (lane & ((1 << q8log) - 1)) << 3;
+        const int np = 1 << (q8log - 2), rp = 64 >> q8log;
         for (int o = 0; o < p.n_out; ++o) {
           const EpiOutK& eo = p.out[o];
-          const int op = eo.op, ia = eo.a, ib = eo.b;
-          const bool scale_a = (p.rscale_mask >> ia) & 1u;
-          const bool scale_b = ib >= 0 && ((p.rscale_mask >> ib) & 1u);
-          // Global operand reads (extra operand, or the RoPE cos/sin rows) are
-          // issued four units at a time before their first use, so their
-          // latencies overlap.
-          const bool uses_e = op == TH_EPI_ADD || op == TH_EPI_SOFTPLUS_ADD || op == TH_EPI_MUL;
-          const bool uses_t = op == TH_EPI_ROPE || op == TH_EPI_ROPE_PAIR;
-          auto fetch = [&](int k, float4& x, float4& y) {
-            x = y = make_float4(0.f, 0.f, 0.f, 0.f);
-            const int un = lane + 64 * k;
-            const int r16 = un >> qlog;
-            const int cl = (un & ((1 << qlog) - 1)) << 2;
-            const int64_t gm = row0 + r16, gn = col_w + cl;
-            if (k >= nu || gm >= p.M || gn >= p.N) return;
-            if (uses_e) {
-              const int e = eo.e;
-              x = load4(p.extra[e], gm * p.ld_extra[e] + gn, p.extra_dtype[e], p.extra_vec[e] != 0,
-                        (int)min((int64_t)4, p.N - gn));
-            } else if (uses_t) {
-              const int64_t toff = (int64_t)((int)gm % p.period) * p.hd + (int)gn % p.hd;
-              x = *(const float4*)(p.rcos + toff);
-              y = *(const float4*)(p.rsin + toff);
-            }
-          };
-          auto unit = [&](int k, const float4& xk, const float4& yk) {
-            const int un = lane + 64 * k;
-            const int r16 = un >> qlog;
-            const int cl = (un & ((1 << qlog) - 1)) << 2;
-            const int64_t gm = row0 + r16, gn = col_w + cl;
-            if (k >= nu || gm >= p.M || gn >= p.N) return;
-            const int valid = (int)min((int64_t)4, p.N - gn);
-            const float rr = SUMSQ ? rsrow[r16] : 1.f;
-            const float* srow = wsl + r16 * WS;
-            float4 a = *(const float4*)(srow + ia * hbn + cl);
-            if (scale_a) { a.x *= rr; a.y *= rr; a.z *= rr; a.w *= rr; }
-            float4 v;
-            switch (op) {
-              case TH_EPI_ACC:
-                v = a;
-                break;
-              case TH_EPI_ROPE:
-              case TH_EPI_ROPE_PAIR: {
-                float4 rot;
-                const int within = (int)gn % p.hd;
-                if (op == TH_EPI_ROPE) {
-                  const int half = p.hd >> 1;
-                  const int pc = within < half ? cl + half : cl - half;
-                  const float sg = within < half ? -1.f : 1.f;
-                  rot = *(const float4*)(srow + ia * hbn + pc);
-                  const float s2 = scale_a ? sg * rr : sg;
-                  rot.x *= s2; rot.y *= s2; rot.z *= s2; rot.w *= s2;
-                } else {
-                  rot = *(const float4*)(srow + ib * hbn + cl);
-                  if (scale_b) { rot.x *= rr; rot.y *= rr; rot.z *= rr; rot.w *= rr; }
-                }
-                const float4 c = xk, s = yk;
-                v.x = a.x * c.x + rot.x * s.x;
-                v.y = a.y * c.y + rot.y * s.y;
-                v.z = a.z * c.z + rot.z * s.z;
-                v.w = a.w * c.w + rot.w * s.w;
-                break;
-              }
-              case TH_EPI_SILU:
-                v.x = a.x * sigmoidf_(a.x);
-                v.y = a.y * sigmoidf_(a.y);
-                v.z = a.z * sigmoidf_(a.z);
-                v.w = a.w * sigmoidf_(a.w);
-                break;
-              case TH_EPI_SWIGLU: {
-                float4 b = *(const float4*)(srow + ib * hbn + cl);
-                if (scale_b) { b.x *= rr; b.y *= rr; b.z *= rr; b.w *= rr; }
-                v.x = a.x * sigmoidf_(a.x) * b.x;
-                v.y = a.y * sigmoidf_(a.y) * b.y;
-                v.z = a.z * sigmoidf_(a.z) * b.z;
-                v.w = a.w * sigmoidf_(a.w) * b.w;
-                break;
-              }
-              default: {  // TH_EPI_ADD, TH_EPI_SOFTPLUS_ADD, TH_EPI_MUL
-                const float4 x = xk;
-                if (op == TH_EPI_MUL) {
-                  v.x = a.x * x.x; v.y = a.y * x.y; v.z = a.z * x.z; v.w = a.w * x.w;
-                } else {
-                  v.x = a.x + x.x; v.y = a.y + x.y; v.z = a.z + x.z; v.w = a.w + x.w;
-                  if (op == TH_EPI_SOFTPLUS_ADD) {
-                    v.x = softplusf_(v.x); v.y = softplusf_(v.y); v.z = softplusf_(v.z); v.w = softplusf_(v.w);
-                  }
-                }
-                break;
-              }
-            }
-            store4(eo.ptr, gm * eo.ld + gn, eo.dtype, eo.vec != 0, valid, v);
-          };
-          for (int k0 = 0; k0 < nu; k0 += 4) {
-            float4 x0, x1, x2, x3, y0, y1, y2, y3;
-            fetch(k0, x0, y0);
-            fetch(k0 + 1, x1, y1);
-            fetch(k0 + 2, x2, y2);
-            fetch(k0 + 3, x3, y3);
-            unit(k0, x0, y0);
-            unit(k0 + 1, x1, y1);
-            unit(k0 + 2, x2, y2);
-            unit(k0 + 3, x3, y3);
+#define TH_EPI_CASE(OP_) \
+  case OP_: epi_slice<OP_, SUMSQ>(p, eo, wsl, WS, hbn, rsrow, row0, col_w, r_l, c8, np, rp); break
+          switch (eo.op) {
+            TH_EPI_CASE(TH_EPI_ACC);
+            TH_EPI_CASE(TH_EPI_ROPE);
+            TH_EPI_CASE(TH_EPI_ROPE_PAIR);
+            TH_EPI_CASE(TH_EPI_SILU);
+            TH_EPI_CASE(TH_EPI_SWIGLU);
+            TH_EPI_CASE(TH_EPI_ADD);
+            TH_EPI_CASE(TH_EPI_SOFTPLUS_ADD);
+            default: epi_slice<TH_EPI_MUL, SUMSQ>(p, eo, wsl, WS, hbn, rsrow, row0, col_w, r_l, c8, np, rp); break;
           }
+#undef TH_EPI_CASE
         }
         // the next 16 rows overwrite this slice
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -1250,6 +1301,7 @@ extern "C" int th_gemm(const th_gemm_desc* d, void* stream) {
     k.extra_dtype[e] = d->extra_dtype[e];
     const int eb = d->extra_dtype[e] == TH_F32 ? 16 : 8;
     k.extra_vec[e] = aligned(d->extra[e], eb) && d->ld_extra[e] % 4 == 0;
+    k.extra_vec8[e] = aligned(d->extra[e], 16) && d->ld_extra[e] % (d->extra_dtype[e] == TH_F32 ? 4 : 8) == 0;
   }
   bool need_rope = false;
   for (int o = 0; o < d->n_out; ++o) {
@@ -1272,6 +1324,7 @@ extern "C" int th_gemm(const th_gemm_desc* d, void* stream) {
     k.out[o].dtype = eo.dtype;
     const int ob = eo.dtype == TH_F32 ? 16 : 8;
     k.out[o].vec = aligned(eo.ptr, ob) && eo.ld % 4 == 0;
+    k.out[o].vec8 = aligned(eo.ptr, 16) && eo.ld % (eo.dtype == TH_F32 ? 4 : 8) == 0;
     if (eo.op == TH_EPI_ROPE) {
       TH_CHECK_ARG(d->rope_head_dim > 0 && bn % d->rope_head_dim == 0,
                    "th_gemm: fused RoPE needs the column tile (%d) to hold whole heads (head_dim %d)", bn,

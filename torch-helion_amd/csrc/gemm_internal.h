@@ -9,7 +9,8 @@ struct EpiOutK {
   int op, a, b, e;
   void* ptr;
   int64_t ld;
-  int dtype, vec;
+  int dtype, vec;  // vec: 4-element vector access possible
+  int vec8;        // 8-element (16-byte bf16 / 2 x 16-byte fp32) access possible
 };
 
 struct GemmK {
@@ -27,6 +28,7 @@ struct GemmK {
   int64_t ld_extra[TH_MAX_EXTRA];
   int extra_dtype[TH_MAX_EXTRA];
   int extra_vec[TH_MAX_EXTRA];
+  int extra_vec8[TH_MAX_EXTRA];
   const float* rcos;
   const float* rsin;
   int hd, period;

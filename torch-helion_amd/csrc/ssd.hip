@@ -974,12 +974,22 @@ extern "C" int th_conv1d_causal(const th_conv_desc* d, void* stream) {
   const bool vec = k.K == 4 && k.xdt == TH_BF16 && k.W % 8 == 0 && k.ldx % 8 == 0 && k.ldy % 8 == 0 &&
                    (!k.y32 || k.ldy32 % 4 == 0) && al16(k.x) && al16(k.y) && al16(k.y32);
   if (vec) {
-    constexpr int TT = 16;
+    // the longest token run (fewest halo re-reads) that still gives about two
+    // 256-thread blocks per CU; small problems take short runs
     const int cg = k.W / 8;
-    const int runs = (int)cdiv(k.S, TT);
-    const int64_t threads = (int64_t)cg * k.B * runs;
-    hipLaunchKernelGGL((conv1d_vec_kernel<4, TT>), dim3((unsigned)cdiv(threads, 256)), dim3(256), 0,
-                       (hipStream_t)stream, k, cg, runs);
+    const int64_t want = (int64_t)std::max(device_cus(), 1) * 512;
+    int tt = 16;
+    while (tt > 1 && (int64_t)cg * k.B * cdiv(k.S, tt) < want) tt >>= 1;
+    const int runs = (int)cdiv(k.S, tt);
+    const dim3 grid((unsigned)cdiv((int64_t)cg * k.B * runs, 256));
+    hipStream_t st = (hipStream_t)stream;
+    switch (tt) {
+      case 16: hipLaunchKernelGGL((conv1d_vec_kernel<4, 16>), grid, dim3(256), 0, st, k, cg, runs); break;
+      case 8: hipLaunchKernelGGL((conv1d_vec_kernel<4, 8>), grid, dim3(256), 0, st, k, cg, runs); break;
+      case 4: hipLaunchKernelGGL((conv1d_vec_kernel<4, 4>), grid, dim3(256), 0, st, k, cg, runs); break;
+      case 2: hipLaunchKernelGGL((conv1d_vec_kernel<4, 2>), grid, dim3(256), 0, st, k, cg, runs); break;
+      default: hipLaunchKernelGGL((conv1d_vec_kernel<4, 1>), grid, dim3(256), 0, st, k, cg, runs); break;
+    }
   } else {
     hipLaunchKernelGGL(conv1d_causal_kernel, dim3((unsigned)((int64_t)k.B * k.S), (unsigned)cdiv(k.W, 256)), dim3(256),
                        0, (hipStream_t)stream, k);
