@@ -32,6 +32,11 @@ sys.path.insert(0, str(REPO))
 
 METRIC = "µs per block fwd (Llama-8B block, Mamba-2 layer); % of MFMA/HBM roofline"
 
+# HBM bytes per launch of the C3 gate/up kernel (k4_gemm), from rocprofv3 --pmc passes:
+# FETCH_SIZE 2,752,830 KiB x 2.0 (the counter reads half of a calibrated 1 GiB copy's
+# fetch) + WRITE_SIZE 458,752 KiB x 1.0 (profiles/llama_c3_gateup_traffic.md).
+C3_K4_TRAFFIC_BYTES = (2752830 * 2.0 + 458752 * 1.0) * 1024
+
 
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
@@ -265,8 +270,8 @@ def main() -> int:
     dom_name, dom = max(b["kernels"].items(), key=lambda kv: kv[1]["us"])
     if dom["bound"] == "mfma":
         roof = {"bound": "mfma", "achieved": dom["achieved_tflops"], "peak": dom["peak_tflops"], "unit": "TFLOP/s",
-                "frac": dom["frac"], "traffic": None, "kernel": dom_name, "kernel_us": dom["us"],
-                "algorithmic_flops": dom["flops"]}
+                "frac": dom["frac"], "traffic": C3_K4_TRAFFIC_BYTES if dom_name == "k4_gemm" else None,
+                "kernel": dom_name, "kernel_us": dom["us"], "algorithmic_flops": dom["flops"]}
     else:
         roof = {"bound": "hbm", "achieved": dom["achieved_gbs"], "peak": dom["peak_gbs"], "unit": "GB/s",
                 "frac": dom["frac"], "traffic": None, "kernel": dom_name, "kernel_us": dom["us"],
