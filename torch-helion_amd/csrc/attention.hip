@@ -28,7 +28,7 @@ struct AttnK {
 };
 
 template <int D>
-__global__ void __launch_bounds__(256, 1) attn_fwd_bf16_kernel(AttnK p) {
+__global__ void __launch_bounds__(256, 2) attn_fwd_bf16_kernel(AttnK p) {
   constexpr int BQ = 128, BKV = 64;
   constexpr int KCH = D / 8;             // 16-byte chunks per K row
   constexpr int KROW = D * 2;            // bytes per K row in LDS
@@ -157,40 +157,52 @@ __global__ void __launch_bounds__(256, 1) attn_fwd_bf16_kernel(AttnK p) {
           s[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[ks], s[t], 0, 0, 0);
         }
       }
-      // scale, mask, online softmax (per query column)
+      // Online softmax per query column on raw scores; c = scale * log2(e) > 0 is
+      // folded into the exponent, exp2(s c - m). The running max m moves only when
+      // a tile's max exceeds it by more than 8 (log2 units): probabilities stay
+      // below 2^8 and the O rescale is skipped while no lane of the wave moves.
+      const float c = p.scale_log2;
       const bool need_mask = (k0 + BKV > p.Skv) || (p.causal && k0 + BKV - 1 > q0w + p.off);
       float mloc = -INFINITY;
+      if (need_mask) {
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
+        for (int t = 0; t < 2; ++t)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          float x = s[t][r] * p.scale_log2;
-          if (need_mask) {
+          for (int r = 0; r < 16; ++r) {
             const int kv = k0 + 32 * t + 8 * (r >> 2) + 4 * hl + (r & 3);
-            if (kv >= p.Skv || (p.causal && kv > qrow + p.off)) x = -INFINITY;
+            if (kv >= p.Skv || (p.causal && kv > qrow + p.off)) s[t][r] = -INFINITY;
+            mloc = fmaxf(mloc, s[t][r]);
           }
-          s[t][r] = x;
-          mloc = fmaxf(mloc, x);
-        }
-      mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
-      const float m_new = fmaxf(m_run, mloc);
-      const float m_use = m_new == -INFINITY ? 0.f : m_new;
-      const float alpha = exp2f(m_run - m_use);
-      m_run = m_new;
+      } else {
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) mloc = fmaxf(mloc, s[t][r]);
+      }
+      mloc = fmaxf(mloc, __shfl_xor(mloc, 32)) * c;
+      const bool move = mloc > m_run + 8.f;
+      float alpha = 1.f;
+      if (move) {
+        alpha = __builtin_amdgcn_exp2f(m_run - mloc);
+        m_run = mloc;
+      }
+      const float nm = m_run == -INFINITY ? 0.f : -m_run;
       float lsum = 0.f;
 #pragma unroll
       for (int t = 0; t < 2; ++t)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const float e = exp2f(s[t][r] - m_use);
+          const float e = __builtin_amdgcn_exp2f(fmaf(s[t][r], c, nm));
           s[t][r] = e;
           lsum += e;
         }
       l_run = l_run * alpha + lsum;
+      if (__any(move)) {
 #pragma unroll
-      for (int t = 0; t < NDT; ++t)
+        for (int t = 0; t < NDT; ++t)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) oacc[t][r] *= alpha;
+          for (int r = 0; r < 16; ++r) oacc[t][r] *= alpha;
+      }
       // O^T += V^T P^T over 4 k steps of 16 keys
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
@@ -301,6 +313,8 @@ extern "C" int th_attention_prefill(const th_attn_desc* d, void* stream) {
                d->heads_q, d->heads_kv);
   TH_CHECK_ARG(d->q && d->k && d->v && d->o, "th_attention_prefill: null tensor pointer");
   TH_CHECK_ARG(d->dtype == TH_BF16 || d->dtype == TH_F32, "th_attention_prefill: dtype %d unsupported", d->dtype);
+  TH_CHECK_ARG(d->dtype != TH_BF16 || d->scale > 0.f, "th_attention_prefill: bf16 kernel needs scale > 0 (got %g)",
+               (double)d->scale);
   const int hd = d->head_dim;
   TH_CHECK_ARG(hd == 64 || hd == 128 || (d->dtype == TH_F32 && (hd == 32 || hd == 16)),
                "th_attention_prefill: head_dim %d unsupported", hd);
