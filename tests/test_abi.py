@@ -136,6 +136,9 @@ def test_attention_rejects_bad_heads(lib):
     d.heads_q, d.head_dim = 4, 96
     assert lib.th_attention_prefill(C.byref(d), None) == abi.TH_ERR_INVALID
     assert "head_dim" in abi.last_error(lib)
+    d.head_dim, d.scale = 64, -0.125  # the bf16 kernel folds a positive scale into exp2
+    assert lib.th_attention_prefill(C.byref(d), None) == abi.TH_ERR_INVALID
+    assert "scale > 0" in abi.last_error(lib)
 
 
 def test_valid_descriptor_without_init_stops_before_the_device(lib):

@@ -313,8 +313,6 @@ extern "C" int th_attention_prefill(const th_attn_desc* d, void* stream) {
                d->heads_q, d->heads_kv);
   TH_CHECK_ARG(d->q && d->k && d->v && d->o, "th_attention_prefill: null tensor pointer");
   TH_CHECK_ARG(d->dtype == TH_BF16 || d->dtype == TH_F32, "th_attention_prefill: dtype %d unsupported", d->dtype);
-  TH_CHECK_ARG(d->dtype != TH_BF16 || d->scale > 0.f, "th_attention_prefill: bf16 kernel needs scale > 0 (got %g)",
-               (double)d->scale);
   const int hd = d->head_dim;
   TH_CHECK_ARG(hd == 64 || hd == 128 || (d->dtype == TH_F32 && (hd == 32 || hd == 16)),
                "th_attention_prefill: head_dim %d unsupported", hd);
@@ -327,6 +325,8 @@ extern "C" int th_attention_prefill(const th_attn_desc* d, void* stream) {
     TH_CHECK_ARG(((uintptr_t)d->q | (uintptr_t)d->k | (uintptr_t)d->v) % 16 == 0 && (uintptr_t)d->o % 8 == 0,
                  "th_attention_prefill: tensors must be 16-byte aligned");
   }
+  TH_CHECK_ARG(d->dtype != TH_BF16 || d->scale > 0.f, "th_attention_prefill: bf16 kernel needs scale > 0 (got %g)",
+               (double)d->scale);
   if (!device_ready()) {
     set_error("th_attention_prefill: th_init was not called for the current device");
     return TH_ERR_NOT_INIT;
