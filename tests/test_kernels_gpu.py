@@ -181,6 +181,41 @@ def test_gemm_rope_whole_heads_per_wave(gpu, hd, n_acc):
         assert _maxabs(o16[i], ref) < BF16_TOL, i
 
 
+@pytest.mark.parametrize("S", [512, 2048])
+def test_gemm_kv_rope_head_wider_than_half_tile(gpu, S):
+    """k and v projections in one launch (two accumulators, 128-column tiles) with RoPE on k at head_dim 128:
+    a head spans both column halves of the tile, so each wave holds one whole accumulator instead. M = 8 S
+    rows selects 128-row (S=512) and 256-row (S=2048) persistent tiles. RMS fold on both accumulators."""
+    from torch_helion.hip import abi, ops
+
+    B, Hkv, hd, K, eps = 8, 8, 128, 512, 1e-5
+    M, N = B * S, Hkv * hd
+    announce(f"gemm bf16 kv rope M={M} N={N} hd={hd}")
+    g = torch.Generator().manual_seed(S)
+    x = torch.randn(M, K, generator=g).bfloat16()
+    wk, wv = [(torch.randn(K, N, generator=g) * 0.05).bfloat16() for _ in range(2)]
+    cos, sin = _rope_tables(S, hd, theta=500000.0)
+    xf = x.float()
+    r = ((xf * xf).sum(-1, keepdim=True) / K + eps).pow(-0.5)
+    k_acc, v_ref = (xf @ wk.float()) * r, (xf @ wv.float()) * r
+    k_ref = k_acc * cos.repeat(B, Hkv) + _rot_heads(k_acc, hd) * sin.repeat(B, Hkv)
+    xd = x.to(gpu)
+    packed = ops.pack_rhs([wk.to(gpu), wv.to(gpu)], torch.bfloat16)
+    ok, ov = [torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=gpu) for _ in range(2)]
+    ok32 = torch.full((M, N), float("nan"), device=gpu)
+    ss = torch.full((M,), float("nan"), device=gpu)
+    ops.gemm(ops.GemmCall(M, N, K, 2, xd, packed, [ops.EpiSpec(abi.EPI_ROPE, ok, a=0), ops.EpiSpec(abi.EPI_ACC, ov, a=1),
+                                                    ops.EpiSpec(abi.EPI_ROPE, ok32, a=0)],
+                          sumsq=True, rscale_mask=0b11, inv_k=1.0 / K, eps=eps, sumsq_out=ss,
+                          rope_cos=cos.to(gpu).contiguous(), rope_sin=sin.to(gpu).contiguous(), rope_head_dim=hd,
+                          rope_period=S))
+    torch.cuda.synchronize()
+    assert _rel(ok32, k_ref) < 1e-5
+    assert _maxabs(ok, k_ref) < BF16_TOL
+    assert _maxabs(ov, v_ref) < BF16_TOL
+    assert _rel(ss, (xf * xf).sum(-1)) < 1e-5
+
+
 def _quant_e4m3(w: torch.Tensor):
     """Per-output-channel e4m3: s_n = max|W[:, n]| / 448, q = e4m3(W / s_n)."""
     s = (w.abs().amax(0).clamp_min(1e-12) / 448.0).float()

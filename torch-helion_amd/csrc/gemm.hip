@@ -130,10 +130,11 @@ __device__ __forceinline__ void store8(void* p, int64_t off, int dtype, bool vec
 // octets per row) of rows r_l + pass * rp, pass < np. The op is a template
 // argument, so each output runs one straight loop; every global operand of
 // the slice (extra rows, RoPE table rows) is loaded before the first use.
+// aoff / boff: slice columns where the op's accumulators a / b start.
 template <int OP, bool SUMSQ>
-__device__ __forceinline__ void epi_slice(const GemmK& p, const EpiOutK& eo, const float* wsl, int ws, int hbn,
-                                          const float* rsrow, int64_t row0, int64_t col_w, int r_l, int c8, int np,
-                                          int rp) {
+__device__ __forceinline__ void epi_slice(const GemmK& p, const EpiOutK& eo, const float* wsl, int ws, int aoff,
+                                          int boff, const float* rsrow, int64_t row0, int64_t col_w, int r_l, int c8,
+                                          int np, int rp) {
   constexpr bool USES_E = OP == TH_EPI_ADD || OP == TH_EPI_SOFTPLUS_ADD || OP == TH_EPI_MUL;
   constexpr bool USES_T = OP == TH_EPI_ROPE || OP == TH_EPI_ROPE_PAIR;
   const int ia = eo.a, ib = eo.b;
@@ -171,7 +172,7 @@ __device__ __forceinline__ void epi_slice(const GemmK& p, const EpiOutK& eo, con
     const float* srow = wsl + r16 * ws;
     float a[8], v[8];
     {
-      const float4 a0 = *(const float4*)(srow + ia * hbn + c8), a1 = *(const float4*)(srow + ia * hbn + c8 + 4);
+      const float4 a0 = *(const float4*)(srow + aoff + c8), a1 = *(const float4*)(srow + aoff + c8 + 4);
       a[0] = a0.x; a[1] = a0.y; a[2] = a0.z; a[3] = a0.w; a[4] = a1.x; a[5] = a1.y; a[6] = a1.z; a[7] = a1.w;
     }
     if (sa) {
@@ -185,7 +186,7 @@ __device__ __forceinline__ void epi_slice(const GemmK& p, const EpiOutK& eo, con
 #pragma unroll
       for (int i = 0; i < 8; ++i) v[i] = a[i] * sigmoidf_(a[i]);
     } else if constexpr (OP == TH_EPI_SWIGLU) {
-      const float4 b0 = *(const float4*)(srow + ib * hbn + c8), b1 = *(const float4*)(srow + ib * hbn + c8 + 4);
+      const float4 b0 = *(const float4*)(srow + boff + c8), b1 = *(const float4*)(srow + boff + c8 + 4);
       float bb[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
 #pragma unroll
       for (int i = 0; i < 8; ++i) v[i] = a[i] * sigmoidf_(a[i]) * (sb ? bb[i] * rr : bb[i]);
@@ -199,12 +200,12 @@ __device__ __forceinline__ void epi_slice(const GemmK& p, const EpiOutK& eo, con
           const int within = (int)((gn + 4 * q) % p.hd);
           const int pc = within < half ? c8 + 4 * q + half : c8 + 4 * q - half;
           const float sg = within < half ? -1.f : 1.f;
-          const float4 r4 = *(const float4*)(srow + ia * hbn + pc);
+          const float4 r4 = *(const float4*)(srow + aoff + pc);
           const float s2 = sa ? sg * rr : sg;
           rot[4 * q] = r4.x * s2; rot[4 * q + 1] = r4.y * s2; rot[4 * q + 2] = r4.z * s2; rot[4 * q + 3] = r4.w * s2;
         }
       } else {
-        const float4 b0 = *(const float4*)(srow + ib * hbn + c8), b1 = *(const float4*)(srow + ib * hbn + c8 + 4);
+        const float4 b0 = *(const float4*)(srow + boff + c8), b1 = *(const float4*)(srow + boff + c8 + 4);
         const float bb[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
 #pragma unroll
         for (int i = 0; i < 8; ++i) rot[i] = sb ? bb[i] * rr : bb[i];
@@ -474,8 +475,10 @@ __global__ void __launch_bounds__(256, 1) gemm_bf16_kernel(GemmK p) {
 
 // ------------------------------------------------- bf16 MFMA, direct-to-LDS
 // Same tiling and epilogue as gemm_bf16_kernel, with the operand tiles
-// streamed from HBM straight into LDS by buffer_load_dwordx4 ... lds (gfx950):
-// no staging VGPRs and no ds_write. Requires K % 64 == 0.
+// streamed from HBM straight into LDS by global_load_lds_dwordx4 (gfx950):
+// no staging VGPRs and no ds_write. Requires K % 64 == 0. (A wave issues the
+// global form about 1.5x as fast as buffer_load ... lds, measured: one 1 KB
+// load per ~80 cycles against ~120.)
 //
 // LDS layout: row R of a tile holds its 8 16-byte K chunks with chunk c in
 // slot c ^ g(R), g(R) = (R & 7) ^ ((R >> 3) & 1). An MFMA fragment read (32
@@ -484,9 +487,8 @@ __global__ void __launch_bounds__(256, 1) gemm_bf16_kernel(GemmK p) {
 // 8 lanes (32 banks): no bank conflicts under either service pattern.
 // LDS fill: the wave's i-th load of a tile writes 1 KB = LDS rows
 // 32*i + 8*wave .. +8 (128 bytes each); lane l lands in row +l/8, slot l%8, so
-// it fetches global chunk (l%8) ^ g(row) = (l%8) ^ (l/8) ^ (wave&1). Out-of-range
-// rows of A read as zero (the buffer descriptor ends at the block's last valid
-// row).
+// it fetches global chunk (l%8) ^ g(row) = (l%8) ^ (l/8) ^ (wave&1). Rows of A
+// past M re-read row M-1: in bounds, and the epilogue stores no row past M.
 //
 // Pipeline (2 stages): the loads of tile kt+1 are in flight during tile kt.
 // Within a tile the fragments of step ks+1 are read from LDS while the MFMAs of
@@ -495,10 +497,6 @@ __global__ void __launch_bounds__(256, 1) gemm_bf16_kernel(GemmK p) {
 // the stage everyone has just finished reading.
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
-  // word 3 = 0x00020000: raw 32-bit data format, the gfx9 default for untyped buffer access
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
-}
 
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
@@ -520,7 +518,7 @@ __device__ __forceinline__ void wait_tiles(int n) {
 
 template <int BM, int BNC, bool SUMSQ, int STAGES>
 __global__ void __launch_bounds__(256, 1) gemm_bf16_dl_kernel(GemmK p) {
-#if defined(__HIP_DEVICE_COMPILE__)  // the buffer-resource type exists only in the device pass
+#if defined(__HIP_DEVICE_COMPILE__)  // gfx950 LDS-load builtins exist only in the device pass
   constexpr int WM = BM / 2, WN = BNC / 2;
   constexpr int TM = WM / 32, TN = WN / 32;
   constexpr int LA = BM / 32, LB = BNC / 32;  // 1 KB loads per wave per tile
@@ -540,17 +538,16 @@ __global__ void __launch_bounds__(256, 1) gemm_bf16_dl_kernel(GemmK p) {
   int tmi, tni;
   map_tile(p.tiles_m, p.tiles_n, tmi, tni);
   const int64_t m0 = (int64_t)tmi * BM;
-  const int64_t arows = min((int64_t)BM, p.M - m0);
-  const __amdgpu_buffer_rsrc_t rsa = make_rsrc((const uint16_t*)p.A + m0 * p.lda, (uint32_t)(arows * p.lda * 2));
-  const __amdgpu_buffer_rsrc_t rsb =
-      make_rsrc((const uint16_t*)p.B + (int64_t)tni * BNC * p.ldb, (uint32_t)(BNC * p.ldb * 2));
-  // Per-lane byte offsets of each load's row (VGPR offsets, so the descriptor's
-  // range check sees the row); the K position goes in the scalar offset.
+  const int arows = (int)min((int64_t)BM, p.M - m0);
+  // Uniform base pointers plus per-lane 32-bit byte offsets of each load's row;
+  // lhs rows past M re-read row M-1 (in bounds; their results are never stored).
+  const char* ga = (const char*)p.A + m0 * p.lda * 2;
+  const char* gb = (const char*)p.B + (int64_t)tni * BNC * p.ldb * 2;
   const int lrow = lane >> 3;
   const uint32_t chunk = (uint32_t)(((lane & 7) ^ lrow ^ (wave & 1)) << 4);
   uint32_t voa[LA], vob[LB];
 #pragma unroll
-  for (int i = 0; i < LA; ++i) voa[i] = (uint32_t)((32 * i + 8 * wave + lrow) * p.lda * 2) + chunk;
+  for (int i = 0; i < LA; ++i) voa[i] = (uint32_t)(min(32 * i + 8 * wave + lrow, arows - 1) * p.lda * 2) + chunk;
 #pragma unroll
   for (int i = 0; i < LB; ++i) vob[i] = (uint32_t)((32 * i + 8 * wave + lrow) * p.ldb * 2) + chunk;
   const int nk = (int)(p.K / 64);
@@ -558,13 +555,13 @@ __global__ void __launch_bounds__(256, 1) gemm_bf16_dl_kernel(GemmK p) {
   auto issue_tile = [&](int kt, int st) {
     char* sa = smem + st * STAGE;
     char* sb = sa + BM * 128;
-    const uint32_t kofs = (uint32_t)kt * 128;
+    const int64_t kofs = (int64_t)kt * 128;
 #pragma unroll
     for (int i = 0; i < LA; ++i)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, (lds_ptr_t)(sa + (4 * i + wave) * 1024), 16, voa[i], kofs, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void*)(ga + kofs + voa[i]), (lds_ptr_t)(sa + (4 * i + wave) * 1024), 16, 0, 0);
 #pragma unroll
     for (int i = 0; i < LB; ++i)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsb, (lds_ptr_t)(sb + (4 * i + wave) * 1024), 16, vob[i], kofs, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void*)(gb + kofs + vob[i]), (lds_ptr_t)(sb + (4 * i + wave) * 1024), 16, 0, 0);
   };
 
   bf16x8_t fa[2][TM], fb[2][TN];
@@ -694,24 +691,44 @@ __global__ void __launch_bounds__(256, 1) gemm_bf16_dl_kernel(GemmK p) {
 // through a private slice of LDS stage 1 and writes 4 consecutive columns per
 // lane. Before the epilogue starts, the next tile's first K tile is already
 // streaming into stage 0, so its latency hides behind the epilogue.
-template <int BM, int BNC, bool SUMSQ>
-__global__ void __launch_bounds__(256, 1) gemm_bf16_pk_kernel(GemmK p) {
-#if defined(__HIP_DEVICE_COMPILE__)  // the buffer-resource type exists only in the device pass
-  constexpr int WM = BM / 2, WN = BNC / 2;
+//
+// NW = 8 waves (two per SIMD, at most 256 registers each) split the rows in
+// four: each wave holds 64 rows of its column half. A wave issues one global
+// load per ~120 cycles whatever its width, and in order, so with one wave per
+// SIMD the loads of a K tile hold back that SIMD's MFMAs; with two, one wave
+// issues MFMAs while the other waits on its loads.
+// NACC (the number of accumulators, p.n_acc) is a template argument so that
+// every fragment's LDS row offset is a constant and the address registers of
+// the main loop stay few.
+// ASPLIT (two accumulators): wave column half wn holds all bn columns of
+// accumulator wn instead, so a RoPE head as wide as bn stays in one wave; every
+// output then reads one accumulator and is written by the waves that hold it.
+template <int BM, int BNC, bool SUMSQ, int NW, int NACC, bool ASPLIT = false>
+__global__ void __launch_bounds__(64 * NW, 1) gemm_bf16_pk_kernel(GemmK p) {
+#if defined(__HIP_DEVICE_COMPILE__)  // gfx950 LDS-load builtins exist only in the device pass
+  static_assert(NW == 4 || NW == 8, "4 or 8 waves");
+  constexpr int WM = BM / (NW / 2), WN = BNC / 2;
   constexpr int TM = WM / 32, TN = WN / 32;
-  constexpr int LA = BM / 32, LB = BNC / 32;
+  constexpr int LR = 8 * NW;                 // rows covered by one load of every wave
+  constexpr int LA = BM / LR, LB = BNC / LR;  // 1 KB loads per wave per K tile
+  static_assert(LA * LR == BM && LB * LR == BNC, "tile rows must be a multiple of 8 per wave");
   constexpr int STAGE = (BM + BNC) * 128;
   constexpr int NMF = TM * TN;
+  constexpr int NLD = LA + LB, HLD = NLD / 2;  // loads per K tile; the first HLD go out with step 3
   constexpr int WS = WN + 8;                 // epilogue slice row stride (floats)
   constexpr int SLICE = 16 * WS * 4;         // bytes per wave: 16 rows
-  static_assert(4 * SLICE <= STAGE, "epilogue slices must fit in one stage");
-  __shared__ __attribute__((aligned(16))) char smem[2 * STAGE + BM * 4];
-  float* rsx = (float*)(smem + 2 * STAGE);  // row scales of the current tile
+  // the slices start at stage 1 (free while the next tile's K tile 0 streams into stage 0)
+  constexpr int BODY = STAGE + NW * SLICE > 2 * STAGE ? STAGE + NW * SLICE : 2 * STAGE;
+  __shared__ __attribute__((aligned(16))) char smem[BODY + BM * 4];
+  float* rsx = (float*)(smem + BODY);  // row scales of the current tile
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
-  const int n_acc = p.n_acc, bn = p.bn, hbn = bn >> 1;
+  constexpr int n_acc = NACC, bn = BNC / NACC, hbn = bn >> 1;
+  static_assert(bn * NACC == BNC && hbn % 32 == 0, "column tile per accumulator");
+  static_assert(!ASPLIT || NACC == 2, "the accumulator split needs two accumulators");
+  constexpr int wcols = ASPLIT ? bn : hbn;  // columns of one accumulator held by a wave
   const int tiles = p.tiles_m * p.tiles_n;
   const int nk = (int)(p.K / 64);
 
@@ -719,41 +736,65 @@ __global__ void __launch_bounds__(256, 1) gemm_bf16_pk_kernel(GemmK p) {
   int brow[TN], lcol[TN];
 #pragma unroll
   for (int u = 0; u < TN; ++u) {
-    const int a = u % n_acc, c32 = u / n_acc;
-    brow[u] = a * bn + wn * hbn + c32 * 32 + (lane & 31);
-    lcol[u] = a * hbn + c32 * 32;
+    if constexpr (ASPLIT) {
+      brow[u] = wn * bn + u * 32 + (lane & 31);
+      lcol[u] = u * 32;
+    } else {
+      const int a = u % n_acc, c32 = u / n_acc;
+      brow[u] = a * bn + wn * hbn + c32 * 32 + (lane & 31);
+      lcol[u] = a * hbn + c32 * 32;
+    }
   }
 
+  // Load i of a wave fills LDS rows LR*i + 8*wave .. +8 (1 KB); row R's chunk
+  // slot is c ^ g(R) with g(R) = (R & 7) ^ ((R >> 3) & 1) = (lane >> 3) ^ (wave & 1).
   const int lrow = lane >> 3;
   const uint32_t chunk = (uint32_t)(((lane & 7) ^ lrow ^ (wave & 1)) << 4);
   uint32_t voa[LA], vob[LB];
 #pragma unroll
-  for (int i = 0; i < LA; ++i) voa[i] = (uint32_t)((32 * i + 8 * wave + lrow) * p.lda * 2) + chunk;
+  for (int i = 0; i < LA; ++i) voa[i] = (uint32_t)((LR * i + 8 * wave + lrow) * p.lda * 2) + chunk;
 #pragma unroll
-  for (int i = 0; i < LB; ++i) vob[i] = (uint32_t)((32 * i + 8 * wave + lrow) * p.ldb * 2) + chunk;
+  for (int i = 0; i < LB; ++i) vob[i] = (uint32_t)((LR * i + 8 * wave + lrow) * p.ldb * 2) + chunk;
 
-  auto tile_rsrc = [&](int L, int& tm, int& tn, __amdgpu_buffer_rsrc_t& ra, __amdgpu_buffer_rsrc_t& rb) {
+  // Operand rows of tile L: uniform base pointers (lhs rows m0.., rhs rows
+  // tn*BNC..) plus the per-lane 32-bit offsets above. lhs rows past M re-read
+  // row M-1, which is in bounds; their results are never stored. The offsets
+  // of a new tile are set only after every load of the previous one landed.
+  auto tile_rsrc = [&](int L, int& tm, int& tn, const char*& ga, const char*& gb) {
     map_tile_id(L, p.tiles_m, p.tiles_n, tm, tn);
     const int64_t m0 = (int64_t)tm * BM;
-    const int64_t arows = min((int64_t)BM, p.M - m0);
-    ra = make_rsrc((const uint16_t*)p.A + m0 * p.lda, (uint32_t)(arows * p.lda * 2));
-    rb = make_rsrc((const uint16_t*)p.B + (int64_t)tn * BNC * p.ldb, (uint32_t)(BNC * p.ldb * 2));
+    const int arows = (int)min((int64_t)BM, p.M - m0);
+    ga = (const char*)p.A + m0 * p.lda * 2;
+    gb = (const char*)p.B + (int64_t)tn * BNC * p.ldb * 2;
+#pragma unroll
+    for (int i = 0; i < LA; ++i) voa[i] = (uint32_t)(min(LR * i + 8 * wave + lrow, arows - 1) * p.lda * 2) + chunk;
   };
-  auto issue_tile = [&](const __amdgpu_buffer_rsrc_t& ra, const __amdgpu_buffer_rsrc_t& rb, int kt, int st) {
+  // Load i of K tile kt into stage st: i < LA fills lhs rows, the rest rhs
+  // rows. global_load_lds: a wave issues these about 1.5x as fast as the
+  // buffer-descriptor form.
+  auto issue_one = [&](const char* ga, const char* gb, int kt, int st, int i) {
     char* sa = smem + st * STAGE;
-    char* sb = sa + BM * 128;
-    const uint32_t kofs = (uint32_t)kt * 128;
+    const int64_t kofs = (int64_t)kt * 128;
+    if (i < LA)
+      __builtin_amdgcn_global_load_lds((const void*)(ga + kofs + voa[i < LA ? i : 0]),
+                                       (lds_ptr_t)(sa + (NW * i + wave) * 1024), 16, 0, 0);
+    else
+      __builtin_amdgcn_global_load_lds((const void*)(gb + kofs + vob[i >= LA ? i - LA : 0]),
+                                       (lds_ptr_t)(sa + BM * 128 + (NW * (i - LA) + wave) * 1024), 16, 0, 0);
+  };
+  auto issue_tile = [&](const char* ga, const char* gb, int kt, int st) {
 #pragma unroll
-    for (int i = 0; i < LA; ++i)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr_t)(sa + (4 * i + wave) * 1024), 16, voa[i], kofs, 0, 0);
+    for (int i = 0; i < NLD; ++i) issue_one(ga, gb, kt, st, i);
+  };
+  auto issue_half = [&](const char* ga, const char* gb, int kt, int st) {
 #pragma unroll
-    for (int i = 0; i < LB; ++i)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_ptr_t)(sb + (4 * i + wave) * 1024), 16, vob[i], kofs, 0, 0);
+    for (int i = 0; i < HLD; ++i) issue_one(ga, gb, kt, st, i);
   };
 
   bf16x8_t fa[2][TM], fb[2][TN];
   f32x16_t acc[TM][TN];
-  float ss[TM];
+  static_assert(TM % 2 == 0, "the two column-half waves split the 32-row groups");
+  float ss[TM / 2];  // ss[j]: row group t = 2j + wn
   auto read_frags = [&](int st, int ks, int slot) {
     const char* sa = smem + st * STAGE;
     const char* sb = sa + BM * 128;
@@ -771,44 +812,67 @@ __global__ void __launch_bounds__(256, 1) gemm_bf16_pk_kernel(GemmK p) {
       acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[slot][t], fb[slot][u], acc[t][u], 0, 0, 0);
     }
   };
+  // MFMAs lo .. hi with loads l0 .. l1 of K tile kt (into stage st) spread
+  // evenly between them, in this order: a wave issues in order, so a burst of
+  // loads would hold back the MFMAs behind it until the load queue drains.
+  auto mfmas_ld = [&](int slot, int lo, int hi, const char* ra, const char* rb, int kt, int st, int l0, int l1) {
+#pragma unroll
+    for (int i = 0; i < NMF; ++i) {
+      if (i < lo || i >= hi) continue;
+      const int t = i / TN, u = i % TN;
+      acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[slot][t], fb[slot][u], acc[t][u], 0, 0, 0);
+#pragma unroll
+      for (int j = 0; j < NLD; ++j)
+        if (j >= l0 && j < l1 && (j - l0) * (hi - lo) / (l1 - l0) == i - lo) issue_one(ra, rb, kt, st, j);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
   // wave wn accumulates the row sums of squares of the 32-row groups t % 2 == wn
+  // (a select, not a branch, so the MFMA sequence stays one basic block)
   auto sumsq_frags = [&](int slot) {
     if constexpr (SUMSQ) {
 #pragma unroll
-      for (int t = 0; t < TM; ++t)
-        if ((t & 1) == wn) ss[t] = sumsq8_dot(fa[slot][t], ss[t]);
+      for (int j = 0; j < TM / 2; ++j) ss[j] = sumsq8_dot(wn ? fa[slot][2 * j + 1] : fa[slot][2 * j], ss[j]);
     }
   };
 
   int L = blockIdx.x;
   if (L >= tiles) return;
   int tmi, tni;
-  __amdgpu_buffer_rsrc_t rsa, rsb;
+  const char *rsa, *rsb;
   tile_rsrc(L, tmi, tni, rsa, rsb);
   issue_tile(rsa, rsb, 0, 0);
-  if (nk > 1) issue_tile(rsa, rsb, 1, 1);
+  if (nk > 1) issue_half(rsa, rsb, 1, 1);
 
   char* slice = smem + STAGE + wave * SLICE;
   float* wsl = (float*)slice;
 
   for (;;) {
-    // K tile 0 of tile L is in flight into stage 0 (and K tile 1 into stage 1)
+    // K tile 0 of tile L is in flight into stage 0 (and half of K tile 1 into stage 1)
     if (nk > 1)
-      wait_vmcnt<LA + LB>();
+      wait_vmcnt<HLD>();
     else
       wait_vmcnt<0>();
     __syncthreads();
     read_frags(0, 0, 0);
 #pragma unroll
+    for (int j = 0; j < TM / 2; ++j) ss[j] = 0.f;
+#pragma unroll
     for (int t = 0; t < TM; ++t) {
-      ss[t] = 0.f;
 #pragma unroll
       for (int u = 0; u < TN; ++u)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[t][u][r] = 0.f;
     }
 
-    for (int kt = 0; kt < nk; ++kt) {
+    // One K tile. K tile kt+2 goes into stage kt & 1 once every wave is past
+    // the barrier of tile kt: loads 0 .. HLD with the last MFMAs of tile kt, the
+    // rest with the first step of tile kt+1 (tile 1: its first half was issued
+    // with tile 0). Past the last K tile the first-half loads fetch tile nk-1
+    // again into the stage that is no longer read; the last tile issues nothing
+    // and has no successor. STEADY is compile-time: two straight-line bodies.
+    auto ktile = [&](int kt, auto steady) __attribute__((always_inline)) {
+      constexpr bool STEADY = decltype(steady)::value;
       const int st = kt & 1;
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
@@ -816,32 +880,38 @@ __global__ void __launch_bounds__(256, 1) gemm_bf16_pk_kernel(GemmK p) {
         if (ks < 3) {
           read_frags(st, ks + 1, slot ^ 1);
           __builtin_amdgcn_sched_barrier(0);
-          mfmas(slot, 0, NMF);
+          if (STEADY && ks == 0)
+            mfmas_ld(slot, 0, NMF, rsa, rsb, kt + 1, st ^ 1, HLD, NLD);
+          else
+            mfmas(slot, 0, NMF);
           sumsq_frags(slot);
           __builtin_amdgcn_sched_barrier(0);
         } else {
           mfmas(slot, 0, NMF / 2);
           __builtin_amdgcn_sched_barrier(0);
-          if (kt + 1 < nk) {
+          if constexpr (STEADY) {
             wait_vmcnt<0>();
             __syncthreads();
             read_frags(st ^ 1, 0, 0);
-            if (kt + 2 < nk) issue_tile(rsa, rsb, kt + 2, st);
+            __builtin_amdgcn_sched_barrier(0);
+            mfmas_ld(slot, NMF / 2, NMF, rsa, rsb, min(kt + 2, nk - 1), st, 0, HLD);
+          } else {
+            mfmas(slot, NMF / 2, NMF);
           }
-          __builtin_amdgcn_sched_barrier(0);
-          mfmas(slot, NMF / 2, NMF);
           sumsq_frags(slot);
           __builtin_amdgcn_sched_barrier(0);
         }
       }
-    }
+    };
+    for (int kt = 0; kt < nk - 1; ++kt) ktile(kt, std::true_type{});
+    ktile(nk - 1, std::false_type{});
 
     if constexpr (SUMSQ) {
 #pragma unroll
-      for (int t = 0; t < TM; ++t) {
-        const float v = ss[t] + __shfl_xor(ss[t], 32);
-        if ((t & 1) == wn && lane < 32) {
-          const int r = wm * WM + t * 32 + lane;
+      for (int j = 0; j < TM / 2; ++j) {
+        const float v = ss[j] + __shfl_xor(ss[j], 32);
+        if (lane < 32) {
+          const int r = wm * WM + (2 * j + wn) * 32 + lane;
           rsx[r] = rsqrtf(v * p.inv_k + p.eps);
           const int64_t gr = (int64_t)tmi * BM + r;
           if (p.sumsq_out && tni == 0 && gr < p.M) p.sumsq_out[gr] = v;
@@ -854,7 +924,7 @@ __global__ void __launch_bounds__(256, 1) gemm_bf16_pk_kernel(GemmK p) {
     const int Ln = L + (int)gridDim.x;
     const bool more = Ln < tiles;
     int tmn = 0, tnn = 0;
-    __amdgpu_buffer_rsrc_t rsan = rsa, rsbn = rsb;
+    const char *rsan = rsa, *rsbn = rsb;
     if (more) {
       tile_rsrc(Ln, tmn, tnn, rsan, rsbn);
       issue_tile(rsan, rsbn, 0, 0);
@@ -862,8 +932,9 @@ __global__ void __launch_bounds__(256, 1) gemm_bf16_pk_kernel(GemmK p) {
 
     // ---- epilogue of tile (tmi, tni), wave-private
     const int64_t row_w = (int64_t)tmi * BM + wm * WM;  // first row of this wave
-    const int64_t col_w = (int64_t)tni * bn + wn * hbn;  // first column of this wave (every accumulator)
-    const int qlog = __builtin_ctz((unsigned)(hbn >> 2));  // quads per row = hbn / 4
+    // first column of this wave (in every accumulator it holds)
+    const int64_t col_w = (int64_t)tni * bn + (ASPLIT ? 0 : wn * hbn);
+    const int qlog = __builtin_ctz((unsigned)(wcols >> 2));  // quads per row = wcols / 4
     // Rows 16*h .. +16 of the 32-row group t go through the slice. The copy out
     // of the accumulators is unrolled per (t, h) so every register index is a
     // constant; the read-back below is an ordinary loop.
@@ -898,13 +969,15 @@ __global__ void __launch_bounds__(256, 1) gemm_bf16_pk_kernel(GemmK p) {
 
         const int64_t row0 = row_w + t * 32 + h * 16;
         const float* rsrow = rsx + wm * WM + t * 32 + h * 16;
-        const int q8log = qlog - 1;  // octets per row = hbn / 8 (4, 8 or 16)
+        const int q8log = qlog - 1;  // octets per row = wcols / 8 (4, 8 or 16)
         const int r_l = lane >> q8log, c8 = (lane & ((1 << q8log) - 1)) << 3;
         const int np = 1 << (q8log - 2), rp = 64 >> q8log;
         for (int o = 0; o < p.n_out; ++o) {
           const EpiOutK& eo = p.out[o];
+          if (ASPLIT && eo.a != wn) continue;
+          const int aoff = ASPLIT ? 0 : eo.a * hbn, boff = ASPLIT ? 0 : eo.b * hbn;
 #define TH_EPI_CASE(OP_) \
-  case OP_: epi_slice<OP_, SUMSQ>(p, eo, wsl, WS, hbn, rsrow, row0, col_w, r_l, c8, np, rp); break
+  case OP_: epi_slice<OP_, SUMSQ>(p, eo, wsl, WS, aoff, boff, rsrow, row0, col_w, r_l, c8, np, rp); break
           switch (eo.op) {
             TH_EPI_CASE(TH_EPI_ACC);
             TH_EPI_CASE(TH_EPI_ROPE);
@@ -913,7 +986,7 @@ __global__ void __launch_bounds__(256, 1) gemm_bf16_pk_kernel(GemmK p) {
             TH_EPI_CASE(TH_EPI_SWIGLU);
             TH_EPI_CASE(TH_EPI_ADD);
             TH_EPI_CASE(TH_EPI_SOFTPLUS_ADD);
-            default: epi_slice<TH_EPI_MUL, SUMSQ>(p, eo, wsl, WS, hbn, rsrow, row0, col_w, r_l, c8, np, rp); break;
+            default: epi_slice<TH_EPI_MUL, SUMSQ>(p, eo, wsl, WS, aoff, boff, rsrow, row0, col_w, r_l, c8, np, rp); break;
           }
 #undef TH_EPI_CASE
         }
@@ -926,7 +999,7 @@ __global__ void __launch_bounds__(256, 1) gemm_bf16_pk_kernel(GemmK p) {
 
     __syncthreads();  // every wave is done with its stage-1 slice
     if (!more) break;
-    if (nk > 1) issue_tile(rsan, rsbn, 1, 1);
+    if (nk > 1) issue_half(rsan, rsbn, 1, 1);
     L = Ln;
     tmi = tmn;
     tni = tnn;
@@ -1144,6 +1217,16 @@ static int forced_main_loop() {
   return v;
 }
 
+// TH_GEMM_WAVES=4 keeps the 256-row persistent tiles on four waves per block
+// (one per SIMD); the default is eight.
+static int persistent_waves() {
+  static const int v = [] {
+    const char* e = getenv("TH_GEMM_WAVES");
+    return (e && e[0] == '4') ? 4 : 8;
+  }();
+  return v;
+}
+
 }  // namespace th
 
 using namespace th;
@@ -1231,10 +1314,49 @@ static void launch_bf16_pk(const GemmK& k, hipStream_t s) {
   const int tiles = k.tiles_m * k.tiles_n;
   const int cus = device_cus();
   const int grid = cus > 0 && tiles > cus ? cus : tiles;
-  if (k.sumsq)
-    hipLaunchKernelGGL((gemm_bf16_pk_kernel<BM, BNC, true>), dim3(grid), dim3(256), 0, s, k);
-  else
-    hipLaunchKernelGGL((gemm_bf16_pk_kernel<BM, BNC, false>), dim3(grid), dim3(256), 0, s, k);
+  const int nw = BM == 256 ? persistent_waves() : 4;
+  auto go = [&](auto nacc) {
+    constexpr int NA = decltype(nacc)::value;
+    if constexpr (BNC % NA == 0 && (BNC / NA / 2) % 32 == 0) {
+      constexpr int NW8 = BM == 256 ? 8 : 4;  // eight waves only for 256-row tiles
+      if constexpr (NA == 2) {
+        if (k.asplit) {
+          if (nw == 8) {
+            if (k.sumsq)
+              hipLaunchKernelGGL((gemm_bf16_pk_kernel<BM, BNC, true, NW8, 2, true>), dim3(grid), dim3(64 * NW8), 0, s, k);
+            else
+              hipLaunchKernelGGL((gemm_bf16_pk_kernel<BM, BNC, false, NW8, 2, true>), dim3(grid), dim3(64 * NW8), 0, s,
+                                 k);
+          } else {
+            if (k.sumsq)
+              hipLaunchKernelGGL((gemm_bf16_pk_kernel<BM, BNC, true, 4, 2, true>), dim3(grid), dim3(256), 0, s, k);
+            else
+              hipLaunchKernelGGL((gemm_bf16_pk_kernel<BM, BNC, false, 4, 2, true>), dim3(grid), dim3(256), 0, s, k);
+          }
+          return;
+        }
+      }
+      if (nw == 8) {
+        if (k.sumsq)
+          hipLaunchKernelGGL((gemm_bf16_pk_kernel<BM, BNC, true, NW8, NA>), dim3(grid), dim3(64 * NW8), 0, s, k);
+        else
+          hipLaunchKernelGGL((gemm_bf16_pk_kernel<BM, BNC, false, NW8, NA>), dim3(grid), dim3(64 * NW8), 0, s, k);
+      } else {
+        if (k.sumsq)
+          hipLaunchKernelGGL((gemm_bf16_pk_kernel<BM, BNC, true, 4, NA>), dim3(grid), dim3(256), 0, s, k);
+        else
+          hipLaunchKernelGGL((gemm_bf16_pk_kernel<BM, BNC, false, 4, NA>), dim3(grid), dim3(256), 0, s, k);
+      }
+    } else {
+      launch_bf16_dl<BM, BNC>(k, s);  // no per-wave split of this column tile (the host selects none such)
+    }
+  };
+  switch (k.n_acc) {
+    case 1: go(std::integral_constant<int, 1>{}); break;
+    case 2: go(std::integral_constant<int, 2>{}); break;
+    case 3: go(std::integral_constant<int, 3>{}); break;
+    default: go(std::integral_constant<int, 4>{}); break;
+  }
 }
 
 enum class MainLoop { staged, direct, persistent };
@@ -1380,8 +1502,17 @@ extern "C" int th_gemm(const th_gemm_desc* d, void* stream) {
     // every accumulator's columns (bn/2, a multiple of 32), so a fused RoPE
     // head must fit in that half.
     bool wave_epi = bn >= 64 && d->M < ((int64_t)1 << 31) && d->N < ((int64_t)1 << 31);
+    bool rope_in_half = true;
     for (int o = 0; o < d->n_out; ++o)
-      if (d->out[o].op == TH_EPI_ROPE) wave_epi &= (bn / 2) % k.hd == 0;
+      if (d->out[o].op == TH_EPI_ROPE) rope_in_half &= (bn / 2) % k.hd == 0;
+    if (!rope_in_half) {
+      // two accumulators, each output reading one: a wave can hold a whole
+      // accumulator tile (bn columns) instead, and with it whole heads
+      bool split = d->n_acc == 2 && bn % k.hd == 0;
+      for (int o = 0; o < d->n_out; ++o) split &= d->out[o].b < 0;
+      k.asplit = split ? 1 : 0;
+      wave_epi &= split;
+    }
     MainLoop ml = MainLoop::staged;
     const int force = forced_main_loop();
     if (direct) ml = wave_epi ? MainLoop::persistent : MainLoop::direct;

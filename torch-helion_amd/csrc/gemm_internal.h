@@ -33,6 +33,7 @@ struct GemmK {
   const float* rsin;
   int hd, period;
   int n_out;
+  int asplit;  // persistent kernel: each wave's column half is one whole accumulator (n_acc == 2)
   EpiOutK out[TH_MAX_OUT];
   float* sumsq_out;
 };

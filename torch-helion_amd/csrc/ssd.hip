@@ -490,7 +490,8 @@ __global__ void __launch_bounds__(256) ssd_carry2_kernel(SsdK p, uint4* hf) {
 // a 32-row t-block with NPT p-tiles; for each s-block s <= t the wave forms
 // G^T = B_s C_t^T on the MFMA (lane = t, registers = s in C order), weighs it
 // element-wise with the decay (every exponent a difference cl_t - cl_s <= 0,
-// in base 2) and uses it directly as the A operand of the product with x.
+// in base 2, on the raw v_exp_f32: results below 2^-126 flush to zero) and
+// uses it directly as the A operand of the product with x.
 // Full chunks load without guards; only the diagonal s-block is masked. The
 // result goes out through a per-wave LDS tile as 16-byte rows (gate in, y out).
 constexpr int kEpiStride = 36;  // floats per row of the per-wave 32 x 32 output tile
@@ -581,7 +582,8 @@ __global__ void __launch_bounds__(256, 2) ssd_out2_kernel(SsdK p, const uint4* h
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const float4 c4 = *(const float4*)&cl[tb * 32 + 8 * q + 4 * gl];
-        const float ex[4] = {exp2f(c4.x), exp2f(c4.y), exp2f(c4.z), exp2f(c4.w)};
+        const float ex[4] = {__builtin_amdgcn_exp2f(c4.x), __builtin_amdgcn_exp2f(c4.y),
+                             __builtin_amdgcn_exp2f(c4.z), __builtin_amdgcn_exp2f(c4.w)};
 #pragma unroll
         for (int j = 0; j < NPT; ++j)
 #pragma unroll
@@ -604,7 +606,8 @@ __global__ void __launch_bounds__(256, 2) ssd_out2_kernel(SsdK p, const uint4* h
         const float4 d4 = *(const float4*)&dts[s0];
         const float cs[4] = {c4.x, c4.y, c4.z, c4.w}, ds[4] = {d4.x, d4.y, d4.z, d4.w};
 #pragma unroll
-        for (int i2 = 0; i2 < 4; ++i2) m[4 * q + i2] = gt[4 * q + i2] * exp2f(clt - cs[i2]) * ds[i2];
+        for (int i2 = 0; i2 < 4; ++i2)
+          m[4 * q + i2] = gt[4 * q + i2] * __builtin_amdgcn_exp2f(clt - cs[i2]) * ds[i2];
       }
       if (sb == tb) {
 #pragma unroll
