@@ -33,9 +33,9 @@ sys.path.insert(0, str(REPO))
 METRIC = "µs per block fwd (Llama-8B block, Mamba-2 layer); % of MFMA/HBM roofline"
 
 # HBM bytes per launch of the C3 gate/up kernel (k4_gemm), from rocprofv3 --pmc passes:
-# FETCH_SIZE 2,752,830 KiB x 2.0 (the counter reads half of a calibrated 1 GiB copy's
-# fetch) + WRITE_SIZE 458,752 KiB x 1.0 (profiles/llama_c3_gateup_traffic.md).
-C3_K4_TRAFFIC_BYTES = (2752830 * 2.0 + 458752 * 1.0) * 1024
+# FETCH_SIZE 2,825,776 KiB x 2.0 (the counter reads half of a calibrated 1 GiB copy's
+# fetch) + WRITE_SIZE 464,389 KiB x 1.0 (profiles/llama_c3_gateup_traffic.md).
+C3_K4_TRAFFIC_BYTES = (2825776 * 2.0 + 464389 * 1.0) * 1024
 
 
 def log(msg: str) -> None:
