@@ -69,14 +69,18 @@ class DeviceProgram:
                     t = program.tensors[o.tensor]
                     self.buffers[o.tensor] = torch.empty(t.shape, dtype=_TORCH_DT[t.dtype], device=self.device)
         # Residual operands produced inside the program get an fp32 shadow:
-        # the producer also writes fp32 and every kernel that adds it as an
+        # the producer also writes fp32 and every GEMM that adds it as an
         # epilogue operand reads the shadow, so the residual stream is rounded
         # to the activation dtype only where a GEMM consumes it as its LHS.
+        # (The SSD's gate multiplies its output: it is read in its own dtype,
+        # as the eager model does, and keeps the kernel's vector epilogue.)
         self.shadow: dict[str, torch.Tensor] = {}
         produced = {o.tensor for k in program.kernels for o in k.outputs}
         # a gathered table row is exact in the table's dtype: no shadow needed
         exact = {o.tensor for k in program.kernels if k.kind == "embedding" for o in k.outputs}
         for k in program.kernels:
+            if k.kind != "gemm":
+                continue
             for a in k.args:
                 if (a.role == "extra" and a.tensor in produced and a.tensor not in self.shadow
                         and a.tensor not in exact and self.buffers[a.tensor].dtype in (torch.bfloat16, torch.float16)):
