@@ -82,7 +82,7 @@ def cpu_baseline(model, cfg, x, out_gpu, sample_seqs: int = 1) -> tuple[dict, di
     # oracle. Max-abs is reported beside it together with the floor that any bf16-storage
     # block has at this size (output magnitudes reach ~14, where one bf16 ulp is 0.0625).
     parity = {"max_rel_err": rel, "tolerance": 2e-2, "ok": rel <= 2e-2,
-              "against": "oracle fp32 (oracle.llama.block_forward), first sequence, fp32 copy of the GPU output",
+              "against": "oracle fp32 (oracle.llama.block_forward), first sequence, the GPU's bf16 output",
               "max_abs_err": err32, "max_abs_err_vs_bf16_storage_oracle": err,
               "bf16_storage_floor_max_abs": floor}
     return base, parity
@@ -99,9 +99,11 @@ def bench_mamba_c2(args) -> dict:
     cfg = config_c2()
     model = build_mamba_block(cfg, seed=0)
     x = model.example_inputs(seed=0)
+    # one layer at the eager model's precision: bf16 activations and residual, bf16 output
     res = compile_model(model, x, CompileConfig(run_name="bench_mamba_c2", results_dir=REPO / "gpurun_out" / "results",
                                                 backend="hip", device_check=True, reference_check=False,
-                                                verify_passes=False, planner_mode="exhaustive"))
+                                                verify_passes=False, planner_mode="exhaustive",
+                                                fp32_outputs=False, residual_fp32=False))
     b = bench_program(res.device_program, x, res.hw, warmup=args.warmup, reps=args.steps)
     us = b["us_median"]
     return {"us": us, "tokens_per_s": cfg.batch * cfg.seq / (us * 1e-6), "kernels": len(res.program.kernels),
@@ -257,14 +259,19 @@ def main() -> int:
     log("building the Llama-3-8B-shaped block (random init, seed 0)")
     cfg, model, x = build_c3()
     t0 = time.time()
+    # One block at the eager model's precision: bf16 activations, the residual
+    # stream rounded to bf16 where it is stored, the block output in bf16 (the
+    # fp32 residual mode is for deep stacks; on one block it costs 2% and moves
+    # the error against the fp32 oracle from 0.475% to 0.468%).
     res = compile_model(model, x, CompileConfig(run_name="bench_llama_c3", results_dir=REPO / "gpurun_out" / "results",
                                                 backend="hip", device_check=False, reference_check=False,
-                                                verify_passes=False, planner_mode="exhaustive"))
+                                                verify_passes=False, planner_mode="exhaustive",
+                                                fp32_outputs=False, residual_fp32=False))
     log(f"compiled in {time.time() - t0:.1f} s: {len(res.program.kernels)} kernels")
     dp = res.device_program
     b = bench_program(dp, x, res.hw, warmup=args.warmup, reps=args.steps)
     us = b["us_median"]
-    out_gpu = dp.outputs(fp32=True)[0]
+    out_gpu = dp.outputs(fp32=False)[0]
     torch.cuda.synchronize()
     tokens = cfg.batch * cfg.seq
     dom_name, dom = max(b["kernels"].items(), key=lambda kv: kv[1]["us"])

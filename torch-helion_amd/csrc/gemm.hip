@@ -132,9 +132,9 @@ __device__ __forceinline__ void store8(void* p, int64_t off, int dtype, bool vec
 // the slice (extra rows, RoPE table rows) is loaded before the first use.
 // aoff / boff: slice columns where the op's accumulators a / b start.
 template <int OP, bool SUMSQ>
-__device__ __forceinline__ void epi_slice(const GemmK& p, const EpiOutK& eo, const float* wsl, int ws, int aoff,
-                                          int boff, const float* rsrow, int64_t row0, int64_t col_w, int r_l, int c8,
-                                          int np, int rp) {
+__device__ __forceinline__ void epi_pair(const GemmK& p, const EpiOutK& eo, const float* wsl, int ws, int aoff,
+                                         int boff, const float* rsrow, int64_t row0, int64_t col_w, int r_l, int c8,
+                                         int np, int rp, int p0) {
   constexpr bool USES_E = OP == TH_EPI_ADD || OP == TH_EPI_SOFTPLUS_ADD || OP == TH_EPI_MUL;
   constexpr bool USES_T = OP == TH_EPI_ROPE || OP == TH_EPI_ROPE_PAIR;
   const int ia = eo.a, ib = eo.b;
@@ -142,29 +142,31 @@ __device__ __forceinline__ void epi_slice(const GemmK& p, const EpiOutK& eo, con
   const bool sb = SUMSQ && ib >= 0 && ((p.rscale_mask >> ib) & 1u);
   const int64_t gn = col_w + c8;
   const int valid = (int)min((int64_t)8, p.N - gn);
-  float xe[4][8], ye[4][8];
+  float xe[2][8], ye[2][8];
   if constexpr (USES_E || USES_T) {
 #pragma unroll
-    for (int ps = 0; ps < 4; ++ps) {
+    for (int pi = 0; pi < 2; ++pi) {
+      const int ps = p0 + pi;
       const int64_t gm = row0 + r_l + ps * rp;
       if (ps >= np || gm >= p.M || valid <= 0) continue;
       if constexpr (USES_E) {
         const int e = eo.e;
-        load8(p.extra[e], gm * p.ld_extra[e] + gn, p.extra_dtype[e], p.extra_vec8[e] != 0, valid, xe[ps]);
+        load8(p.extra[e], gm * p.ld_extra[e] + gn, p.extra_dtype[e], p.extra_vec8[e] != 0, valid, xe[pi]);
       } else {
         // head_dim is a multiple of 8, so the octet lies inside one head
         const int64_t toff = (int64_t)((int)gm % p.period) * p.hd + (int)gn % p.hd;
         const float4 c0 = *(const float4*)(p.rcos + toff), c1 = *(const float4*)(p.rcos + toff + 4);
         const float4 s0 = *(const float4*)(p.rsin + toff), s1 = *(const float4*)(p.rsin + toff + 4);
-        xe[ps][0] = c0.x; xe[ps][1] = c0.y; xe[ps][2] = c0.z; xe[ps][3] = c0.w;
-        xe[ps][4] = c1.x; xe[ps][5] = c1.y; xe[ps][6] = c1.z; xe[ps][7] = c1.w;
-        ye[ps][0] = s0.x; ye[ps][1] = s0.y; ye[ps][2] = s0.z; ye[ps][3] = s0.w;
-        ye[ps][4] = s1.x; ye[ps][5] = s1.y; ye[ps][6] = s1.z; ye[ps][7] = s1.w;
+        xe[pi][0] = c0.x; xe[pi][1] = c0.y; xe[pi][2] = c0.z; xe[pi][3] = c0.w;
+        xe[pi][4] = c1.x; xe[pi][5] = c1.y; xe[pi][6] = c1.z; xe[pi][7] = c1.w;
+        ye[pi][0] = s0.x; ye[pi][1] = s0.y; ye[pi][2] = s0.z; ye[pi][3] = s0.w;
+        ye[pi][4] = s1.x; ye[pi][5] = s1.y; ye[pi][6] = s1.z; ye[pi][7] = s1.w;
       }
     }
   }
 #pragma unroll
-  for (int ps = 0; ps < 4; ++ps) {
+  for (int pi = 0; pi < 2; ++pi) {
+    const int ps = p0 + pi;
     const int r16 = r_l + ps * rp;
     const int64_t gm = row0 + r16;
     if (ps >= np || gm >= p.M || valid <= 0) continue;
@@ -211,17 +213,27 @@ __device__ __forceinline__ void epi_slice(const GemmK& p, const EpiOutK& eo, con
         for (int i = 0; i < 8; ++i) rot[i] = sb ? bb[i] * rr : bb[i];
       }
 #pragma unroll
-      for (int i = 0; i < 8; ++i) v[i] = a[i] * xe[ps][i] + rot[i] * ye[ps][i];
+      for (int i = 0; i < 8; ++i) v[i] = a[i] * xe[pi][i] + rot[i] * ye[pi][i];
     } else {  // ADD, SOFTPLUS_ADD, MUL
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        if constexpr (OP == TH_EPI_MUL) v[i] = a[i] * xe[ps][i];
-        else if constexpr (OP == TH_EPI_ADD) v[i] = a[i] + xe[ps][i];
-        else v[i] = softplusf_(a[i] + xe[ps][i]);
+        if constexpr (OP == TH_EPI_MUL) v[i] = a[i] * xe[pi][i];
+        else if constexpr (OP == TH_EPI_ADD) v[i] = a[i] + xe[pi][i];
+        else v[i] = softplusf_(a[i] + xe[pi][i]);
       }
     }
     store8(eo.ptr, gm * eo.ld + gn, eo.dtype, eo.vec8 != 0, valid, v);
   }
+}
+
+template <int OP, bool SUMSQ>
+__device__ __forceinline__ void epi_slice(const GemmK& p, const EpiOutK& eo, const float* wsl, int ws, int aoff,
+                                          int boff, const float* rsrow, int64_t row0, int64_t col_w, int r_l, int c8,
+                                          int np, int rp) {
+  // two passes at a time: their global operands load together, and at most 2 x 16
+  // of them are live (np = 4 with all loaded up front spilled the 8-wave kernel)
+  epi_pair<OP, SUMSQ>(p, eo, wsl, ws, aoff, boff, rsrow, row0, col_w, r_l, c8, np, rp, 0);
+  if (np > 2) epi_pair<OP, SUMSQ>(p, eo, wsl, ws, aoff, boff, rsrow, row0, col_w, r_l, c8, np, rp, 2);
 }
 
 // Evaluate every output op for the `rows` slab rows staged in LDS.

@@ -47,6 +47,7 @@ class CompileConfig:
     ssd_chunk: int = 0                            # 0: 64 for sequences up to 1024, else 256
     fuse_rope: bool = True
     fp32_outputs: bool = True                     # producers of program outputs also write an fp32 copy
+    residual_fp32: bool = True                    # residual operands of GEMM epilogues travel in fp32
     cpu_flop_budget: float = 2e10                 # graphs above this skip CPU-side checks in "auto" mode
 
     @property

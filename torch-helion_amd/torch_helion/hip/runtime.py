@@ -45,7 +45,7 @@ class DeviceProgram:
     """A Program lowered and bound for execution on ``device``."""
 
     def __init__(self, program: Program, params: dict[str, torch.Tensor], device: int | torch.device = 0,
-                 fuse_rope: bool = True, fp32_outputs: bool = True) -> None:
+                 fuse_rope: bool = True, fp32_outputs: bool = True, residual_fp32: bool = True) -> None:
         self.program = program
         self.device = torch.device("cuda", device) if isinstance(device, int) else torch.device(device)
         if self.device.type != "cuda":
@@ -79,7 +79,7 @@ class DeviceProgram:
         # a gathered table row is exact in the table's dtype: no shadow needed
         exact = {o.tensor for k in program.kernels if k.kind == "embedding" for o in k.outputs}
         for k in program.kernels:
-            if k.kind != "gemm":
+            if k.kind != "gemm" or not residual_fp32:
                 continue
             for a in k.args:
                 if (a.role == "extra" and a.tensor in produced and a.tensor not in self.shadow
