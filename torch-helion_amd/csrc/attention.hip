@@ -4,15 +4,15 @@
 // causal flag and grouped KV heads.
 //
 // bf16 prefill kernel (gfx950): one workgroup = 4 waves = 128 queries of one
-// (batch, q-head); kv tiles of 64 keys are staged through LDS, double
-// buffered. Each wave computes S^T = K Q^T with v_mfma_f32_32x32x16_bf16 so a
-// lane owns one query column: the online-softmax max/sum needs a single
+// (batch, q-head); kv tiles of 64 keys stream into LDS by direct loads,
+// double buffered. Each wave computes S^T = K Q^T with v_mfma_f32_32x32x16_bf16
+// so a lane owns one query column: the online-softmax max/sum needs a single
 // lane^32 exchange and P^T is already in the B-operand layout of the P V
 // product O^T = V^T P^T (the kv order inside one 16-wide k step is permuted,
-// identically for V^T, which is harmless for a contraction). V is written to
-// LDS transposed (kv contiguous) with an XOR swizzle that keeps the two
-// 8-byte reads per MFMA operand conflict-free. Causal workgroups are issued
-// longest-first; a wave skips kv tiles entirely above its diagonal.
+// identically for V^T, which is harmless for a contraction). V stays
+// row-major in LDS; its transposed operands come from ds_read_b64_tr_b16.
+// Causal workgroups are issued longest-first; a wave skips kv tiles entirely
+// above its diagonal.
 #include "common.h"
 
 namespace th {
@@ -27,25 +27,42 @@ struct AttnK {
   float scale_log2;
 };
 
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+
+// K and V tiles stream from HBM straight into LDS (global_load_lds_dwordx4,
+// 1 KB per wave instruction: 1024 / (2 D) rows), row-major with each row's
+// 16-byte chunks permuted:
+//   K row R: chunk c in slot c ^ (R % (D/8)): the 32-row reads of an S^T
+//            operand (one chunk per lane) hit distinct banks.
+//   V row R: chunk c in slot c ^ vsw(R), vsw(R) = 4 (R % 4) for D = 128 and
+//            4 ((R / 2) % 2) for D = 64.
+// V^T operands come from ds_read_b64_tr_b16: in each 16-lane group, output
+// lane i, element e = the element i % 4 of the 8 bytes at source lane
+// 4 e + i / 4's address. Source lane 4 e + j points at V row kb + e, columns
+// d0 + 4 j .. +3, so output lane i holds keys kb .. kb+3 of column d0 + i; the
+// swizzle puts the 4 rows of a group (and the two groups sharing them) on
+// distinct banks. Rows past the last key re-read the last key: in bounds, and
+// their scores are masked to -inf (P = 0).
 template <int D>
 __global__ void __launch_bounds__(256, 2) attn_fwd_bf16_kernel(AttnK p) {
   constexpr int BQ = 128, BKV = 64;
-  constexpr int KCH = D / 8;             // 16-byte chunks per K row
-  constexpr int KROW = D * 2;            // bytes per K row in LDS
-  constexpr int VROW = BKV * 2;          // bytes per V^T row (one d) in LDS
-  constexpr int KT_BYTES = BKV * KROW;
-  constexpr int VT_BYTES = D * VROW;
-  constexpr int STAGE = KT_BYTES + VT_BYTES;
-  constexpr int OROW = D + 4;            // fp32 staging row for the output
+  constexpr int RB = D * 2;               // bytes per K or V row
+  constexpr int KCH = D / 8;              // 16-byte chunks per row
+  constexpr int RPI = 1024 / RB;          // rows per 1 KB load
+  constexpr int NLOAD = BKV / RPI / 4;    // loads per wave per tile, per tensor
+  constexpr int KT_BYTES = BKV * RB;
+  constexpr int STAGE = 2 * KT_BYTES;     // K tile then V tile
+  constexpr int OROW = D + 4;             // fp32 staging row for the output
   constexpr int O_BYTES = 4 * 32 * OROW * 4;
   constexpr int SMEM = 2 * STAGE > O_BYTES ? 2 * STAGE : O_BYTES;
-  constexpr int KLD = BKV * KCH / 256;   // K chunks per thread per tile
-  constexpr int VPAIRS = KCH / 8;        // V row pairs per thread per tile
-  constexpr int NKS = D / 16;            // k steps of S^T = K Q^T
-  constexpr int NDT = D / 32;            // 32-row blocks of O^T
+  constexpr int NKS = D / 16;             // k steps of S^T = K Q^T
+  constexpr int NDT = D / 32;             // 32-row blocks of O^T
+  static_assert(NLOAD * RPI * 4 == BKV, "tile rows per wave");
   __shared__ __attribute__((aligned(16))) char smem[SMEM];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int hl = lane >> 5, col = lane & 31;
   const int bh_count = p.B * p.Hq;
   const int qb = p.nqb - 1 - (int)(blockIdx.x / bh_count);
@@ -56,8 +73,8 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_bf16_kernel(AttnK p) {
   const int qrow = q0w + col;
 
   const uint16_t* qbase = p.q + (int64_t)b * p.Sq * p.ldq + (int64_t)hq * D;
-  const uint16_t* kbase = p.k + (int64_t)b * p.Skv * p.ldk + (int64_t)hk * D;
-  const uint16_t* vbase = p.v + (int64_t)b * p.Skv * p.ldv + (int64_t)hk * D;
+  const char* kbase = (const char*)(p.k + (int64_t)b * p.Skv * p.ldk + (int64_t)hk * D);
+  const char* vbase = (const char*)(p.v + (int64_t)b * p.Skv * p.ldv + (int64_t)hk * D);
 
   bf16x8_t qf[NKS];
 #pragma unroll
@@ -75,52 +92,29 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_bf16_kernel(AttnK p) {
   if (p.causal) last_kv = min(last_kv, q0 + BQ - 1 + p.off);
   const int ntiles = last_kv < 0 ? 0 : last_kv / BKV + 1;
 
-  uint4 rk[KLD], rv[VPAIRS][2];
-  auto gload = [&](int it) {
+  // this lane's place in the tile loads: load n = NLOAD*wave + i covers rows RPI*n ..
+  const int lrow = lane / KCH, slot = lane % KCH;
+  auto vsw = [](int r) { return D == 128 ? 4 * (r & 3) : 4 * ((r >> 1) & 1); };
+  auto issue = [&](int it, int st) {
     const int k0 = it * BKV;
+    char* sk = smem + st * STAGE;
 #pragma unroll
-    for (int i = 0; i < KLD; ++i) {
-      const int c = tid + 256 * i;
-      const int row = c / KCH, ch = c - row * KCH;
-      const int kv = k0 + row;
-      rk[i] = kv < p.Skv ? *(const uint4*)(kbase + (int64_t)kv * p.ldk + ch * 8) : make_uint4(0, 0, 0, 0);
-    }
-    const int dc = tid % KCH;
-#pragma unroll
-    for (int i = 0; i < VPAIRS; ++i) {
-      const int pr = tid / KCH + (256 / KCH) * i;
-#pragma unroll
-      for (int e = 0; e < 2; ++e) {
-        const int kv = k0 + 2 * pr + e;
-        rv[i][e] = kv < p.Skv ? *(const uint4*)(vbase + (int64_t)kv * p.ldv + dc * 8) : make_uint4(0, 0, 0, 0);
-      }
+    for (int i = 0; i < NLOAD; ++i) {
+      const int n = NLOAD * wave + i;
+      const int row = RPI * n + lrow;
+      const int kv = min(k0 + row, p.Skv - 1);
+      __builtin_amdgcn_global_load_lds((const void*)(kbase + (int64_t)kv * p.ldk * 2 + ((slot ^ (row % KCH)) << 4)),
+                                       (lds_ptr_t)(sk + n * 1024), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void*)(vbase + (int64_t)kv * p.ldv * 2 + ((slot ^ vsw(row)) << 4)),
+                                       (lds_ptr_t)(sk + KT_BYTES + n * 1024), 16, 0, 0);
     }
   };
-  auto sstore = [&](int buf) {
-    char* sk = smem + buf * STAGE;
-    char* sv = sk + KT_BYTES;
-#pragma unroll
-    for (int i = 0; i < KLD; ++i) {
-      const int c = tid + 256 * i;
-      const int row = c / KCH, ch = c - row * KCH;
-      *(uint4*)(sk + row * KROW + ((ch ^ (row % KCH)) << 4)) = rk[i];
-    }
-    const int dc = tid % KCH;
-#pragma unroll
-    for (int i = 0; i < VPAIRS; ++i) {
-      const int pr = tid / KCH + (256 / KCH) * i;
-      const uint32_t a[4] = {rv[i][0].x, rv[i][0].y, rv[i][0].z, rv[i][0].w};
-      const uint32_t c2[4] = {rv[i][1].x, rv[i][1].y, rv[i][1].z, rv[i][1].w};
-#pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        const int d = dc * 8 + q;
-        const uint32_t lo = (q & 1) ? (a[q >> 1] >> 16) : (a[q >> 1] & 0xffffu);
-        const uint32_t hi = (q & 1) ? (c2[q >> 1] >> 16) : (c2[q >> 1] & 0xffffu);
-        const int sw = ((d >> 1) & 15) << 1;
-        *(uint32_t*)(sv + d * VROW + ((pr ^ sw) << 2)) = lo | (hi << 16);
-      }
-    }
-  };
+
+  // V^T operand reads: this lane is source lane 4e + j of its 16-lane group
+  const int e4 = (lane & 15) >> 2, j4 = lane & 3, g2 = (lane >> 4) & 1;
+  const int ee = D == 128 ? e4 : (e4 >> 1);
+  const int vrow_l = (4 * hl + e4) * RB + (j4 & 1) * 8;  // row part (keys +4hl+e) and the 8-byte half
+  const int vc0 = 2 * g2 + (j4 >> 1);                   // chunk within the 32-column block, before the swizzle
 
   f32x16_t oacc[NDT];
 #pragma unroll
@@ -129,14 +123,13 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_bf16_kernel(AttnK p) {
     for (int r = 0; r < 16; ++r) oacc[t][r] = 0.f;
   float m_run = -INFINITY, l_run = 0.f;
 
-  if (ntiles > 0) {
-    gload(0);
-    sstore(0);
-  }
-  __syncthreads();
+  if (ntiles > 0) issue(0, 0);
   for (int it = 0; it < ntiles; ++it) {
     const int cur = it & 1;
-    if (it + 1 < ntiles) gload(it + 1);
+    // tile it has landed everywhere, and every wave is done with stage cur ^ 1
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (it + 1 < ntiles) issue(it + 1, cur ^ 1);
     const int k0 = it * BKV;
     const bool active = !p.causal || k0 <= q0w + 31 + p.off;
     if (active) {
@@ -153,7 +146,7 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_bf16_kernel(AttnK p) {
         for (int t = 0; t < 2; ++t) {
           const int row = 32 * t + col;
           const int ch = 2 * ks + hl;
-          const bf16x8_t kf = *(const bf16x8_t*)(sk + row * KROW + ((ch ^ (row % KCH)) << 4));
+          const bf16x8_t kf = *(const bf16x8_t*)(sk + row * RB + ((ch ^ (row % KCH)) << 4));
           s[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[ks], s[t], 0, 0, 0);
         }
       }
@@ -192,9 +185,9 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_bf16_kernel(AttnK p) {
       for (int t = 0; t < 2; ++t)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const float e = __builtin_amdgcn_exp2f(fmaf(s[t][r], c, nm));
-          s[t][r] = e;
-          lsum += e;
+          const float ex = __builtin_amdgcn_exp2f(fmaf(s[t][r], c, nm));
+          s[t][r] = ex;
+          lsum += ex;
         }
       l_run = l_run * alpha + lsum;
       if (__any(move)) {
@@ -203,31 +196,30 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_bf16_kernel(AttnK p) {
 #pragma unroll
           for (int r = 0; r < 16; ++r) oacc[t][r] *= alpha;
       }
-      // O^T += V^T P^T over 4 k steps of 16 keys
+      // O^T += V^T P^T over 4 k steps of 16 keys. The lane's 8 P values are the
+      // keys 16 hh + 4 hl + 0..3 and 16 hh + 8 + 4 hl + 0..3 of 32-key block t
+      // (S^T's C layout); one transposing read fetches each group of 4.
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
         const int t = ks >> 1, hh = ks & 1;
         bf16x8_t pf;
 #pragma unroll
         for (int e = 0; e < 8; ++e) pf[e] = (__bf16)s[t][8 * hh + e];
-        const int w0 = 16 * t + 8 * hh + 2 * hl;
+        const char* vb = sv + (32 * t + 16 * hh) * RB + vrow_l;
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt) {
-          const int d = 32 * dt + col;
-          const int sw = ((d >> 1) & 15) << 1;
-          const char* vrow = sv + d * VROW;
-          const uint2 lo = *(const uint2*)(vrow + ((w0 ^ sw) << 2));
-          const uint2 hi = *(const uint2*)(vrow + (((w0 + 4) ^ sw) << 2));
-          bf16x8_t vf;
-          uint32_t* vw = (uint32_t*)&vf;
-          vw[0] = lo.x; vw[1] = lo.y; vw[2] = hi.x; vw[3] = hi.y;
+          const int cofs = ((4 * (dt ^ ee) + vc0) << 4);
+          const s16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (__attribute__((address_space(3))) s16x4_t*)(vb + cofs));
+          const s16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (__attribute__((address_space(3))) s16x4_t*)(vb + 8 * RB + cofs));
+          const bf16x8_t vf = __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
           oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf, oacc[dt], 0, 0, 0);
         }
       }
     }
-    if (it + 1 < ntiles) sstore(cur ^ 1);
-    __syncthreads();
   }
+  __syncthreads();  // every wave is done with the stages before they hold the output
 
   // normalise and write through LDS so rows are stored contiguously
   const float l_tot = l_run + __shfl_xor(l_run, 32);
