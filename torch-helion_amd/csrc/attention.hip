@@ -93,20 +93,41 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_bf16_kernel(AttnK p) {
   const int ntiles = last_kv < 0 ? 0 : last_kv / BKV + 1;
 
   // this lane's place in the tile loads: load n = NLOAD*wave + i covers rows RPI*n ..
+  // Per-lane byte offsets of those rows within a tile (32-bit: 63 rows of a row
+  // stride under 32 MiB) plus the chunk swizzle; a full tile adds them to a
+  // uniform base, the ragged last tile clamps its rows to the last key.
   const int lrow = lane / KCH, slot = lane % KCH;
   auto vsw = [](int r) { return D == 128 ? 4 * (r & 3) : 4 * ((r >> 1) & 1); };
+  uint32_t kro[NLOAD], vro[NLOAD];
+#pragma unroll
+  for (int i = 0; i < NLOAD; ++i) {
+    const int row = RPI * (NLOAD * wave + i) + lrow;
+    kro[i] = (uint32_t)row * (uint32_t)p.ldk * 2u + (uint32_t)((slot ^ (row % KCH)) << 4);
+    vro[i] = (uint32_t)row * (uint32_t)p.ldv * 2u + (uint32_t)((slot ^ vsw(row)) << 4);
+  }
   auto issue = [&](int it, int st) {
     const int k0 = it * BKV;
     char* sk = smem + st * STAGE;
+    if (k0 + BKV <= p.Skv) {
+      const char* kb = kbase + (int64_t)k0 * p.ldk * 2;
+      const char* vb = vbase + (int64_t)k0 * p.ldv * 2;
 #pragma unroll
-    for (int i = 0; i < NLOAD; ++i) {
-      const int n = NLOAD * wave + i;
-      const int row = RPI * n + lrow;
-      const int kv = min(k0 + row, p.Skv - 1);
-      __builtin_amdgcn_global_load_lds((const void*)(kbase + (int64_t)kv * p.ldk * 2 + ((slot ^ (row % KCH)) << 4)),
-                                       (lds_ptr_t)(sk + n * 1024), 16, 0, 0);
-      __builtin_amdgcn_global_load_lds((const void*)(vbase + (int64_t)kv * p.ldv * 2 + ((slot ^ vsw(row)) << 4)),
-                                       (lds_ptr_t)(sk + KT_BYTES + n * 1024), 16, 0, 0);
+      for (int i = 0; i < NLOAD; ++i) {
+        const int n = NLOAD * wave + i;
+        __builtin_amdgcn_global_load_lds((const void*)(kb + kro[i]), (lds_ptr_t)(sk + n * 1024), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds((const void*)(vb + vro[i]), (lds_ptr_t)(sk + KT_BYTES + n * 1024), 16, 0, 0);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < NLOAD; ++i) {
+        const int n = NLOAD * wave + i;
+        const int row = RPI * n + lrow;
+        const int kv = min(k0 + row, p.Skv - 1);
+        __builtin_amdgcn_global_load_lds((const void*)(kbase + (int64_t)kv * p.ldk * 2 + ((slot ^ (row % KCH)) << 4)),
+                                         (lds_ptr_t)(sk + n * 1024), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds((const void*)(vbase + (int64_t)kv * p.ldv * 2 + ((slot ^ vsw(row)) << 4)),
+                                         (lds_ptr_t)(sk + KT_BYTES + n * 1024), 16, 0, 0);
+      }
     }
   };
 
@@ -314,6 +335,8 @@ extern "C" int th_attention_prefill(const th_attn_desc* d, void* stream) {
   if (d->dtype == TH_BF16) {
     TH_CHECK_ARG(d->ld_q % 8 == 0 && d->ld_k % 8 == 0 && d->ld_v % 8 == 0 && d->ld_o % 4 == 0,
                  "th_attention_prefill: bf16 row strides must be multiples of 8 elements");
+    TH_CHECK_ARG(d->ld_k < ((int64_t)1 << 24) && d->ld_v < ((int64_t)1 << 24),
+                 "th_attention_prefill: bf16 k/v row strides must be under 2^24 elements");
     TH_CHECK_ARG(((uintptr_t)d->q | (uintptr_t)d->k | (uintptr_t)d->v) % 16 == 0 && (uintptr_t)d->o % 8 == 0,
                  "th_attention_prefill: tensors must be 16-byte aligned");
   }
