@@ -139,6 +139,9 @@ def test_attention_rejects_bad_heads(lib):
     d.head_dim, d.scale = 64, -0.125  # the bf16 kernel folds a positive scale into exp2
     assert lib.th_attention_prefill(C.byref(d), None) == abi.TH_ERR_INVALID
     assert "scale > 0" in abi.last_error(lib)
+    d.scale, d.ld_k = 0.125, 1 << 24  # the bf16 kernel keeps a tile's k/v row offsets in 32 bits
+    assert lib.th_attention_prefill(C.byref(d), None) == abi.TH_ERR_INVALID
+    assert "under 2^24" in abi.last_error(lib)
 
 
 def test_valid_descriptor_without_init_stops_before_the_device(lib):
