@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define TH_ABI_VERSION 3
+#define TH_ABI_VERSION 4
 
 typedef enum th_status {
   TH_OK = 0,
@@ -84,9 +84,16 @@ typedef struct th_epi_out {
   int32_t op;     /* th_epi_op */
   int32_t a, b;   /* accumulator indices (b only for ROPE_PAIR / SWIGLU) */
   int32_t e;      /* extra operand index for ADD / SOFTPLUS_ADD / MUL, else -1 */
-  void* ptr;      /* [M, N] row-major output */
+  void* ptr;      /* [M, N] row-major output (or [M, col_end - col_begin], see below) */
   int64_t ld;     /* row stride of ptr, in elements */
   int32_t dtype;  /* TH_F32 or TH_BF16 */
+  /* Column window: the output holds accumulator columns [col_begin, col_end)
+   * only, column n at ptr[m * ld + n - col_begin]; its extra operand is read
+   * at the same relative column. Both multiples of 8 (and of the RoPE head
+   * dim for ROPE ops); col_end = 0 means N. Several outputs with disjoint
+   * windows of one accumulator are how one launch computes sibling
+   * projections of a shared input (bf16 / fp32 only). */
+  int32_t col_begin, col_end;
   int32_t pad_;
 } th_epi_out;
 

@@ -102,6 +102,29 @@ def _gemm_desc(**over):
     return d
 
 
+@pytest.mark.parametrize("window,ld,msg", [
+    ((4, 32), 64, "multiples of 8"), ((32, 32), 64, "column window"), ((0, 72), 64, "column window"),
+    ((16, 48), 24, "ld < its width"),
+])
+def test_gemm_rejects_bad_column_windows(lib, window, ld, msg):
+    from torch_helion.hip import abi
+
+    d = _gemm_desc()
+    d.out[0].col_begin, d.out[0].col_end = window
+    d.out[0].ld = ld
+    assert lib.th_gemm(C.byref(d), None) == abi.TH_ERR_INVALID
+    assert msg in abi.last_error(lib)
+
+
+def test_gemm_column_windows_only_for_bf16_and_fp32(lib):
+    from torch_helion.hip import abi
+
+    d = _gemm_desc(in_dtype=abi.TH_F8E4M3, rhs_scale=16384, workspace=20480, workspace_bytes=1 << 30)
+    d.out[0].col_begin, d.out[0].col_end = 0, 32
+    assert lib.th_gemm(C.byref(d), None) == abi.TH_ERR_INVALID
+    assert "bf16 / fp32" in abi.last_error(lib), abi.last_error(lib)
+
+
 @pytest.mark.parametrize("field,value,msg", [
     ("n_acc", 7, "n_acc"), ("K", 60, "multiple of 8"), ("in_dtype", 2, "in_dtype"), ("n_out", 0, "n_out"),
     ("rscale_mask", 1, "without sumsq"), ("lhs", 4100, "aligned"),

@@ -161,6 +161,27 @@ def test_mamba_layer_c2_bf16(gpu, tmp_path, fp32_copies):
     assert (out - ref).abs().max().item() < 5e-2
 
 
+def test_mamba_layer_c2_merged_in_projection(gpu, tmp_path):
+    """merge_siblings=True: the three in-projection GEMMs of the Mamba layer (B|C, dt, z|x) launch as one
+    th_gemm over concatenated weights with column-windowed outputs; same results as the separate launches."""
+    from targets.mamba import build_mamba_block, config_c2
+
+    announce("e2e mamba C2 merged in-projection")
+    cfg = config_c2()
+    m = build_mamba_block(cfg, seed=0)
+    x = m.example_inputs(seed=0)
+    sep = _compile(m, x, tmp_path, "c2_sep", residual_fp32=False, fp32_outputs=False)
+    mer = _compile(m, x, tmp_path, "c2_mer", residual_fp32=False, fp32_outputs=False, merge_siblings=True)
+    assert mer.validation["ok"], mer.validation
+    merged = [l for l in mer.device_program.launches if "+" in l.kernel]
+    assert merged and len(merged[0].info["merged"]) == 3, [l.kernel for l in mer.device_program.launches]
+    assert len(mer.device_program.launches) == len(sep.device_program.launches) - 2
+    a = sep.run(*x)[0].float().cpu()
+    b = mer.run(*x)[0].float().cpu()
+    # same products, one accumulator instead of three: fp32 sums in a different tile order
+    assert (a - b).abs().max().item() / a.abs().max().item() < 1e-2
+
+
 @pytest.mark.parametrize("which", ["llama_gqa_bf16", "mamba_c2_bf16"])
 def test_graph_replays_match_eager(gpu, tmp_path, which):
     """The captured HIP graph of a whole program reproduces the eager launch sequence bit for bit,

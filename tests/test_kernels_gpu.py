@@ -604,3 +604,40 @@ def test_gemm_tied_lm_head_ragged_vocab(gpu):
     assert _rel(o32, ref) < 1e-5
     assert _maxabs(o16, ref) < BF16_TOL * max(1.0, float(ref.abs().max()))
     assert not torch.isnan(o16).any()
+
+
+@pytest.mark.parametrize("M", [2048, 16384])
+def test_gemm_column_windows(gpu, M):
+    """One accumulator over concatenated weights with outputs on column windows (the merged
+    in-projection of a Mamba layer: B | C | dt | z | x), each with its own op, extra operand and
+    RMS row scale: every window equals the separate projection; no output writes outside its window."""
+    from torch_helion.hip import abi, ops
+
+    K, eps = 512, 1e-5
+    widths = [64, 64, 16, 1024, 1024]
+    announce(f"gemm column windows M={M} widths={widths}")
+    g = torch.Generator().manual_seed(M)
+    x = torch.randn(M, K, generator=g).bfloat16()
+    ws = [(torch.randn(K, n, generator=g) * 0.05).bfloat16() for n in widths]
+    bias = torch.randn(M, widths[2], generator=g)
+    xf = x.float()
+    r = ((xf * xf).sum(-1, keepdim=True) / K + eps).pow(-0.5)
+    accs = [(xf @ w.float()) * r for w in ws]
+    refs = [accs[0], accs[1], torch.nn.functional.softplus(accs[2] + bias, threshold=1e9),
+            accs[3] * torch.sigmoid(accs[3]), accs[4]]
+    ops_ = [abi.EPI_ACC, abi.EPI_ACC, abi.EPI_SOFTPLUS_ADD, abi.EPI_SILU, abi.EPI_ACC]
+    xd = x.to(gpu)
+    packed = ops.pack_rhs([torch.cat([w.to(gpu) for w in ws], dim=1).contiguous()], torch.bfloat16)
+    # outputs padded by 8 columns on the right: the pad must stay untouched
+    outs = [torch.full((M, n + 8), float("nan"), dtype=torch.bfloat16, device=gpu) for n in widths]
+    epi, c0 = [], 0
+    for n, op, o in zip(widths, ops_, outs):
+        epi.append(ops.EpiSpec(op, o, a=0, e=0 if op == abi.EPI_SOFTPLUS_ADD else -1, cols=(c0, c0 + n)))
+        c0 += n
+    ops.gemm(ops.GemmCall(M, c0, K, 1, xd, packed, epi, sumsq=True, rscale_mask=1, inv_k=1.0 / K, eps=eps,
+                          extras=[bias.to(gpu)]))
+    torch.cuda.synchronize()
+    for i, (n, o, ref) in enumerate(zip(widths, outs, refs)):
+        got = o.cpu()
+        assert torch.isnan(got[:, n:].float()).all(), i
+        assert _maxabs(got[:, :n], ref) < BF16_TOL * max(1.0, float(ref.abs().max())), i

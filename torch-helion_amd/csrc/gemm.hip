@@ -141,7 +141,9 @@ __device__ __forceinline__ void epi_pair(const GemmK& p, const EpiOutK& eo, cons
   const bool sa = SUMSQ && ((p.rscale_mask >> ia) & 1u);
   const bool sb = SUMSQ && ib >= 0 && ((p.rscale_mask >> ib) & 1u);
   const int64_t gn = col_w + c8;
-  const int valid = (int)min((int64_t)8, p.N - gn);
+  // the output's column window (multiples of 8: an octet is wholly in or out)
+  const int valid = gn >= eo.cb && gn < eo.ce ? (int)min((int64_t)8, (int64_t)eo.ce - gn) : 0;
+  const int64_t gc = gn - eo.cb;  // output (and extra) column
   float xe[2][8], ye[2][8];
   if constexpr (USES_E || USES_T) {
 #pragma unroll
@@ -151,7 +153,7 @@ __device__ __forceinline__ void epi_pair(const GemmK& p, const EpiOutK& eo, cons
       if (ps >= np || gm >= p.M || valid <= 0) continue;
       if constexpr (USES_E) {
         const int e = eo.e;
-        load8(p.extra[e], gm * p.ld_extra[e] + gn, p.extra_dtype[e], p.extra_vec8[e] != 0, valid, xe[pi]);
+        load8(p.extra[e], gm * p.ld_extra[e] + gc, p.extra_dtype[e], p.extra_vec8[e] != 0, valid, xe[pi]);
       } else {
         // head_dim is a multiple of 8, so the octet lies inside one head
         const int64_t toff = (int64_t)((int)gm % p.period) * p.hd + (int)gn % p.hd;
@@ -222,7 +224,7 @@ __device__ __forceinline__ void epi_pair(const GemmK& p, const EpiOutK& eo, cons
         else v[i] = softplusf_(a[i] + xe[pi][i]);
       }
     }
-    store8(eo.ptr, gm * eo.ld + gn, eo.dtype, eo.vec8 != 0, valid, v);
+    store8(eo.ptr, gm * eo.ld + gc, eo.dtype, eo.vec8 != 0, valid, v);
   }
 }
 
@@ -246,6 +248,7 @@ __device__ void epilogue_slab(const GemmK& p, const float* slab, int srow, int r
   const int64_t col0 = (int64_t)tile_n * bn;
   for (int o = 0; o < p.n_out; ++o) {
     const EpiOutK& eo = p.out[o];
+    if (eo.ce <= col0 || eo.cb >= col0 + bn) continue;  // the output's window misses this tile
     const int op = eo.op;
     const int ia = eo.a, ib = eo.b;
     const float sa = 1.f, sb = 1.f;
@@ -256,8 +259,9 @@ __device__ void epilogue_slab(const GemmK& p, const float* slab, int srow, int r
       const int j = (u - r * q4) << 2;
       const int64_t gm = row0 + r;
       const int64_t gn = col0 + j;
-      if (gm >= p.M || gn >= p.N) continue;
-      const int valid = (int)min((int64_t)4, p.N - gn);
+      if (gm >= p.M || gn < eo.cb || gn >= eo.ce) continue;
+      const int valid = (int)min((int64_t)4, (int64_t)eo.ce - gn);
+      const int64_t gc = gn - eo.cb;  // output (and extra) column
       const float rr = p.sumsq ? rs[r] : 1.f;
       const float* srow_p = slab + r * srow;
       float4 a = *(const float4*)(srow_p + ia * bn + j);
@@ -310,7 +314,7 @@ __device__ void epilogue_slab(const GemmK& p, const float* slab, int srow, int r
         case TH_EPI_SOFTPLUS_ADD:
         case TH_EPI_MUL: {
           const int e = eo.e;
-          const float4 x = load4(p.extra[e], gm * p.ld_extra[e] + gn, p.extra_dtype[e],
+          const float4 x = load4(p.extra[e], gm * p.ld_extra[e] + gc, p.extra_dtype[e],
                                  p.extra_vec[e] != 0, valid);
           if (op == TH_EPI_MUL) {
             v.x = a.x * x.x; v.y = a.y * x.y; v.z = a.z * x.z; v.w = a.w * x.w;
@@ -327,7 +331,7 @@ __device__ void epilogue_slab(const GemmK& p, const float* slab, int srow, int r
           break;
       }
       (void)sa; (void)sb;
-      store4(eo.ptr, gm * eo.ld + gn, eo.dtype, eo.vec != 0, valid, v);
+      store4(eo.ptr, gm * eo.ld + gc, eo.dtype, eo.vec != 0, valid, v);
     }
   }
 }
@@ -987,6 +991,7 @@ __global__ void __launch_bounds__(64 * NW, 1) gemm_bf16_pk_kernel(GemmK p) {
         for (int o = 0; o < p.n_out; ++o) {
           const EpiOutK& eo = p.out[o];
           if (ASPLIT && eo.a != wn) continue;
+          if (eo.ce <= col_w || eo.cb >= col_w + wcols) continue;  // the window misses this wave's columns
           const int aoff = ASPLIT ? 0 : eo.a * hbn, boff = ASPLIT ? 0 : eo.b * hbn;
 #define TH_EPI_CASE(OP_) \
   case OP_: epi_slice<OP_, SUMSQ>(p, eo, wsl, WS, aoff, boff, rsrow, row0, col_w, r_l, c8, np, rp); break
@@ -1429,7 +1434,6 @@ extern "C" int th_gemm(const th_gemm_desc* d, void* stream) {
   for (int e = 0; e < d->n_extra; ++e) {
     TH_CHECK_ARG(d->extra[e] != nullptr, "th_gemm: extra[%d] is null", e);
     TH_CHECK_ARG(d->extra_dtype[e] == TH_BF16 || d->extra_dtype[e] == TH_F32, "th_gemm: extra_dtype[%d] unsupported", e);
-    TH_CHECK_ARG(d->ld_extra[e] >= d->N, "th_gemm: ld_extra[%d] < N", e);
     k.extra[e] = d->extra[e];
     k.ld_extra[e] = d->ld_extra[e];
     k.extra_dtype[e] = d->extra_dtype[e];
@@ -1446,7 +1450,14 @@ extern "C" int th_gemm(const th_gemm_desc* d, void* stream) {
     TH_CHECK_ARG(!uses_b || (eo.b >= 0 && eo.b < d->n_acc), "th_gemm: out[%d].b=%d out of range", o, eo.b);
     const bool uses_e = eo.op == TH_EPI_ADD || eo.op == TH_EPI_SOFTPLUS_ADD || eo.op == TH_EPI_MUL;
     TH_CHECK_ARG(!uses_e || (eo.e >= 0 && eo.e < d->n_extra), "th_gemm: out[%d].e=%d out of range", o, eo.e);
-    TH_CHECK_ARG(eo.ptr != nullptr && eo.ld >= d->N, "th_gemm: out[%d] null or ld < N", o);
+    const int64_t cb = eo.col_begin, ce = eo.col_end ? eo.col_end : d->N;
+    TH_CHECK_ARG(cb >= 0 && cb < ce && ce <= d->N && cb % 8 == 0 && (ce % 8 == 0 || ce == d->N),
+                 "th_gemm: out[%d] column window [%lld, %lld) must lie in [0, N=%lld) on multiples of 8", o,
+                 (long long)cb, (long long)ce, (long long)d->N);
+    TH_CHECK_ARG(d->in_dtype != TH_F8E4M3 || (cb == 0 && ce == d->N),
+                 "th_gemm: out[%d]: column windows are for bf16 / fp32 inputs", o);
+    TH_CHECK_ARG(eo.ptr != nullptr && eo.ld >= ce - cb, "th_gemm: out[%d] null or ld < its width", o);
+    TH_CHECK_ARG(!uses_e || d->ld_extra[eo.e] >= ce - cb, "th_gemm: out[%d] extra row stride < its width", o);
     TH_CHECK_ARG(eo.dtype == TH_BF16 || eo.dtype == TH_F32, "th_gemm: out[%d].dtype unsupported", o);
     need_rope |= eo.op == TH_EPI_ROPE || eo.op == TH_EPI_ROPE_PAIR;
     k.out[o].op = eo.op;
@@ -1459,6 +1470,12 @@ extern "C" int th_gemm(const th_gemm_desc* d, void* stream) {
     const int ob = eo.dtype == TH_F32 ? 16 : 8;
     k.out[o].vec = aligned(eo.ptr, ob) && eo.ld % 4 == 0;
     k.out[o].vec8 = aligned(eo.ptr, 16) && eo.ld % (eo.dtype == TH_F32 ? 4 : 8) == 0;
+    k.out[o].cb = (int)cb;
+    k.out[o].ce = (int)ce;
+    if (eo.op == TH_EPI_ROPE || eo.op == TH_EPI_ROPE_PAIR) {
+      TH_CHECK_ARG(d->rope_head_dim > 0 && cb % d->rope_head_dim == 0,
+                   "th_gemm: out[%d] RoPE window must start on a head (head_dim %d)", o, d->rope_head_dim);
+    }
     if (eo.op == TH_EPI_ROPE) {
       TH_CHECK_ARG(d->rope_head_dim > 0 && bn % d->rope_head_dim == 0,
                    "th_gemm: fused RoPE needs the column tile (%d) to hold whole heads (head_dim %d)", bn,

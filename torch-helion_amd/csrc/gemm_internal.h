@@ -11,6 +11,7 @@ struct EpiOutK {
   int64_t ld;
   int dtype, vec;  // vec: 4-element vector access possible
   int vec8;        // 8-element (16-byte bf16 / 2 x 16-byte fp32) access possible
+  int cb, ce;      // accumulator columns [cb, ce) land at output columns 0 .. ce - cb
 };
 
 struct GemmK {

@@ -48,6 +48,9 @@ class CompileConfig:
     fuse_rope: bool = True
     fp32_outputs: bool = True                     # producers of program outputs also write an fp32 copy
     residual_fp32: bool = True                    # residual operands of GEMM epilogues travel in fp32
+    merge_siblings: bool = False                  # GEMM kernels sharing an lhs run as one launch (column windows);
+                                                  # off: at C2/C4 the concatenated width adds a ragged tile column
+                                                  # (288 blocks on 256 CUs) and costs more than the launches it saves
     cpu_flop_budget: float = 2e10                 # graphs above this skip CPU-side checks in "auto" mode
 
     @property

@@ -13,7 +13,7 @@ from pathlib import Path
 
 from .build import LIB_PATH
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 # th_status
 TH_OK = 0
@@ -45,7 +45,7 @@ _i64 = C.c_int64
 
 class EpiOut(C.Structure):
     _fields_ = [("op", _i32), ("a", _i32), ("b", _i32), ("e", _i32), ("ptr", _p), ("ld", _i64),
-                ("dtype", _i32), ("pad_", _i32)]
+                ("dtype", _i32), ("col_begin", _i32), ("col_end", _i32), ("pad_", _i32)]
 
 
 class GemmDesc(C.Structure):

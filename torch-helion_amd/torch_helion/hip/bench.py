@@ -58,8 +58,15 @@ def bench_program(dp, inputs, hw: HardwareSpec, warmup: int = 10, reps: int = 50
         entry["entries"].append(l.entry)
         entry["us"] += statistics.mean(times)
     for name, entry in kernels.items():
-        cb = kernel_cost(specs[name], dp.program.tensors, hw)
-        dtype = _kernel_dtype(specs[name], dp.program)
+        # a launch that merged sibling kernels ("k0_gemm+k2_gemm") carries their summed work
+        members = [specs[n] for n in name.split("+")]
+        costs = [kernel_cost(sp, dp.program.tensors, hw) for sp in members]
+        cb = costs[0]
+        if len(costs) > 1:
+            bound = "mfma" if any(c.bound == "mfma" for c in costs) else costs[0].bound
+            cb = type(cb)(**{**cb.__dict__, "flops": sum(c.flops for c in costs), "bytes": sum(c.bytes for c in costs),
+                             "bound": bound})
+        dtype = _kernel_dtype(members[0], dp.program)
         entry.update({"flops": cb.flops, "bytes": cb.bytes, "bound": cb.bound})
         sec = entry["us"] * 1e-6
         if cb.bound == "mfma":

@@ -72,13 +72,15 @@ def pack_rhs(ws: Sequence[torch.Tensor], dtype: torch.dtype, out: torch.Tensor |
 
 @dataclass
 class EpiSpec:
-    """One fused output of th_gemm (see th_epi_op in include/th_hip.h)."""
+    """One fused output of th_gemm (see th_epi_op in include/th_hip.h). ``cols``: the
+    accumulator column window [begin, end) the output holds (None: all N columns)."""
 
     op: int
     out: torch.Tensor
     a: int = 0
     b: int = -1
     e: int = -1
+    cols: tuple[int, int] | None = None
 
 
 @dataclass
@@ -137,6 +139,8 @@ class GemmCall:
             e.ptr = o.out.data_ptr()
             e.ld = _row_major(o.out, "th_gemm out")
             e.dtype = th_dtype(o.out)
+            if o.cols is not None:
+                e.col_begin, e.col_end = o.cols
         if self.sumsq_out is not None:
             d.sumsq_out = self.sumsq_out.data_ptr()
         return d

@@ -45,7 +45,8 @@ class DeviceProgram:
     """A Program lowered and bound for execution on ``device``."""
 
     def __init__(self, program: Program, params: dict[str, torch.Tensor], device: int | torch.device = 0,
-                 fuse_rope: bool = True, fp32_outputs: bool = True, residual_fp32: bool = True) -> None:
+                 fuse_rope: bool = True, fp32_outputs: bool = True, residual_fp32: bool = True,
+                 merge_siblings: bool = False) -> None:
         self.program = program
         self.device = torch.device("cuda", device) if isinstance(device, int) else torch.device(device)
         if self.device.type != "cuda":
@@ -98,8 +99,14 @@ class DeviceProgram:
             if k.kind == "embedding" and k.arg("ids").tensor in program.inputs:
                 ids = k.arg("ids").tensor
                 self._vocab[ids] = min(self._vocab.get(ids, k.attrs["vocab"]), k.attrs["vocab"])
+        self._merge_groups, self._merged_away = self._plan_sibling_merges(program) if merge_siblings else ({}, set())
         for k in program.kernels:
-            self.launches.extend(self._lower(k))
+            if k.name in self._merged_away:
+                continue
+            if k.name in self._merge_groups:
+                self.launches.extend(self._lower_gemm_merged(self._merge_groups[k.name]))
+            else:
+                self.launches.extend(self._lower(k))
 
     # -------------------------------------------------------------- running
     def set_inputs(self, inputs: dict[str, torch.Tensor] | list[torch.Tensor] | tuple) -> None:
@@ -387,6 +394,109 @@ class DeviceProgram:
 
         self.plans[spec.name] = info
         return [Launch(spec.name, "gemm", run, "th_gemm", info)]
+
+    # sibling merge --------------------------------------------------------
+    # GEMM kernels that multiply the same lhs by weights (projections of one
+    # input that the partition kept apart because their widths or epilogue ops
+    # differ) run as ONE th_gemm: the used weight columns of every kernel are
+    # concatenated into one accumulator, and each output keeps its op on its own
+    # column window. One launch reads the lhs once and fills the GPU with the
+    # sum of the widths instead of several small grids.
+    _MERGE_OPS = (abi.EPI_ACC, abi.EPI_SILU, abi.EPI_ADD, abi.EPI_SOFTPLUS_ADD, abi.EPI_MUL)
+
+    def _merge_key(self, k: KernelSpec):
+        if k.kind != "gemm" or not k.gemms:
+            return None
+        lhs_t = k.arg("lhs").tensor
+        if self.buffers[lhs_t].dtype != torch.bfloat16 or k.grid["cols"] % 8:
+            return None
+        plan = match_epilogue(k)
+        if not plan.fused or not plan.outs:
+            return None
+        if any(o.op not in self._MERGE_OPS or o.rope is not None or o.b >= 0 for o in plan.outs):
+            return None
+        used = sorted({o.a for o in plan.outs})
+        if any(k.arg(k.gemms[a].rhs).tensor not in self.program.params for a in used):
+            return None
+        flags = {bool(plan.scaled.get(a, False)) for a in used}
+        if len(flags) != 1:
+            return None
+        return (lhs_t, k.k_extent, plan.rscale, flags.pop()), plan, used
+
+    def _plan_sibling_merges(self, program: Program):
+        """Leader kernel name -> [(spec, plan, used accumulators)] in launch
+        order; the other members launch with their leader (they read only the
+        shared lhs, parameters and tensors ready before the leader)."""
+        produced_at = {o.tensor: i for i, k in enumerate(program.kernels) for o in k.outputs}
+        keyed = [(i, k, self._merge_key(k)) for i, k in enumerate(program.kernels)]
+        groups: dict[str, list] = {}
+        away: set[str] = set()
+        for i, k, m in keyed:
+            if m is None or k.name in away:
+                continue
+            key, plan, used = m
+            members = [(k, plan, used)]
+            n_out = sum(1 + (o.tensor in self.shadow) for o in plan.outs)
+            extras = {k.arg(o.extra).tensor for o in plan.outs if o.extra is not None}
+            for j, k2, m2 in keyed[i + 1:]:
+                if m2 is None or k2.name in away or m2[0] != key:
+                    continue
+                _, plan2, used2 = m2
+                ext2 = {k2.arg(o.extra).tensor for o in plan2.outs if o.extra is not None}
+                ready = all(t in program.params or produced_at.get(t, len(program.kernels)) < i for t in ext2)
+                n2 = n_out + sum(1 + (o.tensor in self.shadow) for o in plan2.outs)
+                if not ready or n2 > abi.MAX_OUT or len(extras | ext2) > abi.MAX_EXTRA:
+                    continue
+                members.append((k2, plan2, used2))
+                n_out, extras = n2, extras | ext2
+            if len(members) > 1:
+                groups[k.name] = members
+                away.update(m[0].name for m in members[1:])
+        return groups, away
+
+    def _lower_gemm_merged(self, members) -> list[Launch]:
+        lead = members[0][0]
+        lhs = self.buffers[lead.arg("lhs").tensor]
+        T, K = lead.grid["rows"], lead.k_extent
+        plan0 = members[0][1]
+        cols: dict[tuple[str, int], tuple[int, int]] = {}
+        weights: list[torch.Tensor] = []
+        n_tot = 0
+        for spec, plan, used in members:
+            n = spec.grid["cols"]
+            for a in used:
+                w = self.buffers[spec.arg(spec.gemms[a].rhs).tensor]
+                weights.append(w if w.dtype in (torch.float32, torch.bfloat16) else w.float())
+                cols[(spec.name, a)] = (n_tot, n_tot + n)
+                n_tot += n
+        packed = ops.pack_rhs([torch.cat([w.float() for w in weights], dim=1).contiguous()], torch.bfloat16)
+        extras: list[str] = []
+        epi = []
+        for spec, plan, _ in members:
+            for o in plan.outs:
+                e = -1
+                if o.extra is not None:
+                    t = spec.arg(o.extra).tensor
+                    if t not in extras:
+                        extras.append(t)
+                    e = extras.index(t)
+                for buf in [self.buffers[o.tensor]] + ([self.shadow[o.tensor]] if o.tensor in self.shadow else []):
+                    epi.append(ops.EpiSpec(o.op, buf, a=0, e=e, cols=cols[(spec.name, o.a)]))
+        extra_bufs = [self.operand(t) for t in extras]
+        scaled = bool(plan0.scaled.get(members[0][2][0], False))
+        inv_k, eps = plan0.rscale if plan0.rscale else (0.0, 0.0)
+        names = [m[0].name for m in members]
+        info = {"n_acc": 1, "merged": names, "cols": n_tot, "ops": [x.op for x in epi], "rscale": plan0.rscale is not None,
+                "rope_fused": False}
+
+        def run() -> None:
+            ops.gemm(ops.GemmCall(T, n_tot, K, 1, lhs, packed, epi, sumsq=plan0.rscale is not None,
+                                  rscale_mask=1 if scaled else 0, inv_k=inv_k, eps=eps, extras=extra_bufs),
+                     kernel="+".join(names))
+
+        for n in names:
+            self.plans[n] = info
+        return [Launch("+".join(names), "gemm", run, "th_gemm", info)]
 
     # generic path ---------------------------------------------------------
     def _lower_gemm_vm(self, spec: KernelSpec) -> list[Launch]:

@@ -146,7 +146,8 @@ def compile_model(model: torch.nn.Module, example_args: Sequence[Any], config: C
             from .hip.runtime import DeviceProgram
 
             device_program = DeviceProgram(program, graph.params, config.device, fuse_rope=config.fuse_rope,
-                                           fp32_outputs=config.fp32_outputs, residual_fp32=config.residual_fp32)
+                                           fp32_outputs=config.fp32_outputs, residual_fp32=config.residual_fp32,
+                                           merge_siblings=config.merge_siblings)
             rw.write_json("kernels/launches.json", [{"kernel": l.kernel, "entry": l.entry, "info": l.info}
                                                     for l in device_program.launches])
 
