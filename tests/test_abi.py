@@ -116,13 +116,14 @@ def test_gemm_rejects_bad_column_windows(lib, window, ld, msg):
     assert msg in abi.last_error(lib)
 
 
-def test_gemm_column_windows_only_for_bf16_and_fp32(lib):
+def test_gemm_column_windows_accepted_for_fp8(lib):
+    """e4m3 weights take column windows too: a valid window passes every argument check (the
+    call then stops at the missing device, not at the window)."""
     from torch_helion.hip import abi
 
     d = _gemm_desc(in_dtype=abi.TH_F8E4M3, rhs_scale=16384, workspace=20480, workspace_bytes=1 << 30)
     d.out[0].col_begin, d.out[0].col_end = 0, 32
-    assert lib.th_gemm(C.byref(d), None) == abi.TH_ERR_INVALID
-    assert "bf16 / fp32" in abi.last_error(lib), abi.last_error(lib)
+    assert lib.th_gemm(C.byref(d), None) == abi.TH_ERR_NOT_INIT, abi.last_error(lib)
 
 
 @pytest.mark.parametrize("field,value,msg", [

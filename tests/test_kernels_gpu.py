@@ -224,22 +224,27 @@ def _quant_e4m3(w: torch.Tensor):
 
 
 @pytest.mark.parametrize("M,N,K,case", [(64, 4096, 4096, "add"), (64, 1024, 4096, "rope_kv"),
-                                        (37, 2048, 1024, "swiglu"), (100, 512, 512, "acc")])
+                                        (37, 2048, 1024, "swiglu"), (100, 512, 512, "acc"),
+                                        (16, 1024, 2048, "add"), (20, 256, 992, "acc"),
+                                        (64, 14336, 512, "swiglu"), (32, 24576, 256, "rope_q")])
 def test_gemm_fp8_weights(gpu, M, N, K, case):
     """bf16 activations x e4m3 weights with per-column scales (the decode projections), split-K,
-    against fp32 math on the dequantised weights."""
+    against fp32 math on the dequantised weights. K a multiple of 128 takes the shared-activation
+    kernel (32-, 64- and 128-row variants here); K = 992 the per-wave split-K kernel. The two
+    widest cases run as one split whose workgroups finish their tiles themselves (SwiGLU pairs
+    and RoPE partners inside a tile); the others go through the reduce pass."""
     from torch_helion.hip import abi, ops
 
     announce(f"gemm fp8 weights M={M} N={N} K={K} {case}")
     g = torch.Generator().manual_seed(M + N + K)
-    n_acc = {"add": 1, "rope_kv": 2, "swiglu": 2, "acc": 1}[case]
+    n_acc = {"add": 1, "rope_kv": 2, "swiglu": 2, "acc": 1, "rope_q": 1}[case]
     x = torch.randn(M, K, generator=g).bfloat16()
     qs = [_quant_e4m3(torch.randn(K, N, generator=g) * 0.02) for _ in range(n_acc)]
     wdq = [q.float() * s[None, :] for q, s in qs]
     xf = x.float()
     accs = [xf @ w for w in wdq]
     kw = {}
-    if case in ("rope_kv", "swiglu"):
+    if case in ("rope_kv", "swiglu", "rope_q"):
         r = ((xf * xf).sum(-1, keepdim=True) / K + 1e-5).pow(-0.5)
         accs = [a * r for a in accs]
         kw = dict(sumsq=True, rscale_mask=(1 << n_acc) - 1, inv_k=1.0 / K, eps=1e-5)
@@ -256,6 +261,13 @@ def test_gemm_fp8_weights(gpu, M, N, K, case):
         refs = [accs[0] * c1.repeat(M, N // hd) + _rot_heads(accs[0], hd) * s1.repeat(M, N // hd), accs[1]]
         kw.update(rope_cos=c1.to(gpu), rope_sin=s1.to(gpu), rope_head_dim=hd, rope_period=1)
         ops_ = [(abi.EPI_ROPE, 0, -1, -1), (abi.EPI_ACC, 1, -1, -1)]
+    elif case == "rope_q":
+        hd, pos = 128, 77
+        cos, sin = _rope_tables(pos + 1, hd, theta=10000.0)
+        c1, s1 = cos[pos:pos + 1].contiguous(), sin[pos:pos + 1].contiguous()
+        refs = [accs[0] * c1.repeat(M, N // hd) + _rot_heads(accs[0], hd) * s1.repeat(M, N // hd)]
+        kw.update(rope_cos=c1.to(gpu), rope_sin=s1.to(gpu), rope_head_dim=hd, rope_period=1)
+        ops_ = [(abi.EPI_ROPE, 0, -1, -1)]
     elif case == "swiglu":
         refs = [accs[0] * torch.sigmoid(accs[0]) * accs[1]]
         ops_ = [(abi.EPI_SWIGLU, 0, 1, -1)]
@@ -275,6 +287,70 @@ def test_gemm_fp8_weights(gpu, M, N, K, case):
     for i, ref in enumerate(refs):
         assert _rel(o32[i], ref) < 1e-4, (case, i, _rel(o32[i], ref))
         assert _maxabs(o16[i], ref) < BF16_TOL, (case, i)
+
+
+@pytest.mark.parametrize("M,N,K", [(64, 2048, 1024), (32, 24576, 256)])
+def test_gemm_fp8_column_windows(gpu, M, N, K):
+    """e4m3 weights, one accumulator split into column-window outputs (the merged q | k | v
+    projection of the decode step): RoPE on the first half, add-extra on the second (the extra
+    read at the window-relative column). N = 2048 goes through the reduce pass, N = 24576 is a
+    single split finished inside the main kernel."""
+    from torch_helion.hip import abi, ops
+
+    announce(f"gemm fp8 column windows M={M} N={N} K={K}")
+    g = torch.Generator().manual_seed(N + K)
+    x = torch.randn(M, K, generator=g).bfloat16()
+    q, s = _quant_e4m3(torch.randn(K, N, generator=g) * 0.02)
+    acc = x.float() @ (q.float() * s[None, :])
+    hd, pos, h = 128, 9, N // 2
+    cos, sin = _rope_tables(pos + 1, hd, theta=10000.0)
+    c1, s1 = cos[pos:pos + 1].contiguous(), sin[pos:pos + 1].contiguous()
+    a0 = acc[:, :h]
+    ref0 = a0 * c1.repeat(M, h // hd) + _rot_heads(a0, hd) * s1.repeat(M, h // hd)
+    extra = torch.randn(M, N - h, generator=g)
+    ref1 = acc[:, h:] + extra
+    packed = ops.pack_rhs([q.to(gpu)], torch.float8_e4m3fn)
+    ws = torch.empty(ops.gemm_workspace_bytes(M, N, K, 1, torch.float8_e4m3fn), dtype=torch.uint8, device=gpu)
+    o0 = torch.full((M, h), float("nan"), device=gpu)
+    o1 = torch.full((M, N - h), float("nan"), device=gpu)
+    ops.gemm(ops.GemmCall(M, N, K, 1, x.to(gpu), packed,
+                          [ops.EpiSpec(abi.EPI_ROPE, o0, a=0, cols=(0, h)),
+                           ops.EpiSpec(abi.EPI_ADD, o1, a=0, e=0, cols=(h, N))],
+                          extras=[extra.to(gpu)], in_dtype=torch.float8_e4m3fn, rhs_scale=s[None, :].to(gpu).contiguous(),
+                          workspace=ws, rope_cos=c1.to(gpu), rope_sin=s1.to(gpu), rope_head_dim=hd, rope_period=1))
+    torch.cuda.synchronize()
+    assert _rel(o0, ref0) < 1e-4 and _rel(o1, ref1) < 1e-4, (_rel(o0, ref0), _rel(o1, ref1))
+
+
+def test_gemm_fp8_workspace_reuse(gpu):
+    """One workspace, holding garbage (0xff bytes: NaN floats) to begin with, serves fp8 calls
+    of different shapes in any order: no call depends on what an earlier one left in it."""
+    from torch_helion.hip import abi, ops
+
+    announce("gemm fp8 shared workspace A B A B")
+    g = torch.Generator().manual_seed(11)
+    shapes = [(64, 1024, 2048, 1), (48, 512, 1024, 2)]
+    cases = []
+    for M, N, K, n_acc in shapes:
+        x = torch.randn(M, K, generator=g).bfloat16()
+        qs = [_quant_e4m3(torch.randn(K, N, generator=g) * 0.02) for _ in range(n_acc)]
+        accs = [x.float() @ (q.float() * s[None, :]) for q, s in qs]
+        packed = ops.pack_rhs([q.to(gpu) for q, _ in qs], torch.float8_e4m3fn)
+        scale = torch.stack([s for _, s in qs]).to(gpu).contiguous()
+        outs = [torch.empty(M, N, device=gpu) for _ in range(n_acc)]
+        cases.append((M, N, K, n_acc, x.to(gpu), packed, scale, outs, accs))
+    nbytes = max(ops.gemm_workspace_bytes(M, N, K, n_acc, torch.float8_e4m3fn) for M, N, K, n_acc in shapes)
+    ws = torch.full((nbytes,), 255, dtype=torch.uint8, device=gpu)
+    for rep in range(2):
+        for M, N, K, n_acc, x, packed, scale, outs, accs in cases:
+            for o in outs:
+                o.fill_(float("nan"))
+            specs = [ops.EpiSpec(abi.EPI_ACC, o, a=i) for i, o in enumerate(outs)]
+            ops.gemm(ops.GemmCall(M, N, K, n_acc, x, packed, specs, in_dtype=torch.float8_e4m3fn,
+                                  rhs_scale=scale, workspace=ws))
+            torch.cuda.synchronize()
+            for o, ref in zip(outs, accs):
+                assert _rel(o, ref) < 1e-4, (rep, M, N, K)
 
 
 def test_gemm_extra_ops(gpu):

@@ -27,7 +27,6 @@ struct AttnK {
   float scale_log2;
 };
 
-typedef __attribute__((address_space(3))) void* lds_ptr_t;
 typedef short s16x4_t __attribute__((ext_vector_type(4)));
 
 // K and V tiles stream from HBM straight into LDS (global_load_lds_dwordx4,

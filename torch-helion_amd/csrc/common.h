@@ -14,6 +14,29 @@ namespace th {
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
 typedef __attribute__((ext_vector_type(16))) float f32x16_t;
 typedef __attribute__((ext_vector_type(4))) float f32x4_t;
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// Wait until at most N of this wave's vector-memory operations (loads, stores,
+// direct-to-LDS loads; they retire in issue order) are outstanding.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  // s_waitcnt fields (gfx9): vmcnt[3:0], expcnt[6:4], lgkmcnt[11:8], vmcnt_hi[15:14]
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Workgroup barrier that leaves global loads in flight (__syncthreads, and
+// even an LDS-only workgroup fence once direct-to-LDS loads are pending,
+// drain all of them). The wavefront-scope fences only keep the compiler from
+// moving memory accesses across the barrier; the caller provides what the
+// hardware needs: each wave has consumed its earlier LDS reads (their values
+// were used before the barrier) and has waited, with wait_vmcnt, for its own
+// direct-to-LDS loads whose data other waves read after the barrier.
+__device__ __forceinline__ void barrier_keep_loads() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
 
 // ------------------------------------------------------------ bf16 helpers
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) {

@@ -511,15 +511,6 @@ __global__ void __launch_bounds__(256, 1) gemm_bf16_kernel(GemmK p) {
 // step ks run; the barrier sits in the middle of the last step, after which the
 // first fragments of tile kt+1 are read and the loads of tile kt+2 issued into
 // the stage everyone has just finished reading.
-typedef __attribute__((address_space(3))) void* lds_ptr_t;
-
-
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  // s_waitcnt fields (gfx9): vmcnt[3:0], expcnt[6:4], lgkmcnt[11:8], vmcnt_hi[15:14]
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
 
 // Wait until at most n tiles of PER loads each are still in flight (n < 4).
 template <int PER>
@@ -1197,6 +1188,9 @@ __global__ void __launch_bounds__(256) pack_rhs_fp8_kernel(PackK p) {
 
 // Per-accumulator column tile bn; the block tile is n_acc * bn columns.
 static int choose_bn(int64_t N, int n_acc, int in_dtype) {
+  // e4m3 weights: 128-column packed tiles, the shared-activation kernel's
+  // workgroup (both SwiGLU halves of a column stay inside one workgroup)
+  if (in_dtype == TH_F8E4M3 && (n_acc == 1 || n_acc == 2) && N >= 128) return 128 / n_acc;
   if (in_dtype == TH_F32) {
     switch (n_acc) {
       case 1: return N > 64 ? 128 : 64;
@@ -1265,7 +1259,7 @@ extern "C" int64_t th_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int3
   if (M <= 0 || N <= 0 || K <= 0 || n_acc < 1 || n_acc > TH_MAX_ACC || !gemm_in_ok(in_dtype)) return -1;
   if (in_dtype != TH_F8E4M3) return 0;
   const int bn = choose_bn(N, n_acc, in_dtype);
-  return fp8_workspace_bytes(M, cdiv(N, bn) * bn * n_acc, K);
+  return fp8_workspace_bytes(M, cdiv(N, bn) * bn * n_acc, K, bn, n_acc);
 }
 
 extern "C" int th_gemm_pack_rhs(const void* const* src, const int64_t* ld_src, int32_t src_dtype,
@@ -1454,8 +1448,6 @@ extern "C" int th_gemm(const th_gemm_desc* d, void* stream) {
     TH_CHECK_ARG(cb >= 0 && cb < ce && ce <= d->N && cb % 8 == 0 && (ce % 8 == 0 || ce == d->N),
                  "th_gemm: out[%d] column window [%lld, %lld) must lie in [0, N=%lld) on multiples of 8", o,
                  (long long)cb, (long long)ce, (long long)d->N);
-    TH_CHECK_ARG(d->in_dtype != TH_F8E4M3 || (cb == 0 && ce == d->N),
-                 "th_gemm: out[%d]: column windows are for bf16 / fp32 inputs", o);
     TH_CHECK_ARG(eo.ptr != nullptr && eo.ld >= ce - cb, "th_gemm: out[%d] null or ld < its width", o);
     TH_CHECK_ARG(!uses_e || d->ld_extra[eo.e] >= ce - cb, "th_gemm: out[%d] extra row stride < its width", o);
     TH_CHECK_ARG(eo.dtype == TH_BF16 || eo.dtype == TH_F32, "th_gemm: out[%d].dtype unsupported", o);
@@ -1477,7 +1469,8 @@ extern "C" int th_gemm(const th_gemm_desc* d, void* stream) {
                    "th_gemm: out[%d] RoPE window must start on a head (head_dim %d)", o, d->rope_head_dim);
     }
     if (eo.op == TH_EPI_ROPE) {
-      TH_CHECK_ARG(d->rope_head_dim > 0 && bn % d->rope_head_dim == 0,
+      // (e4m3 weights: the reduce pass reads rotation partners from any tile)
+      TH_CHECK_ARG(d->rope_head_dim > 0 && d->rope_head_dim % 2 == 0 && (fp8 || bn % d->rope_head_dim == 0),
                    "th_gemm: fused RoPE needs the column tile (%d) to hold whole heads (head_dim %d)", bn,
                    d->rope_head_dim);
     }

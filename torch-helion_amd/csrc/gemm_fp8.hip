@@ -21,6 +21,9 @@
 //   gemm_fp8_reduce_kernel  sums the splits in a fixed order (deterministic),
 //                           applies s_i[n], the RMS row scale and the fused
 //                           output op, and stores.
+#include <cstdlib>
+#include <type_traits>
+
 #include "common.h"
 #include "gemm_internal.h"
 
@@ -160,32 +163,19 @@ __global__ void __launch_bounds__(256) gemm_fp8_splitk_kernel(Fp8K p) {
   }
 }
 
-// acc_i(m, n) from the partials, scaled: s_i[n] * sum over splits.
-__device__ __forceinline__ float fp8_acc(const Fp8K& p, int i, int64_t m, int64_t n) {
-  const int64_t t = n / p.bn, j = n - t * p.bn;
-  const int64_t row = (t * p.k.n_acc + i) * p.bn + j;
-  float s = 0.f;
-  for (int sp = 0; sp < p.splits; ++sp) s += p.part[((int64_t)sp * p.M + m) * p.Npk + row];
-  return s * p.scale[(int64_t)i * p.N + n];
-}
-
-// One thread per (row m, output column n); every fused output op.
-__global__ void __launch_bounds__(256) gemm_fp8_reduce_kernel(Fp8K p) {
-  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (idx >= (int64_t)p.M * p.N) return;
-  const int64_t m = idx / p.N, n = idx - m * p.N;
+// Every fused output op of element (m, n) (outputs whose column window
+// [cb, ce) holds n, stored at n - cb, extras read there too); accf(i, n') is
+// accumulator i at output column n' (partials summed over the splits,
+// per-column scale applied), rr the row's RMS scale (1 without sumsq).
+template <class AccF>
+__device__ __forceinline__ void fp8_emit(const Fp8K& p, int64_t m, int64_t n, float rr, AccF accf) {
   const GemmK& g = p.k;
-  float rr = 1.f;
-  if (g.sumsq) {
-    float ss = 0.f;
-    for (int sp = 0; sp < p.splits; ++sp) ss += p.sumsq_part[(int64_t)sp * p.M + m];
-    rr = rsqrtf(ss * g.inv_k + g.eps);
-    if (g.sumsq_out && n == 0) g.sumsq_out[m] = ss;
-  }
   for (int o = 0; o < g.n_out; ++o) {
     const EpiOutK& eo = g.out[o];
+    if (n < eo.cb || n >= eo.ce) continue;  // column window: stored at n - cb
+    const int64_t gc = n - eo.cb;
     const int op = eo.op;
-    float a = fp8_acc(p, eo.a, m, n);
+    float a = accf(eo.a, n);
     if ((g.rscale_mask >> eo.a) & 1u) a *= rr;
     float v;
     switch (op) {
@@ -199,10 +189,10 @@ __global__ void __launch_bounds__(256) gemm_fp8_reduce_kernel(Fp8K p) {
         if (op == TH_EPI_ROPE) {
           const int half = g.hd >> 1;
           const int64_t pn = within < half ? n + half : n - half;
-          rot = fp8_acc(p, eo.a, m, pn) * (within < half ? -1.f : 1.f);
+          rot = accf(eo.a, pn) * (within < half ? -1.f : 1.f);
           if ((g.rscale_mask >> eo.a) & 1u) rot *= rr;
         } else {
-          rot = fp8_acc(p, eo.b, m, n);
+          rot = accf(eo.b, n);
           if ((g.rscale_mask >> eo.b) & 1u) rot *= rr;
         }
         const int64_t toff = (m % g.period) * g.hd + within;
@@ -213,13 +203,13 @@ __global__ void __launch_bounds__(256) gemm_fp8_reduce_kernel(Fp8K p) {
         v = a * sigmoidf_(a);
         break;
       case TH_EPI_SWIGLU: {
-        float b = fp8_acc(p, eo.b, m, n);
+        float b = accf(eo.b, n);
         if ((g.rscale_mask >> eo.b) & 1u) b *= rr;
         v = a * sigmoidf_(a) * b;
         break;
       }
       default: {  // TH_EPI_ADD, TH_EPI_SOFTPLUS_ADD, TH_EPI_MUL
-        const float x = load_elem(g.extra[eo.e], m * g.ld_extra[eo.e] + n, g.extra_dtype[eo.e]);
+        const float x = load_elem(g.extra[eo.e], m * g.ld_extra[eo.e] + gc, g.extra_dtype[eo.e]);
         if (op == TH_EPI_MUL) {
           v = a * x;
         } else {
@@ -229,12 +219,343 @@ __global__ void __launch_bounds__(256) gemm_fp8_reduce_kernel(Fp8K p) {
         break;
       }
     }
-    store_elem(eo.ptr, m * eo.ld + n, eo.dtype, v);
+    store_elem(eo.ptr, m * eo.ld + gc, eo.dtype, v);
   }
+}
+
+// Every output op of row m, columns n4 .. n4+3 (n4 a multiple of 4, the 4
+// columns inside one packed tile and one RoPE half-head); sum4(i, nn) is
+// accumulator i at columns nn .. nn+3, scaled.
+template <class Sum4>
+__device__ __forceinline__ void fp8_emit4(const Fp8K& p, int64_t m, int64_t n4, float rr, Sum4 sum4) {
+  const GemmK& g = p.k;
+  float4 c[TH_MAX_ACC];
+  for (int i = 0; i < g.n_acc; ++i) c[i] = sum4(i, n4);
+  float4 pr = make_float4(0.f, 0.f, 0.f, 0.f);  // RoPE partner columns (the other half-head)
+  int pr_i = -1;
+  int64_t pn4 = 0;
+  for (int o = 0; o < g.n_out; ++o)
+    if (g.out[o].op == TH_EPI_ROPE) {
+      const int half = g.hd >> 1;
+      pn4 = (n4 % g.hd) < half ? n4 + half : n4 - half;
+      pr_i = g.out[o].a;
+      pr = sum4(pr_i, pn4);
+      break;
+    }
+  auto lane4 = [](const float4& v, int e) { return e == 0 ? v.x : e == 1 ? v.y : e == 2 ? v.z : v.w; };
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    if (n4 + e >= p.N) break;
+    fp8_emit(p, m, n4 + e, rr, [&](int i, int64_t nn) {
+      if (nn >= n4 && nn < n4 + 4) return lane4(c[i], (int)(nn - n4));
+      return i == pr_i && nn >= pn4 && nn < pn4 + 4 ? lane4(pr, (int)(nn - pn4)) : 0.f;
+    });
+  }
+}
+
+// The outputs of packed tile t (output columns t bn .. +bn of every
+// accumulator) from the workgroup's finished sums, staged in LDS as
+// tl[m][i bn + j] (row stride ld floats); rrs holds the M row scales. One
+// thread per (row, 4 columns).
+__device__ void fp8_tile_out(const Fp8K& p, int t, int tid, const float* tl, int ld, const float* rrs) {
+  const int M = (int)p.M, bn = (int)p.bn, q4 = bn >> 2;
+  const int64_t n0 = (int64_t)t * bn;
+  for (int e = tid; e < M * q4; e += 256) {
+    const int m = e / q4;
+    const int64_t n4 = n0 + ((e - m * q4) << 2);
+    if (n4 >= p.N) continue;
+    const float* row = tl + m * ld - n0;
+    fp8_emit4(p, m, n4, rrs[m], [&](int i, int64_t nn) {
+      const float4 v = *(const float4*)(row + i * bn + nn);
+      const float* sc = p.scale + (int64_t)i * p.N + nn;
+      return make_float4(v.x * sc[0], v.y * sc[1], v.z * sc[2], v.w * sc[3]);
+    });
+  }
+}
+
+// grid (Npk / (128 NG), splits). The four waves of a workgroup own 32 NG
+// packed columns each and share the workgroup's K range: activation slices
+// (KS of K for all 32 TM rows) stream into NBUF rotating LDS buffers by
+// direct loads, cooperatively, while each wave loads its own weights (NG KiB
+// per 32-K chunk, fragment-major) into registers. Both streams run NBUF - 1
+// slices ahead of the MFMAs, so a wave keeps 2 (ALD + WLD) loads in flight;
+// one barrier per slice frees the buffer the next slice lands in.
+// LDS slice layout: row r (one activation row, 2 KS bytes) holds its 16-byte
+// chunk c in slot c ^ (r % 16), so the 32-row operand reads (one chunk per
+// lane) hit distinct banks; the permutation is applied on the load side and
+// the direct loads write 1 KiB (1024 / (2 KS) rows) linearly per instruction.
+template <int TM, int NG, int KS>  // 32-row tiles of M (M <= 32 TM); 32-column groups per wave; K per slice
+__global__ void __launch_bounds__(256, 2) gemm_fp8_lds_kernel(Fp8K p) {
+  constexpr int ROWS = 32 * TM;
+  constexpr int RB = 2 * KS;           // bytes per activation row of a slice
+  constexpr int SLB = ROWS * RB;       // bytes per activation slice
+  constexpr int NBUF = 3;
+  constexpr int ALD = SLB / 1024 / 4;  // activation loads per wave per slice
+  constexpr int RPI = 1024 / RB;       // rows per activation load
+  constexpr int LPR = RB / 16;         // lanes per row in an activation load
+  constexpr int NCH = KS / 32;         // 32-K chunks per slice
+  constexpr int WLD = NCH * NG;        // weight loads per wave per slice
+  constexpr int PARTS = 256 / ROWS;    // threads per row in the sum of squares
+  constexpr int CPP = LPR / PARTS;     // 16-byte chunks per such thread and slice
+  __shared__ __attribute__((aligned(16))) char sa[NBUF * SLB];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int h = lane >> 5, c32 = lane & 31;
+  const int split = blockIdx.y;
+  const int64_t kb = (int64_t)split * p.ksplit;
+  const int nsl = (int)((min(p.K, kb + p.ksplit) - kb) / KS);
+  const int64_t nch = p.ldb / 32;
+  const int64_t g0 = ((int64_t)blockIdx.x * 4 + wave) * NG;  // first 32-row group of this wave
+  const uint8_t* bw = (const uint8_t*)p.B + (g0 * nch + kb / 32) * 1024 + 16 * lane;
+  const char* abase = (const char*)p.A + kb * 2;
+  // row sums of squares: every workgroup when it finishes its tile itself,
+  // else the first column block of each split (for the reduce kernel)
+  const bool do_ss = p.k.sumsq && (p.fused || blockIdx.x == 0);
+
+  // activation load q of this wave fills slice rows RPI (ALD wave + q) + lane / LPR,
+  // slot lane % LPR; rows past M re-read row M - 1 (their sums are dropped)
+  uint32_t aoff[ALD];
+#pragma unroll
+  for (int q = 0; q < ALD; ++q) {
+    const int r = RPI * (ALD * wave + q) + lane / LPR;
+    const int rr = min(r, (int)p.M - 1);
+    aoff[q] = (uint32_t)rr * (uint32_t)p.lda * 2u + (uint32_t)(((lane % LPR) ^ (r & 15)) << 4);
+  }
+
+  uint4 wb[NBUF][NCH][NG];
+  f32x16_t acc[TM][NG];
+#pragma unroll
+  for (int t = 0; t < TM; ++t)
+#pragma unroll
+    for (int g = 0; g < NG; ++g)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[t][g][r] = 0.f;
+  float ss = 0.f;
+
+  // slice j goes to LDS buffer j % NBUF and weight slot j % NBUF
+  // workgroups start their K walk at different slices (rotated), so the
+  // weight streams of concurrent workgroups do not advance in lockstep
+  const int rot = (int)((blockIdx.x * 5u) % (unsigned)nsl);
+  auto issue = [&](int j0, auto slot) {
+    constexpr int SL = decltype(slot)::value;
+    const int j = j0 + rot < nsl ? j0 + rot : j0 + rot - nsl;
+    const char* asrc = abase + (int64_t)j * KS * 2;
+    char* ad = sa + SL * SLB + ALD * wave * 1024;
+#pragma unroll
+    for (int q = 0; q < ALD; ++q)
+      __builtin_amdgcn_global_load_lds((const void*)(asrc + aoff[q]), (lds_ptr_t)(ad + q * 1024), 16, 0, 0);
+    const uint8_t* wsrc = bw + (int64_t)j * NCH * 1024;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c)
+#pragma unroll
+      for (int g = 0; g < NG; ++g) wb[SL][c][g] = *(const uint4*)(wsrc + ((int64_t)g * nch + c) * 1024);
+  };
+  auto compute = [&](auto slot) {
+    constexpr int SL = decltype(slot)::value;
+    const char* ab = sa + SL * SLB + c32 * RB;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      bf16x8_t a[TM][2];
+#pragma unroll
+      for (int t = 0; t < TM; ++t) {
+        a[t][0] = *(const bf16x8_t*)(ab + t * 32 * RB + (((4 * c + 2 * h) ^ (c32 & 15)) << 4));
+        a[t][1] = *(const bf16x8_t*)(ab + t * 32 * RB + (((4 * c + 2 * h + 1) ^ (c32 & 15)) << 4));
+      }
+#pragma unroll
+      for (int g = 0; g < NG; ++g) {
+        const bf16x8_t b0 = fp8x8_to_bf16x8(wb[SL][c][g].x, wb[SL][c][g].y);
+        const bf16x8_t b1 = fp8x8_to_bf16x8(wb[SL][c][g].z, wb[SL][c][g].w);
+#pragma unroll
+        for (int t = 0; t < TM; ++t) {
+          acc[t][g] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[t][0], b0, acc[t][g], 0, 0, 0);
+          acc[t][g] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[t][1], b1, acc[t][g], 0, 0, 0);
+        }
+      }
+    }
+    if (do_ss) {
+      const int row = tid / PARTS, part = tid % PARTS;
+      const char* ar = sa + SL * SLB + row * RB;
+#pragma unroll
+      for (int cc = 0; cc < CPP; ++cc) {
+        const bf16x8_t v = *(const bf16x8_t*)(ar + (((part * CPP + cc) ^ (row & 15)) << 4));
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float x = (float)v[e];
+          ss += x * x;
+        }
+      }
+    }
+  };
+  // Every step issues one slice (past the end: the last slice again, an L2
+  // re-read into a buffer nobody reads), so the in-flight count is the same
+  // at every wait and the compiler needs no waits of its own.
+  auto step = [&](int j, auto slot) {
+    constexpr int SL = decltype(slot)::value;
+    // slice j has landed (only slice j + 1 may still be in flight) and every
+    // wave is done with slice j - 1, whose buffer slice j + 2 reuses
+    wait_vmcnt<ALD + WLD>();
+    barrier_keep_loads();
+    issue(min(j + 2, nsl - 1), std::integral_constant<int, (SL + 2) % NBUF>());
+    compute(slot);
+  };
+
+  issue(0, std::integral_constant<int, 0>());
+  issue(min(1, nsl - 1), std::integral_constant<int, 1>());
+  // whole trips of NBUF steps, then at most two more: no step of a trip is
+  // conditional, so the compiler sees one in-flight pattern at every wait
+  int j = 0;
+  for (; j + NBUF <= nsl; j += NBUF) {
+    step(j, std::integral_constant<int, 0>());
+    step(j + 1, std::integral_constant<int, 1>());
+    step(j + 2, std::integral_constant<int, 2>());
+  }
+  if (j < nsl) step(j, std::integral_constant<int, 0>());
+  if (j + 1 < nsl) step(j + 1, std::integral_constant<int, 1>());
+  wait_vmcnt<0>();  // no direct-to-LDS load may land after the workgroup ends
+
+  if (do_ss) {
+#pragma unroll
+    for (int o = 1; o < PARTS; o <<= 1) ss += __shfl_xor(ss, o);
+  }
+  if (!p.fused) {
+    float* part = p.part + (int64_t)split * p.M * p.Npk;
+#pragma unroll
+    for (int t = 0; t < TM; ++t)
+#pragma unroll
+      for (int g = 0; g < NG; ++g) {
+        const int64_t col = (g0 + g) * 32 + c32;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int m = 32 * t + 8 * (r >> 2) + 4 * h + (r & 3);
+          if (m < p.M) part[(int64_t)m * p.Npk + col] = acc[t][g][r];
+        }
+      }
+    const int row = tid / PARTS;
+    if (do_ss && tid % PARTS == 0 && row < p.M) p.sumsq_part[(int64_t)split * p.M + row] = ss;
+    return;
+  }
+  // One split, every output op inside the tile: finish it here. The
+  // accumulators go to the (now free) slice buffers as tl[m][packed column],
+  // row stride 132 floats, followed by the row scales (one LDS object keeps
+  // the compiler's LDS alias tracking exact, so it adds no waits on the
+  // direct loads).
+  constexpr int LDT = 128 * NG + 4;
+  static_assert(ROWS * LDT * 4 + ROWS * 4 <= NBUF * SLB, "tile staging fits the slice buffers");
+  float* tl = (float*)sa;
+  float* rrs = tl + ROWS * LDT;
+  __syncthreads();
+#pragma unroll
+  for (int t = 0; t < TM; ++t)
+#pragma unroll
+    for (int g = 0; g < NG; ++g)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = 32 * t + 8 * (r >> 2) + 4 * h + (r & 3);
+        tl[m * LDT + (wave * NG + g) * 32 + c32] = acc[t][g][r];
+      }
+  if (tid % PARTS == 0 && tid / PARTS < p.M) {
+    const int row = tid / PARTS;
+    float rr = 1.f;
+    if (p.k.sumsq) {
+      rr = rsqrtf(ss * p.k.inv_k + p.k.eps);
+      if (p.k.sumsq_out && blockIdx.x == 0) p.k.sumsq_out[row] = ss;
+    }
+    rrs[row] = rr;
+  }
+  __syncthreads();
+  fp8_tile_out(p, (int)blockIdx.x, tid, tl, LDT, rrs);
+}
+
+// acc_i(m, n) from the partials, scaled: s_i[n] * sum over splits.
+__device__ __forceinline__ float fp8_acc(const Fp8K& p, int i, int64_t m, int64_t n) {
+  const int64_t t = n / p.bn, j = n - t * p.bn;
+  const int64_t row = (t * p.k.n_acc + i) * p.bn + j;
+  float s = 0.f;
+  for (int sp = 0; sp < p.splits; ++sp) s += p.part[((int64_t)sp * p.M + m) * p.Npk + row];
+  return s * p.scale[(int64_t)i * p.N + n];
+}
+
+// Per-wave split-K kernel's second pass: one thread per (row m, output
+// column n); every fused output op.
+__global__ void __launch_bounds__(256) gemm_fp8_reduce_kernel(Fp8K p) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (int64_t)p.M * p.N) return;
+  const int64_t m = idx / p.N, n = idx - m * p.N;
+  const GemmK& g = p.k;
+  float rr = 1.f;
+  if (g.sumsq) {
+    float ss = 0.f;
+    for (int sp = 0; sp < p.splits; ++sp) ss += p.sumsq_part[(int64_t)sp * p.M + m];
+    rr = rsqrtf(ss * g.inv_k + g.eps);
+    if (g.sumsq_out && n == 0) g.sumsq_out[m] = ss;
+  }
+  fp8_emit(p, m, n, rr, [&](int i, int64_t nn) { return fp8_acc(p, i, m, nn); });
+}
+
+// Second pass after a multi-split launch of the shared-activation kernel:
+// one thread per (row m, 4 consecutive output columns); float4 partial loads
+// (all splits of a column group in flight at once), sums in split order.
+// Requires N % 4 == 0 and a power-of-two bn (so 4 columns share a tile).
+__global__ void __launch_bounds__(256) gemm_fp8_reduce4_kernel(Fp8K p) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t nq = p.N >> 2;
+  if (idx >= p.M * nq) return;
+  const int64_t m = idx / nq, n4 = (idx - m * nq) << 2;
+  const GemmK& g = p.k;
+  const int S = p.splits, na = g.n_acc;
+  const int sh = __builtin_ctz((unsigned)p.bn);
+  const int64_t plane = p.M * p.Npk;
+  // accumulator i at output columns nn .. nn+3 (nn a multiple of 4), scaled
+  auto sum4 = [&](int i, int64_t nn) {
+    const int64_t t = nn >> sh, j = nn & (p.bn - 1);
+    const float* q = p.part + m * p.Npk + ((t * na + i) << sh) + j;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll 8
+    for (int sp = 0; sp < S; ++sp) {
+      const float4 v = *(const float4*)(q + sp * plane);
+      acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
+    }
+    const float4 sc = *(const float4*)(p.scale + (int64_t)i * p.N + nn);
+    return make_float4(acc.x * sc.x, acc.y * sc.y, acc.z * sc.z, acc.w * sc.w);
+  };
+  float rr = 1.f;
+  if (g.sumsq) {
+    float ss = 0.f;
+    for (int sp = 0; sp < S; ++sp) ss += p.sumsq_part[(int64_t)sp * p.M + m];
+    rr = rsqrtf(ss * g.inv_k + g.eps);
+    if (g.sumsq_out && n4 == 0) g.sumsq_out[m] = ss;
+  }
+  fp8_emit4(p, m, n4, rr, sum4);
 }
 
 // Split count: about one workgroup per CU, each wave at least 256 of K.
 static int fp8_groups(int64_t Npk) { return Npk % 64 == 0 ? 2 : 1; }
+
+static int fp8_env(const char* name) {
+  const char* e = getenv(name);
+  return e ? atoi(e) : 0;
+}
+
+// The shared-activation kernel: one workgroup per packed tile of 128 columns
+// (bn = 128 / n_acc), K in whole 128-wide slices. Split count: about one
+// workgroup per CU, a single split once the tiles alone nearly fill the GPU
+// (that launch finishes its tiles itself, without the reduce kernel).
+// TH_FP8_SPLITS overrides the count.
+static bool fp8_lds_ok(int64_t Npk, int64_t K, int bn, int n_acc) {
+  return K % 128 == 0 && bn * n_acc == 128 && Npk % 128 == 0;
+}
+
+static int fp8_lds_splits(int64_t Npk, int64_t K) {
+  static const int forced = fp8_env("TH_FP8_SPLITS");
+  const int64_t nsl = K / 128;
+  if (forced > 0) return (int)std::min((int64_t)forced, nsl);
+  const int64_t cus = device_cus() > 0 ? device_cus() : 256;
+  const int64_t nb = Npk / 128;
+  if (4 * nb >= 3 * cus) return 1;
+  const int64_t s = std::min(cdiv(cus, nb), std::min(nsl, (int64_t)16));
+  return (int)std::max((int64_t)1, s);
+}
 
 static int fp8_splits(int64_t Npk, int64_t K) {
   const int64_t cus = device_cus() > 0 ? device_cus() : 256;
@@ -244,9 +565,9 @@ static int fp8_splits(int64_t Npk, int64_t K) {
   return (int)std::max((int64_t)1, std::min(s, (int64_t)64));
 }
 
-int64_t fp8_workspace_bytes(int64_t M, int64_t Npk, int64_t K) {
-  const int s = fp8_splits(Npk, K);
-  return (int64_t)s * M * (Npk + 1) * 4;
+int64_t fp8_workspace_bytes(int64_t M, int64_t Npk, int64_t K, int bn, int n_acc) {
+  const int64_t s = fp8_lds_ok(Npk, K, bn, n_acc) ? fp8_lds_splits(Npk, K) : fp8_splits(Npk, K);
+  return s * M * (Npk + 1) * 4;
 }
 
 int launch_gemm_fp8(const GemmK& k, int64_t Npk, const float* scale, float* ws, int64_t ws_bytes,
@@ -263,14 +584,44 @@ int launch_gemm_fp8(const GemmK& k, int64_t Npk, const float* scale, float* ws, 
   p.Npk = Npk;
   p.bn = k.bn;
   p.scale = scale;
-  p.splits = fp8_splits(Npk, k.K);
-  p.ksplit = cdiv(cdiv(k.K, p.splits), 128) * 128;  // four waves x a multiple of 32
+  const bool lds = fp8_lds_ok(Npk, k.K, (int)k.bn, k.n_acc);
+  p.splits = lds ? fp8_lds_splits(Npk, k.K) : fp8_splits(Npk, k.K);
+  p.ksplit = cdiv(cdiv(k.K, p.splits), 128) * 128;  // whole slices / four waves x a multiple of 32
   p.splits = (int)cdiv(k.K, p.ksplit);
   const int64_t need = (int64_t)p.splits * k.M * (Npk + 1) * 4;
   TH_CHECK_ARG(ws && ws_bytes >= need, "th_gemm: fp8 weights need a workspace of %lld bytes (got %lld)",
                (long long)need, (long long)ws_bytes);
   p.part = ws;
   p.sumsq_part = k.sumsq ? ws + (int64_t)p.splits * k.M * Npk : nullptr;
+  if (lds) {
+    TH_CHECK_ARG(k.lda < (1 << 24), "th_gemm: fp8 lhs row stride must be under 2^24 elements");
+    // one split finishes in the main kernel when RoPE partners stay in a tile
+    bool local = p.splits == 1;
+    for (int o = 0; o < k.n_out; ++o)
+      if (k.out[o].op == TH_EPI_ROPE && k.bn % k.hd != 0) local = false;
+    p.fused = local ? 1 : 0;
+    const dim3 g1((unsigned)(Npk / 128), (unsigned)p.splits);
+    // (128-wide slices measured as fast as or faster than 256-wide ones at the
+    // Llama-3-8B decode shapes, so only they are instantiated)
+    if (k.M <= 32)
+      hipLaunchKernelGGL((gemm_fp8_lds_kernel<1, 1, 128>), g1, dim3(256), 0, stream, p);
+    else if (k.M <= 64)
+      hipLaunchKernelGGL((gemm_fp8_lds_kernel<2, 1, 128>), g1, dim3(256), 0, stream, p);
+    else
+      hipLaunchKernelGGL((gemm_fp8_lds_kernel<4, 1, 128>), g1, dim3(256), 0, stream, p);
+    TH_CHECK_LAUNCH();
+    if (!p.fused) {
+      bool vec = k.N % 4 == 0 && (k.bn & (k.bn - 1)) == 0;
+      for (int o = 0; o < k.n_out; ++o)
+        if (k.out[o].op == TH_EPI_ROPE && k.hd % 8 != 0) vec = false;  // 4 columns inside one half-head
+      if (vec)
+        hipLaunchKernelGGL(gemm_fp8_reduce4_kernel, dim3((unsigned)cdiv(k.M * (k.N / 4), 256)), dim3(256), 0, stream, p);
+      else
+        hipLaunchKernelGGL(gemm_fp8_reduce_kernel, dim3((unsigned)cdiv(k.M * k.N, 256)), dim3(256), 0, stream, p);
+      TH_CHECK_LAUNCH();
+    }
+    return TH_OK;
+  }
   const int ng = fp8_groups(Npk);
   const dim3 g1((unsigned)(Npk / (32 * ng)), (unsigned)p.splits);
   if (k.M <= 64) {

@@ -52,9 +52,10 @@ struct Fp8K {
   int64_t ksplit;
   float* part;       // [splits][M][Npk]
   float* sumsq_part; // [splits][M]
+  int fused;         // one split finishing its tiles in the main kernel (no reduce pass)
 };
 
-int64_t fp8_workspace_bytes(int64_t M, int64_t Npk, int64_t K);
+int64_t fp8_workspace_bytes(int64_t M, int64_t Npk, int64_t K, int bn, int n_acc);
 int launch_gemm_fp8(const GemmK& k, int64_t Npk, const float* scale, float* ws, int64_t ws_bytes, hipStream_t s);
 
 }  // namespace th

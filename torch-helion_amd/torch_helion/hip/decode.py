@@ -4,16 +4,17 @@ e4m3 weights with per-output-channel scales, a bf16 KV cache.
 The reference has no decode path (its models/llama_block.py:82-105 has no KV
 cache and its OpGraph no fp8 type); this runner is the decode configuration of
 the BASELINE (Llama-3-8B-shaped block, batch 64, cache 4096) built from the same
-kernel library. A step is six launches:
+kernel library. A step is five library calls:
 
-  k0  th_gemm e4m3   q = rope_pos((x r) Wq'),       r = RMS row scale, Wq' = diag(g1) Wq
-  k1  th_gemm e4m3   k = rope_pos((x r) Wk'), v = (x r) Wv'  written straight into
-                     the caches at position ``pos`` (the output row stride is the
-                     cache's sequence stride)
-  k2  th_attention_decode over keys 0..pos
-  k3  th_gemm e4m3   x1 = x + attn Wo
-  k4  th_gemm e4m3   act = silu((x1 r2) Wg') * ((x1 r2) Wu'),  Wg' = diag(g2) Wg
-  k5  th_gemm e4m3   out = x1 + act Wd
+  k0  th_gemm e4m3   [q | k | v] = (x r) [Wq' | Wk' | Wv'],  r = RMS row scale,
+                     W' = diag(g1) W; three column-window outputs: q = rope_pos(.),
+                     k = rope_pos(.) and v written straight into the caches at
+                     position ``pos`` (the output row stride is the cache's
+                     sequence stride)
+  k1  th_attention_decode over keys 0..pos
+  k2  th_gemm e4m3   x1 = x + attn Wo
+  k3  th_gemm e4m3   act = silu((x1 r2) Wg') * ((x1 r2) Wu'),  Wg' = diag(g2) Wg
+  k4  th_gemm e4m3   out = x1 + act Wd
 
 The norm gains are folded into the weights before quantisation (the same fold
 the prefill pipeline makes, reference optimizer/param_transforms.py:18-20), so
@@ -73,17 +74,20 @@ class DecodeBlock:
 
         self._eff: dict[str, torch.Tensor] = {}
 
-        def proj(names: list[str], gain: torch.Tensor | None) -> _Proj:
+        def proj(names: list[str], gain: torch.Tensor | None, concat: bool = False) -> _Proj:
+            """One accumulator per weight, or (concat) one accumulator over the weights'
+            columns side by side; per-output-channel scales either way."""
             qs = [quantize_e4m3(folded(n, gain)) for n in names]
             for n, (q, s) in zip(names, qs):
                 self._eff[n] = (q.float() * s[None, :]).T.contiguous()   # [out, in], what the step multiplies by
+            if concat:
+                qs = [(torch.cat([q.view(torch.uint8) for q, _ in qs], 1).view(_FP8), torch.cat([s for _, s in qs]))]
             k_, n_ = qs[0][0].shape
             packed = ops.pack_rhs([q.to(self.device) for q, _ in qs], _FP8)
             scale = torch.stack([s for _, s in qs]).to(self.device).contiguous()
-            return _Proj(packed, scale, n_, k_, len(names))
+            return _Proj(packed, scale, n_, k_, len(qs))
 
-        self.wq = proj(["attn.q_proj.weight"], g1)
-        self.wkv = proj(["attn.k_proj.weight", "attn.v_proj.weight"], g1)
+        self.wqkv = proj(["attn.q_proj.weight", "attn.k_proj.weight", "attn.v_proj.weight"], g1, concat=True)
         self.wo = proj(["attn.o_proj.weight"], None)
         self.wgu = proj(["mlp.gate_proj.weight", "mlp.up_proj.weight"], g2)
         self.wd = proj(["mlp.down_proj.weight"], None)
@@ -104,7 +108,7 @@ class DecodeBlock:
         ang = torch.cat([ang, ang], -1)
         self.cos = ang.cos().float().to(dev).contiguous()
         self.sin = ang.sin().float().to(dev).contiguous()
-        ws = max(ops.gemm_workspace_bytes(B, p.n, p.k, p.n_acc, _FP8) for p in (self.wq, self.wkv, self.wo, self.wgu, self.wd))
+        ws = max(ops.gemm_workspace_bytes(B, p.n, p.k, p.n_acc, _FP8) for p in (self.wqkv, self.wo, self.wgu, self.wd))
         self.gemm_ws = torch.empty(max(ws, 16), dtype=torch.uint8, device=dev)
         self.graph: torch.cuda.CUDAGraph | None = None
         aw = ops.attention_decode_workspace_bytes(B, heads, kv_heads, self.hd, max_len)
@@ -138,9 +142,11 @@ class DecodeBlock:
         B, kvw = self.B, self.Hkv * self.hd
         kslot = self.k_cache[:, pos].view(B, kvw)
         vslot = self.v_cache[:, pos].view(B, kvw)
-        self._gemm(self.wq, x, [ops.EpiSpec(E.EPI_ROPE, self.q, a=0)], rscale_mask=0b1, **norm, **rope)
-        self._gemm(self.wkv, x, [ops.EpiSpec(E.EPI_ROPE, kslot, a=0), ops.EpiSpec(E.EPI_ACC, vslot, a=1)],
-                   rscale_mask=0b11, **norm, **rope)
+        qw = self.H * self.hd
+        self._gemm(self.wqkv, x, [ops.EpiSpec(E.EPI_ROPE, self.q, a=0, cols=(0, qw)),
+                                  ops.EpiSpec(E.EPI_ROPE, kslot, a=0, cols=(qw, qw + kvw)),
+                                  ops.EpiSpec(E.EPI_ACC, vslot, a=0, cols=(qw + kvw, qw + 2 * kvw))],
+                   rscale_mask=0b1, **norm, **rope)
         ops.attention_decode(self.q, self.k_cache, self.v_cache, self.attn, scale=1.0 / math.sqrt(self.hd),
                              fixed_len=pos + 1, workspace=self.attn_ws)
         self._gemm(self.wo, self.attn, [ops.EpiSpec(E.EPI_ADD, self.x1, e=0), ops.EpiSpec(E.EPI_ADD, self.x1_32, e=0)],
@@ -173,4 +179,4 @@ class DecodeBlock:
         return self.weight_bytes() + kv
 
     def weight_bytes(self) -> int:
-        return sum(p.n * p.k * p.n_acc for p in (self.wq, self.wkv, self.wo, self.wgu, self.wd))
+        return sum(p.n * p.k * p.n_acc for p in (self.wqkv, self.wo, self.wgu, self.wd))
