@@ -48,41 +48,6 @@ __device__ __forceinline__ void map_tile(int tiles_m, int tiles_n, int& tm, int&
   map_tile_id(blockIdx.x, tiles_m, tiles_n, tm, tn);
 }
 
-__device__ __forceinline__ float4 load4(const void* p, int64_t off, int dtype, bool vec, int valid) {
-  float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-  if (vec && valid >= 4) {
-    if (dtype == TH_BF16) {
-      const uint2 w = *(const uint2*)((const uint16_t*)p + off);
-      v.x = __uint_as_float(w.x << 16);
-      v.y = __uint_as_float(w.x & 0xffff0000u);
-      v.z = __uint_as_float(w.y << 16);
-      v.w = __uint_as_float(w.y & 0xffff0000u);
-    } else {
-      v = *(const float4*)((const float*)p + off);
-    }
-    return v;
-  }
-  float t[4] = {0.f, 0.f, 0.f, 0.f};
-  for (int q = 0; q < 4 && q < valid; ++q) t[q] = load_elem(p, off + q, dtype);
-  return make_float4(t[0], t[1], t[2], t[3]);
-}
-
-__device__ __forceinline__ void store4(void* p, int64_t off, int dtype, bool vec, int valid, float4 v) {
-  if (vec && valid >= 4) {
-    if (dtype == TH_BF16) {
-      uint2 w;
-      w.x = (uint32_t)f32_to_bf16(v.x) | ((uint32_t)f32_to_bf16(v.y) << 16);
-      w.y = (uint32_t)f32_to_bf16(v.z) | ((uint32_t)f32_to_bf16(v.w) << 16);
-      *(uint2*)((uint16_t*)p + off) = w;
-    } else {
-      *(float4*)((float*)p + off) = v;
-    }
-    return;
-  }
-  const float t[4] = {v.x, v.y, v.z, v.w};
-  for (int q = 0; q < 4 && q < valid; ++q) store_elem(p, off + q, dtype, t[q]);
-}
-
 // 8 consecutive elements (one 16-byte bf16 or two 16-byte fp32 accesses when
 // vec8, element by element for a ragged end or unaligned rows).
 __device__ __forceinline__ void load8(const void* p, int64_t off, int dtype, bool vec8, int valid, float* v) {

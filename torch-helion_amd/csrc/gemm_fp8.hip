@@ -224,40 +224,107 @@ __device__ __forceinline__ void fp8_emit(const Fp8K& p, int64_t m, int64_t n, fl
 }
 
 // Every output op of row m, columns n4 .. n4+3 (n4 a multiple of 4, the 4
-// columns inside one packed tile and one RoPE half-head); sum4(i, nn) is
-// accumulator i at columns nn .. nn+3, scaled.
+// columns inside one packed tile and one RoPE half-head, column windows on
+// multiples of 8); sum4(i, nn) is accumulator i at columns nn .. nn+3,
+// scaled; n_acc is 1 or 2. Two phases: every load (accumulators, the RoPE partner, extras,
+// RoPE tables) is issued before the first store, so a thread waits for one
+// round of memory latency, not one per output; then one 4-wide store per
+// output.
 template <class Sum4>
 __device__ __forceinline__ void fp8_emit4(const Fp8K& p, int64_t m, int64_t n4, float rr, Sum4 sum4) {
   const GemmK& g = p.k;
-  float4 c[TH_MAX_ACC];
-  for (int i = 0; i < g.n_acc; ++i) c[i] = sum4(i, n4);
-  float4 pr = make_float4(0.f, 0.f, 0.f, 0.f);  // RoPE partner columns (the other half-head)
-  int pr_i = -1;
-  int64_t pn4 = 0;
-  for (int o = 0; o < g.n_out; ++o)
-    if (g.out[o].op == TH_EPI_ROPE) {
-      const int half = g.hd >> 1;
-      pn4 = (n4 % g.hd) < half ? n4 + half : n4 - half;
-      pr_i = g.out[o].a;
-      pr = sum4(pr_i, pn4);
-      break;
-    }
-  auto lane4 = [](const float4& v, int e) { return e == 0 ? v.x : e == 1 ? v.y : e == 2 ? v.z : v.w; };
+  const int valid = (int)min((int64_t)4, p.N - n4);
+  // gather (the shared-activation kernel's packings have one or two accumulators)
+  const float4 c0 = sum4(0, n4);
+  const float4 c1 = g.n_acc > 1 ? sum4(1, n4) : c0;
+  int rope_a = -1;
+  bool tab = false;
+  for (int o = 0; o < g.n_out; ++o) {
+    const EpiOutK& eo = g.out[o];
+    if (n4 < eo.cb || n4 >= eo.ce) continue;
+    if (eo.op == TH_EPI_ROPE) rope_a = eo.a;
+    if (eo.op == TH_EPI_ROPE || eo.op == TH_EPI_ROPE_PAIR) tab = true;
+  }
+  const int within = g.hd > 0 ? (int)n4 % g.hd : 0;
+  const int half = g.hd >> 1;
+  float4 rot = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (rope_a >= 0) rot = sum4(rope_a, within < half ? n4 + half : n4 - half);
+  float4 cs = rot, sn = rot;
+  if (tab) {
+    const int toff = ((int)m % g.period) * g.hd + within;
+    cs = make_float4(g.rcos[toff], g.rcos[toff + 1], g.rcos[toff + 2], g.rcos[toff + 3]);
+    sn = make_float4(g.rsin[toff], g.rsin[toff + 1], g.rsin[toff + 2], g.rsin[toff + 3]);
+  }
+  float4 xe[TH_MAX_OUT];
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    if (n4 + e >= p.N) break;
-    fp8_emit(p, m, n4 + e, rr, [&](int i, int64_t nn) {
-      if (nn >= n4 && nn < n4 + 4) return lane4(c[i], (int)(nn - n4));
-      return i == pr_i && nn >= pn4 && nn < pn4 + 4 ? lane4(pr, (int)(nn - pn4)) : 0.f;
-    });
+  for (int o = 0; o < TH_MAX_OUT; ++o) {
+    xe[o] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (o >= g.n_out) continue;
+    const EpiOutK& eo = g.out[o];
+    const bool uses_e = eo.op == TH_EPI_ADD || eo.op == TH_EPI_SOFTPLUS_ADD || eo.op == TH_EPI_MUL;
+    if (uses_e && n4 >= eo.cb && n4 < eo.ce)
+      xe[o] = load4(g.extra[eo.e], m * g.ld_extra[eo.e] + (n4 - eo.cb), g.extra_dtype[eo.e], g.extra_vec[eo.e] != 0,
+                    (int)min((int64_t)valid, eo.ce - n4));
+  }
+  auto sel = [&](int i) { return i == 1 ? c1 : c0; };
+  auto scl = [](float4 v, float f) { return make_float4(v.x * f, v.y * f, v.z * f, v.w * f); };
+  // emit
+#pragma unroll
+  for (int o = 0; o < TH_MAX_OUT; ++o) {
+    if (o >= g.n_out) continue;
+    const EpiOutK& eo = g.out[o];
+    if (n4 < eo.cb || n4 >= eo.ce) continue;
+    const float4 a = ((g.rscale_mask >> eo.a) & 1u) ? scl(sel(eo.a), rr) : sel(eo.a);
+    float4 v;
+    switch (eo.op) {
+      case TH_EPI_ACC:
+        v = a;
+        break;
+      case TH_EPI_ROPE:
+      case TH_EPI_ROPE_PAIR: {
+        float4 r;
+        if (eo.op == TH_EPI_ROPE) {
+          const float sg = within < half ? -1.f : 1.f;
+          r = scl(rot, ((g.rscale_mask >> eo.a) & 1u) ? sg * rr : sg);
+        } else {
+          r = ((g.rscale_mask >> eo.b) & 1u) ? scl(sel(eo.b), rr) : sel(eo.b);
+        }
+        v = make_float4(a.x * cs.x + r.x * sn.x, a.y * cs.y + r.y * sn.y, a.z * cs.z + r.z * sn.z,
+                        a.w * cs.w + r.w * sn.w);
+        break;
+      }
+      case TH_EPI_SILU:
+        v = make_float4(a.x * sigmoidf_(a.x), a.y * sigmoidf_(a.y), a.z * sigmoidf_(a.z), a.w * sigmoidf_(a.w));
+        break;
+      case TH_EPI_SWIGLU: {
+        const float4 b = ((g.rscale_mask >> eo.b) & 1u) ? scl(sel(eo.b), rr) : sel(eo.b);
+        v = make_float4(a.x * sigmoidf_(a.x) * b.x, a.y * sigmoidf_(a.y) * b.y, a.z * sigmoidf_(a.z) * b.z,
+                        a.w * sigmoidf_(a.w) * b.w);
+        break;
+      }
+      default: {  // TH_EPI_ADD, TH_EPI_SOFTPLUS_ADD, TH_EPI_MUL
+        const float4 x = xe[o];
+        if (eo.op == TH_EPI_MUL) {
+          v = make_float4(a.x * x.x, a.y * x.y, a.z * x.z, a.w * x.w);
+        } else {
+          v = make_float4(a.x + x.x, a.y + x.y, a.z + x.z, a.w + x.w);
+          if (eo.op == TH_EPI_SOFTPLUS_ADD)
+            v = make_float4(softplusf_(v.x), softplusf_(v.y), softplusf_(v.z), softplusf_(v.w));
+        }
+        break;
+      }
+    }
+    store4(eo.ptr, m * eo.ld + (n4 - eo.cb), eo.dtype, eo.vec != 0, (int)min((int64_t)valid, eo.ce - n4), v);
   }
 }
 
 // The outputs of packed tile t (output columns t bn .. +bn of every
 // accumulator) from the workgroup's finished sums, staged in LDS as
-// tl[m][i bn + j] (row stride ld floats); rrs holds the M row scales. One
-// thread per (row, 4 columns).
-__device__ void fp8_tile_out(const Fp8K& p, int t, int tid, const float* tl, int ld, const float* rrs) {
+// tl[m][i bn + j] (row stride ld floats), with the tile's per-column scales
+// at sc[i bn + j]; rrs holds the M row scales. One thread per (row, 4
+// columns).
+__device__ __forceinline__ void fp8_tile_out(const Fp8K& p, int t, int tid, const float* tl, int ld, const float* sc,
+                                             const float* rrs) {
   const int M = (int)p.M, bn = (int)p.bn, q4 = bn >> 2;
   const int64_t n0 = (int64_t)t * bn;
   for (int e = tid; e < M * q4; e += 256) {
@@ -265,10 +332,11 @@ __device__ void fp8_tile_out(const Fp8K& p, int t, int tid, const float* tl, int
     const int64_t n4 = n0 + ((e - m * q4) << 2);
     if (n4 >= p.N) continue;
     const float* row = tl + m * ld - n0;
+    const float* scr = sc - n0;
     fp8_emit4(p, m, n4, rrs[m], [&](int i, int64_t nn) {
       const float4 v = *(const float4*)(row + i * bn + nn);
-      const float* sc = p.scale + (int64_t)i * p.N + nn;
-      return make_float4(v.x * sc[0], v.y * sc[1], v.z * sc[2], v.w * sc[3]);
+      const float4 s4 = *(const float4*)(scr + i * bn + nn);
+      return make_float4(v.x * s4.x, v.y * s4.y, v.z * s4.z, v.w * s4.w);
     });
   }
 }
@@ -441,10 +509,16 @@ __global__ void __launch_bounds__(256, 2) gemm_fp8_lds_kernel(Fp8K p) {
   // the compiler's LDS alias tracking exact, so it adds no waits on the
   // direct loads).
   constexpr int LDT = 128 * NG + 4;
-  static_assert(ROWS * LDT * 4 + ROWS * 4 <= NBUF * SLB, "tile staging fits the slice buffers");
+  static_assert(ROWS * LDT * 4 + ROWS * 4 + 128 * NG * 4 <= NBUF * SLB, "tile staging fits the slice buffers");
   float* tl = (float*)sa;
   float* rrs = tl + ROWS * LDT;
+  float* scl = rrs + ROWS;  // the tile's 128 NG per-column scales, packed-column order
   __syncthreads();
+  for (int c = tid; c < 128 * NG; c += 256) {
+    const int i = c / (int)p.bn, j = c - i * (int)p.bn;
+    const int64_t n = (int64_t)blockIdx.x * p.bn + j;
+    scl[c] = n < p.N ? p.scale[(int64_t)i * p.N + n] : 0.f;
+  }
 #pragma unroll
   for (int t = 0; t < TM; ++t)
 #pragma unroll
@@ -464,7 +538,7 @@ __global__ void __launch_bounds__(256, 2) gemm_fp8_lds_kernel(Fp8K p) {
     rrs[row] = rr;
   }
   __syncthreads();
-  fp8_tile_out(p, (int)blockIdx.x, tid, tl, LDT, rrs);
+  fp8_tile_out(p, (int)blockIdx.x, tid, tl, LDT, scl, rrs);
 }
 
 // acc_i(m, n) from the partials, scaled: s_i[n] * sum over splits.
@@ -543,7 +617,7 @@ static int fp8_env(const char* name) {
 // (that launch finishes its tiles itself, without the reduce kernel).
 // TH_FP8_SPLITS overrides the count.
 static bool fp8_lds_ok(int64_t Npk, int64_t K, int bn, int n_acc) {
-  return K % 128 == 0 && bn * n_acc == 128 && Npk % 128 == 0;
+  return K % 128 == 0 && (n_acc == 1 || n_acc == 2) && bn * n_acc == 128 && Npk % 128 == 0;
 }
 
 static int fp8_lds_splits(int64_t Npk, int64_t K) {
@@ -595,8 +669,14 @@ int launch_gemm_fp8(const GemmK& k, int64_t Npk, const float* scale, float* ws, 
   p.sumsq_part = k.sumsq ? ws + (int64_t)p.splits * k.M * Npk : nullptr;
   if (lds) {
     TH_CHECK_ARG(k.lda < (1 << 24), "th_gemm: fp8 lhs row stride must be under 2^24 elements");
+    // 4-column output groups: inside one tile and one RoPE half-head
+    bool vec = k.N % 4 == 0 && (k.bn & (k.bn - 1)) == 0;
+    for (int o = 0; o < k.n_out; ++o) {
+      if (k.out[o].op == TH_EPI_ROPE && k.hd % 8 != 0) vec = false;
+      if (k.out[o].op == TH_EPI_ROPE_PAIR && k.hd % 4 != 0) vec = false;
+    }
     // one split finishes in the main kernel when RoPE partners stay in a tile
-    bool local = p.splits == 1;
+    bool local = p.splits == 1 && vec;
     for (int o = 0; o < k.n_out; ++o)
       if (k.out[o].op == TH_EPI_ROPE && k.bn % k.hd != 0) local = false;
     p.fused = local ? 1 : 0;
@@ -611,9 +691,6 @@ int launch_gemm_fp8(const GemmK& k, int64_t Npk, const float* scale, float* ws, 
       hipLaunchKernelGGL((gemm_fp8_lds_kernel<4, 1, 128>), g1, dim3(256), 0, stream, p);
     TH_CHECK_LAUNCH();
     if (!p.fused) {
-      bool vec = k.N % 4 == 0 && (k.bn & (k.bn - 1)) == 0;
-      for (int o = 0; o < k.n_out; ++o)
-        if (k.out[o].op == TH_EPI_ROPE && k.hd % 8 != 0) vec = false;  // 4 columns inside one half-head
       if (vec)
         hipLaunchKernelGGL(gemm_fp8_reduce4_kernel, dim3((unsigned)cdiv(k.M * (k.N / 4), 256)), dim3(256), 0, stream, p);
       else
