@@ -627,7 +627,8 @@ static int fp8_lds_splits(int64_t Npk, int64_t K) {
   const int64_t cus = device_cus() > 0 ? device_cus() : 256;
   const int64_t nb = Npk / 128;
   if (4 * nb >= 3 * cus) return 1;
-  const int64_t s = std::min(cdiv(cus, nb), std::min(nsl, (int64_t)16));
+  // as many splits as keep the launch within one round of one workgroup per CU
+  const int64_t s = std::min(std::max((int64_t)1, cus / nb), std::min(nsl, (int64_t)16));
   return (int)std::max((int64_t)1, s);
 }
 
