@@ -209,7 +209,7 @@ typedef struct th_decode_desc {
   int32_t pad_;
   const int32_t* lengths; /* optional [batch] device array of valid keys per sequence (>= 1) */
   const void* q; int64_t ld_q;                         /* [batch, heads_q*head_dim] */
-  const void* k_cache; int64_t k_stride_b, k_stride_t; /* element strides: sequence, token */
+  const void* k_cache; int64_t k_stride_b, k_stride_t; /* element strides: sequence, token (< 2^24) */
   const void* v_cache; int64_t v_stride_b, v_stride_t;
   void* o; int64_t ld_o;                               /* [batch, heads_q*head_dim] */
   float* workspace; int64_t workspace_bytes;

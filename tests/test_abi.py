@@ -168,6 +168,25 @@ def test_attention_rejects_bad_heads(lib):
     assert "under 2^24" in abi.last_error(lib)
 
 
+def test_attention_decode_rejects_wide_token_strides(lib):
+    """The decode kernel keeps a 32-key tile's row offsets in 32 bits: cache token strides of
+    2^24 elements or more are refused before any launch."""
+    from torch_helion.hip import abi
+
+    d = abi.DecodeDesc()
+    d.batch, d.heads_q, d.heads_kv, d.head_dim, d.max_len, d.fixed_len = 2, 8, 2, 128, 64, 64
+    d.dtype, d.scale = abi.TH_BF16, 0.088
+    d.q = d.k_cache = d.v_cache = d.o = 4096
+    d.ld_q = d.ld_o = 8 * 128
+    d.k_stride_t = d.v_stride_t = 1 << 24
+    d.k_stride_b = d.v_stride_b = (1 << 24) * 64
+    assert lib.th_attention_decode(C.byref(d), None) == abi.TH_ERR_INVALID
+    assert "under 2^24" in abi.last_error(lib), abi.last_error(lib)
+    d.k_stride_t = d.v_stride_t = 256
+    d.k_stride_b = d.v_stride_b = 256 * 64
+    assert lib.th_attention_decode(C.byref(d), None) == abi.TH_ERR_NOT_INIT, abi.last_error(lib)
+
+
 def test_valid_descriptor_without_init_stops_before_the_device(lib):
     import torch
     from torch_helion.hip import abi
