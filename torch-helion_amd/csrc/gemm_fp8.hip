@@ -6,21 +6,31 @@
 //
 // Such GEMMs stream every weight byte from HBM once and do little arithmetic
 // per byte, so the work is split along K as well as N until the whole GPU is
-// pulling bandwidth:
+// pulling bandwidth. Every e4m3 value is a bf16 value: the weights are
+// converted exactly (v_cvt_scalef32_pk_bf16_fp8) and multiplied on
+// v_mfma_f32_32x32x16_bf16 with fp32 accumulation.
+//
+// Main path (K a multiple of 128, n_acc 1 or 2, bn = 128 / n_acc):
+//   gemm_fp8_lds_kernel     one workgroup per (128-column packed tile, K split);
+//                           the four waves own 32 columns each and share the
+//                           activation slices, which stream through three
+//                           rotating LDS buffers by direct loads while each
+//                           wave's weights (contiguous KiB blocks of the
+//                           fragment-major packing) go to registers; a single
+//                           split finishes its tiles in the kernel;
+//   gemm_fp8_reduce4_kernel with several splits: sums them in a fixed order
+//                           (deterministic), 4 columns per thread, and applies
+//                           s_i[n], the RMS row scale and the fused output ops.
+// Other shapes:
 //   gemm_fp8_splitk_kernel  one workgroup per (32 packed columns, K range), the
 //                           four waves splitting the range; per 32-K chunk a
-//                           wave loads one contiguous KiB of weights (the
-//                           fragment-major packing of th_gemm_pack_rhs), a lane
+//                           wave loads one contiguous KiB of weights, a lane
 //                           32 contiguous activation bytes (the K order inside a
-//                           chunk is permuted identically for both operands),
-//                           converts the weights with v_cvt_scalef32_pk_bf16_fp8
-//                           (exact: every e4m3 value is a bf16 value) and runs
-//                           v_mfma_f32_32x32x16_bf16; fp32 partial sums per
-//                           split go to the workspace (and, from the first
-//                           column block, partial row sums of squares);
-//   gemm_fp8_reduce_kernel  sums the splits in a fixed order (deterministic),
-//                           applies s_i[n], the RMS row scale and the fused
-//                           output op, and stores.
+//                           chunk is permuted identically for both operands);
+//                           fp32 partial sums per split go to the workspace
+//                           (and, from the first column block, partial row sums
+//                           of squares);
+//   gemm_fp8_reduce_kernel  one thread per output element, same sums and ops.
 #include <cstdlib>
 #include <type_traits>
 
