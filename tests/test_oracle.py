@@ -220,3 +220,83 @@ def test_decode_step_matches_causal_prefill_row_by_row():
         kc[:, t], vc[:, t] = kn, vn
     bad, _, _ = decode_step(x[:, 5], w, kc, vc, 4, **kw)  # planted: cache position off by one
     assert (bad - ref[:, 5]).abs().max() > 1e-3
+
+
+def _ssd_program_operands(bs, s, h, p, n, pad, seed):
+    """Token-major operands of the reference's quadratic ``ssd`` kind (optimizer/evaluate.py:123-138):
+    C/B [T, H*N], x [T, H*P], cum/dt padded to ``pad`` columns per head (value in column 0,
+    garbage in the rest so a wrong column is caught), a [S, S] mask and D broadcast to [T, H*P]."""
+    g = torch.Generator().manual_seed(seed)
+    c = torch.randn(bs * s, h * n, generator=g, dtype=torch.float64)
+    bm = torch.randn(bs * s, h * n, generator=g, dtype=torch.float64)
+    x = torch.randn(bs * s, h * p, generator=g, dtype=torch.float64)
+    dt = torch.rand(bs, s, h, generator=g, dtype=torch.float64) * 0.1 + 0.01
+    A = -(torch.rand(h, generator=g, dtype=torch.float64) * 15 + 1)
+    D = torch.rand(h, generator=g, dtype=torch.float64)
+    cum = torch.cumsum(dt * A, dim=1)                                    # running sum over each sequence
+    cum_pad = torch.randn(bs, s, h, pad, generator=g, dtype=torch.float64) * 50
+    dt_pad = torch.randn(bs, s, h, pad, generator=g, dtype=torch.float64) * 50
+    cum_pad[..., 0], dt_pad[..., 0] = cum, dt
+    d_full = D.repeat_interleave(p).expand(bs * s, h * p).contiguous()
+    return c, bm, x, cum_pad.reshape(bs * s, h * pad), dt_pad.reshape(bs * s, h * pad), d_full, (dt, A, D)
+
+
+def test_interpret_ssd_quadratic_matches_recurrence():
+    """oracle.interpret.ssd_quadratic (the reference's ``ssd`` kind) equals the O(S) recurrence
+    (reference tests/test_mamba.py:27-38) when cum = cumsum(dt*A), the mask is the causal tril and
+    D repeats per head; a full (non-causal) mask or reading cum from the wrong pad column fails."""
+    from oracle.interpret import ssd_quadratic
+    from oracle.mamba import ssd_recurrence
+
+    bs, s, h, p, n, pad = 2, 19, 3, 4, 5, 8
+    c, bm, x, cum_pad, dt_pad, d_full, (dt, A, D) = _ssd_program_operands(bs, s, h, p, n, pad, seed=11)
+    a = {"batch": bs, "seq": s, "heads": h, "head_dim": p, "state_dim": n, "pad": pad}
+    mask = torch.ones(s, s, dtype=torch.float64).tril()
+    y = ssd_quadratic(c, bm, x, cum_pad, dt_pad, mask, d_full, a)
+    x4 = x.reshape(bs, s, h, p).permute(0, 2, 1, 3)
+    b4 = bm.reshape(bs, s, h, n).permute(0, 2, 1, 3)
+    c4 = c.reshape(bs, s, h, n).permute(0, 2, 1, 3)
+    dt3 = dt.permute(0, 2, 1)
+    ref = ssd_recurrence(x4, dt3 * A.reshape(1, h, 1), dt3, b4, c4) + x4 * D.reshape(1, h, 1, 1)
+    ref = ref.permute(0, 2, 1, 3).reshape(bs * s, h * p)
+    assert (y - ref).abs().max() / ref.abs().max() < 1e-10
+    # planted mistakes on the checker's inputs must be caught
+    full = ssd_quadratic(c, bm, x, cum_pad, dt_pad, torch.ones(s, s, dtype=torch.float64), d_full, a)
+    assert (full - ref).abs().max() / ref.abs().max() > 1e-2
+    shifted = ssd_quadratic(c, bm, x, cum_pad.roll(1, dims=1), dt_pad, mask, d_full, a)
+    assert (shifted - ref).abs().max() / ref.abs().max() > 1e-2
+
+
+@pytest.mark.parametrize("h,hk,s,skv,causal", [(4, 4, 17, 17, False), (4, 4, 17, 17, True), (8, 2, 17, 17, True),
+                                                (8, 1, 13, 13, True), (4, 2, 5, 23, True), (4, 2, 9, 23, False)])
+def test_interpret_attention_matches_sdpa(h, hk, s, skv, causal):
+    """oracle.interpret.attention on token-major [T, H*d] operands (the ``attention`` kind,
+    reference optimizer/evaluate.py:139-146, extended with causal masking, grouped KV heads and
+    seq_kv > seq) against torch's scaled_dot_product_attention. For seq_kv > seq the s queries
+    are the LAST s positions of a causal sequence of length seq_kv: their rows must equal those
+    rows of SDPA's full causal attention over all seq_kv positions (bottom-right alignment)."""
+    from oracle.interpret import attention
+
+    bs, d = 2, 16
+    g = torch.Generator().manual_seed(h * 100 + hk * 10 + s)
+    qf = torch.randn(bs, h, skv, d, generator=g, dtype=torch.float64)
+    k = torch.randn(bs, hk, skv, d, generator=g, dtype=torch.float64)
+    v = torch.randn(bs, hk, skv, d, generator=g, dtype=torch.float64)
+    scale = 1.0 / math.sqrt(d)
+    q = qf[:, :, skv - s:]
+
+    def sdpa_rows(k_, v_):
+        if causal:
+            full = F.scaled_dot_product_attention(qf, k_, v_, is_causal=True, enable_gqa=k_.shape[1] != h, scale=scale)
+            return full[:, :, skv - s:]
+        return F.scaled_dot_product_attention(q, k_, v_, enable_gqa=k_.shape[1] != h, scale=scale)
+
+    tok = lambda t: t.permute(0, 2, 1, 3).reshape(bs * t.shape[2], t.shape[1] * d)
+    a = {"batch": bs, "seq": s, "seq_kv": skv, "heads": h, "kv_heads": hk, "head_dim": d, "scale": scale,
+         "causal": causal}
+    out = attention(tok(q), tok(k), tok(v), a)
+    assert (out - tok(sdpa_rows(k, v))).abs().max() < 1e-12
+    if 1 < hk < h:
+        # planted: q heads mapped round-robin onto kv heads instead of in blocks of h / hk
+        rr = torch.arange(h) % hk
+        assert (out - tok(sdpa_rows(k[:, rr], v[:, rr]))).abs().max() > 1e-3
