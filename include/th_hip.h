@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define TH_ABI_VERSION 4
+#define TH_ABI_VERSION 5
 
 typedef enum th_status {
   TH_OK = 0,
@@ -61,6 +61,10 @@ const char* th_last_error(void);
  *   acc_i = lhs[M, K] @ rhs_i[K, N]          (i < n_acc, all sharing lhs)
  *   r     = (sumsq * inv_k + eps) ^ -1/2,    sumsq = sum_k lhs^2   (optional)
  *   a_i   = acc_i * r  if bit i of rscale_mask else acc_i
+ * With lhs_gain (TH_F8E4M3 weights only) the products use lhs[m, k] * g[k]
+ * while sumsq stays the sum of the unscaled lhs^2: the RMSNorm gain sits on
+ * the activation side, (x r g) W = r ((x g) W), so the weights are the
+ * model's own, not diag(g) W (whose quantisation would differ).
  * followed by a fixed catalogue of fused output ops (th_epi_op) that the
  * Python lowering matches against the kernel's epilogue SSA. Epilogues
  * outside the catalogue run as TH_EPI_ACC (fp32) + th_epilogue_vm.
@@ -124,6 +128,7 @@ typedef struct th_gemm_desc {
   const float* rhs_scale; /* TH_F8E4M3: [n_acc][N] fp32, acc_i[:, n] *= rhs_scale[i*N + n] */
   float* workspace;       /* TH_F8E4M3: th_gemm_workspace_bytes(...) bytes */
   int64_t workspace_bytes;
+  const float* lhs_gain;  /* optional [K] fp32 per-column gain of lhs (TH_F8E4M3 only; 16-byte aligned) */
 } th_gemm_desc;
 
 /* Per-accumulator column tile th_gemm uses for (N, n_acc, in_dtype); a block
@@ -207,7 +212,8 @@ typedef struct th_decode_desc {
   int32_t dtype;          /* TH_BF16 for q, caches and o */
   float scale;
   int32_t pad_;
-  const int32_t* lengths; /* optional [batch] device array of valid keys per sequence (>= 1) */
+  const int32_t* lengths; /* optional [batch] device array of valid keys per sequence, 1..max_len
+                             (a value outside that range is clamped to it) */
   const void* q; int64_t ld_q;                         /* [batch, heads_q*head_dim] */
   const void* k_cache; int64_t k_stride_b, k_stride_t; /* element strides: sequence, token (< 2^24) */
   const void* v_cache; int64_t v_stride_b, v_stride_t;

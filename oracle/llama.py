@@ -90,7 +90,8 @@ def block_forward(x: torch.Tensor, w: dict[str, torch.Tensor], *, heads: int, kv
 
 def decode_step(x: torch.Tensor, w: dict[str, torch.Tensor], k_cache: torch.Tensor, v_cache: torch.Tensor, pos: int,
                 *, heads: int, kv_heads: int, eps: float, theta: float,
-                rope: tuple[torch.Tensor, torch.Tensor] | None = None, dtype=torch.float64):
+                rope: tuple[torch.Tensor, torch.Tensor] | None = None, dtype=torch.float64,
+                storage: torch.dtype | None = None):
     """One new token per sequence at position ``pos`` with keys 0..pos-1 cached.
 
     x [b, D]; k_cache, v_cache [b, >= pos, kv_heads, hd] holding the RoPE'd keys
@@ -98,27 +99,39 @@ def decode_step(x: torch.Tensor, w: dict[str, torch.Tensor], k_cache: torch.Tens
     with k_new, v_new [b, kv_heads, hd] the entries for position ``pos``.
     This is block_forward's causal arithmetic for query row ``pos`` only: the
     decode path of the BASELINE's decode configuration (the reference itself
-    has no KV cache)."""
+    has no KV cache).
+
+    ``storage`` (e.g. torch.bfloat16) rounds what a bf16 step keeps in that
+    dtype: the normalised GEMM operands x*g (the RMS row scale is applied to
+    the fp32 accumulators), q, k, v, the attention output, the residual where
+    the MLP reads it and the SwiGLU product. Its distance from the unrounded
+    step is the rounding floor of a correct bf16 implementation."""
     w = {k: v.to(dtype) for k, v in w.items()}
     x = x.to(dtype)
     b, dm = x.shape
+    rnd = (lambda t: t.to(storage).to(dtype)) if storage is not None else (lambda t: t)
+
+    def norm(t, g):
+        return rnd(t * g) * torch.rsqrt(t.pow(2).mean(-1, keepdim=True) + eps)
+
     hd = dm // heads
     if rope is None:
         cos, sin = rope_tables(pos + 1, hd, theta, dtype)
     else:
         cos, sin = rope[0].to(dtype), rope[1].to(dtype)
     cos, sin = cos[pos], sin[pos]
-    h = rms_norm(x, w["input_norm.weight"], eps)
+    h = norm(x, w["input_norm.weight"])
     q = (h @ w["attn.q_proj.weight"].T).view(b, heads, hd)
     k = (h @ w["attn.k_proj.weight"].T).view(b, kv_heads, hd)
     v = (h @ w["attn.v_proj.weight"].T).view(b, kv_heads, hd)
-    q = q * cos + rotate_half(q) * sin
-    k = k * cos + rotate_half(k) * sin
+    q = rnd(q * cos + rotate_half(q) * sin)
+    k = rnd(k * cos + rotate_half(k) * sin)
+    v = rnd(v)
     keys = torch.cat([k_cache[:, :pos].to(dtype), k[:, None]], 1).transpose(1, 2)    # [b, kvh, pos+1, hd]
     vals = torch.cat([v_cache[:, :pos].to(dtype), v[:, None]], 1).transpose(1, 2)
-    a = attention(q[:, :, None], keys, vals, False).reshape(b, heads * hd)
+    a = rnd(attention(q[:, :, None], keys, vals, False).reshape(b, heads * hd))
     x = x + a @ w["attn.o_proj.weight"].T
-    h2 = rms_norm(x, w["post_norm.weight"], eps)
+    h2 = norm(rnd(x), w["post_norm.weight"])
     gate = h2 @ w["mlp.gate_proj.weight"].T
     up = h2 @ w["mlp.up_proj.weight"].T
-    return x + (gate * torch.sigmoid(gate) * up) @ w["mlp.down_proj.weight"].T, k, v
+    return x + rnd(gate * torch.sigmoid(gate) * up) @ w["mlp.down_proj.weight"].T, k, v

@@ -223,6 +223,36 @@ def test_fp8_gemm_validation(lib):
     assert lib.th_gemm_workspace_bytes(64, 4096, 4096, 1, abi.TH_F8E4M3) > 0
 
 
+def test_fp8_gemm_rope_outputs_share_one_accumulator(lib):
+    """e4m3 weights: fused-RoPE outputs rotating two different accumulators are refused (the
+    e4m3 epilogues gather one rotation partner); on one accumulator they pass every check."""
+    from torch_helion.hip import abi
+
+    d = _gemm_desc(in_dtype=abi.TH_F8E4M3, rhs_scale=16384, workspace=20480, workspace_bytes=1 << 30, n_acc=2, n_out=2,
+                   rope_cos=24576, rope_sin=28672, rope_head_dim=32, rope_period=1)
+    for o, a in ((0, 0), (1, 1)):
+        d.out[o].op, d.out[o].a, d.out[o].b, d.out[o].e = abi.EPI_ROPE, a, -1, -1
+        d.out[o].ptr, d.out[o].ld, d.out[o].dtype = 12288 + 4096 * o, 64, abi.TH_BF16
+    assert lib.th_gemm(C.byref(d), None) == abi.TH_ERR_INVALID
+    assert "different accumulators" in abi.last_error(lib), abi.last_error(lib)
+    d.out[1].a = 0
+    assert lib.th_gemm(C.byref(d), None) == abi.TH_ERR_NOT_INIT, abi.last_error(lib)
+
+
+def test_lhs_gain_only_for_fp8(lib):
+    """The activation-side gain is an e4m3-weight feature: a bf16 descriptor carrying one is
+    unsupported, an e4m3 one passes the checks; the gain must be 16-byte aligned."""
+    from torch_helion.hip import abi
+
+    d = _gemm_desc(lhs_gain=32768)
+    assert lib.th_gemm(C.byref(d), None) == abi.TH_ERR_UNSUPPORTED
+    assert "lhs_gain" in abi.last_error(lib)
+    d = _gemm_desc(in_dtype=abi.TH_F8E4M3, rhs_scale=16384, workspace=20480, workspace_bytes=1 << 30, lhs_gain=32772)
+    assert lib.th_gemm(C.byref(d), None) == abi.TH_ERR_INVALID
+    d.lhs_gain = 32768
+    assert lib.th_gemm(C.byref(d), None) == abi.TH_ERR_NOT_INIT, abi.last_error(lib)
+
+
 def test_embedding_validation(lib):
     """Token ids are int64 or int32; strides cover the row; an empty batch is a no-op."""
     from torch_helion.hip import abi

@@ -289,6 +289,53 @@ def test_gemm_fp8_weights(gpu, M, N, K, case):
         assert _maxabs(o16[i], ref) < BF16_TOL, (case, i)
 
 
+@pytest.mark.parametrize("M,N,K,n_acc", [(64, 6144, 4096, 1), (64, 14336, 4096, 2), (17, 1024, 8192, 1),
+                                         (100, 512, 512, 1), (64, 2048, 992, 2)])
+def test_gemm_fp8_lhs_gain(gpu, M, N, K, n_acc):
+    """e4m3 weights with the RMSNorm gain on the activation side (lhs_gain): outputs are
+    r * ((x * g) @ (q s)) with r from the UNSCALED rows, against fp32 math. Covers the
+    shared-activation kernel with several splits (q|k|v), one split finishing in the kernel
+    (gate/up), a K over the gain staging's 4096 (forced extra splits), the 128-row variant and the
+    per-wave split-K kernel (K = 992). A gain applied twice, or a sum of squares of the scaled
+    rows, would miss by far more than the tolerance (g ranges over 0.5..1.5)."""
+    from torch_helion.hip import abi, ops
+
+    announce(f"gemm fp8 lhs_gain M={M} N={N} K={K} n_acc={n_acc}")
+    g = torch.Generator().manual_seed(M * 7 + K)
+    x = torch.randn(M, K, generator=g).bfloat16()
+    gain = torch.rand(K, generator=g) + 0.5
+    qs = [_quant_e4m3(torch.randn(K, N, generator=g) * 0.02) for _ in range(n_acc)]
+    xf = x.float()
+    r = ((xf * xf).sum(-1, keepdim=True) / K + 1e-5).pow(-0.5)
+    xg = (xf * gain).bfloat16().float()                  # the staged operand is bf16(x * g)
+    accs = [(xg @ (q.float() * s[None, :])) * r for q, s in qs]
+    ref = accs[0] * torch.sigmoid(accs[0]) * accs[1] if n_acc == 2 else accs[0]
+    op = abi.EPI_SWIGLU if n_acc == 2 else abi.EPI_ACC
+    packed = ops.pack_rhs([q.to(gpu) for q, _ in qs], torch.float8_e4m3fn)
+    scale = torch.stack([s for _, s in qs]).to(gpu).contiguous()
+    ws = torch.empty(ops.gemm_workspace_bytes(M, N, K, n_acc, torch.float8_e4m3fn), dtype=torch.uint8, device=gpu)
+    o32 = torch.full((M, N), float("nan"), device=gpu)
+    ss = torch.empty(M, device=gpu)
+    ops.gemm(ops.GemmCall(M, N, K, n_acc, x.to(gpu), packed, [ops.EpiSpec(op, o32, a=0, b=1 if n_acc == 2 else -1)],
+                          in_dtype=torch.float8_e4m3fn, rhs_scale=scale, workspace=ws, sumsq=True,
+                          rscale_mask=(1 << n_acc) - 1, inv_k=1.0 / K, eps=1e-5, lhs_gain=gain.to(gpu), sumsq_out=ss))
+    torch.cuda.synchronize()
+    assert _rel(o32, ref) < 1e-4, _rel(o32, ref)
+    assert _rel(ss, (xf * xf).sum(-1)) < 1e-5
+
+
+def test_gemm_lhs_gain_rejected_for_bf16(gpu):
+    """lhs_gain exists for e4m3 weights only: a bf16 GEMM asked for it fails loudly."""
+    from torch_helion.hip import abi, ops
+
+    x = torch.randn(64, 256, device=gpu).bfloat16()
+    packed = ops.pack_rhs([torch.randn(256, 128, device=gpu).bfloat16()], torch.bfloat16)
+    out = torch.empty(64, 128, device=gpu)
+    with pytest.raises(abi.HipBackendError, match="lhs_gain"):
+        ops.gemm(ops.GemmCall(64, 128, 256, 1, x, packed, [ops.EpiSpec(abi.EPI_ACC, out, a=0)],
+                              lhs_gain=torch.ones(256, device=gpu)))
+
+
 @pytest.mark.parametrize("M,N,K", [(64, 2048, 1024), (32, 24576, 256)])
 def test_gemm_fp8_column_windows(gpu, M, N, K):
     """e4m3 weights, one accumulator split into column-window outputs (the merged q | k | v
@@ -444,10 +491,11 @@ def test_attention_f32(gpu):
 @pytest.mark.parametrize("B,Hq,Hkv,hd,max_len,lens,n_split", [
     (3, 8, 2, 128, 1000, [1000, 517, 1], 0), (3, 8, 2, 128, 1000, [1000, 517, 1], 5),
     (2, 4, 4, 64, 300, [300, 33], 1), (2, 16, 1, 64, 777, [777, 640], 0),
-    (64, 32, 8, 128, 4097, None, 0),
+    (64, 32, 8, 128, 4097, None, 0), (2, 8, 2, 128, 300, [1000, -3], 0),
 ])
 def test_attention_decode(gpu, B, Hq, Hkv, hd, max_len, lens, n_split):
-    """KV-cache decode attention vs the oracle attention (pinned against SDPA) per sequence."""
+    """KV-cache decode attention vs the oracle attention (pinned against SDPA) per sequence.
+    Lengths outside 1..max_len are clamped to it (the last case), so no read leaves the cache."""
     from oracle.llama import attention
     from torch_helion.hip import ops
 
@@ -460,7 +508,7 @@ def test_attention_decode(gpu, B, Hq, Hkv, hd, max_len, lens, n_split):
     lengths = lens if lens is not None else [max_len] * B
     refs = []
     for b in range(B):
-        L = lengths[b]
+        L = min(max(lengths[b], 1), max_len)
         qb = q[b].float().reshape(1, Hq, 1, hd)
         kb = kc[b, :L].float().permute(1, 0, 2).unsqueeze(0)
         vb = vc[b, :L].float().permute(1, 0, 2).unsqueeze(0)

@@ -25,6 +25,13 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
+// Wait until this wave's LDS accesses have completed (ds_write results are
+// visible to the other waves once they pass the next barrier).
+__device__ __forceinline__ void wait_lgkmcnt0() {
+  // vmcnt and expcnt at their maxima (no wait), lgkmcnt 0
+  __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4));
+}
+
 // Workgroup barrier that leaves global loads in flight (__syncthreads, and
 // even an LDS-only workgroup fence once direct-to-LDS loads are pending,
 // drain all of them). The wavefront-scope fences only keep the compiler from

@@ -37,6 +37,7 @@ struct DecK {
   int64_t ldo;
   const int32_t* lengths;
   int fixed_len;
+  int max_len;  // per-sequence lengths are clamped to 1..max_len (the cache slab)
   int B, Hq, Hkv, G, nsplit;
   float scale_log2;
   float* part;  // [B][Hq][nsplit][D + 2]: m, l, o[D] (o unnormalised)
@@ -90,7 +91,7 @@ __global__ void __launch_bounds__(256, 2) attn_decode_kernel(DecK p) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int qc = lane & 15, g = lane >> 4;  // query column, lane group
   const int G = p.G;
-  const int len = p.lengths ? p.lengths[b] : p.fixed_len;
+  const int len = p.lengths ? min(max(p.lengths[b], 1), p.max_len) : p.fixed_len;
   const int per = (len + p.nsplit - 1) / p.nsplit;
   const int s0 = split * per, s1 = min(len, s0 + per);
 
@@ -370,7 +371,7 @@ extern "C" int th_attention_decode(const th_decode_desc* d, void* stream) {
   k.k = (const uint16_t*)d->k_cache; k.ksb = d->k_stride_b; k.kst = d->k_stride_t;
   k.v = (const uint16_t*)d->v_cache; k.vsb = d->v_stride_b; k.vst = d->v_stride_t;
   k.o = (uint16_t*)d->o; k.ldo = d->ld_o;
-  k.lengths = d->lengths; k.fixed_len = d->fixed_len;
+  k.lengths = d->lengths; k.fixed_len = d->fixed_len; k.max_len = d->max_len;
   k.B = d->batch; k.Hq = d->heads_q; k.Hkv = d->heads_kv; k.G = d->heads_q / d->heads_kv; k.nsplit = ns;
   k.scale_log2 = d->scale * 1.4426950408889634f;
   k.part = d->workspace;

@@ -8,19 +8,31 @@
 //          holds rows (n*n_acc + i)*bn + j = column n*bn + j of operand i. A
 //          block therefore computes every accumulator of its output columns with
 //          one plain "A * B^T" main loop.
-//   bf16:  block tile BM x BNC x 64, 4 waves in a 2x2 grid, each wave a
-//          (BM/2) x (BNC/2) sub-tile of v_mfma_f32_32x32x16_bf16 ops; LDS double
-//          buffered with an XOR swizzle on 16-byte chunks (conflict-free
-//          ds_read_b128 of MFMA operands); global loads for tile k+1 are issued
-//          before the MFMAs of tile k. The RMS sum of squares of lhs rows is
-//          accumulated from the staged registers, so it costs no extra traffic.
+//   bf16:  v_mfma_f32_32x32x16_bf16 with fp32 accumulation, 64-wide K tiles,
+//          three main loops chosen per shape by th_gemm:
+//          * persistent (gemm_bf16_pk_kernel, large grids): one block per CU
+//            walks output tiles in an XCD-aware order; 256-row tiles run eight
+//            waves (two per SIMD), 128-row tiles four; each wave owns its rows
+//            x half of every accumulator's columns (or, with ASPLIT, one whole
+//            accumulator), so SwiGLU pairs and whole RoPE heads meet inside the
+//            wave. Operand tiles go HBM -> LDS by direct loads
+//            (global_load_lds_dwordx4) three stages deep, into an XOR-swizzled
+//            layout (conflict-free ds_read_b128 of MFMA operands); the epilogue
+//            of tile t overlaps the first loads of tile t+1;
+//          * direct (gemm_bf16_dl_kernel, small grids): one block per output
+//            tile, 64/128/256-row tiles, the same direct loads in a 2-4 stage
+//            ring;
+//          * staged (gemm_bf16_kernel): register-staged loads, for K not a
+//            multiple of 64 or strides the 32-bit direct-load offsets cannot
+//            reach.
+//          The RMS sum of squares of lhs rows comes from the A fragments the
+//          MFMAs already read, so it costs no extra traffic.
 //   fp32:  64 x BNC x 16 tiles of v_mfma_f32_32x32x2f32.
 //   Epilogue: accumulators are staged as fp32 through LDS one half-tile at a
 //          time; every output op then reads its operands (its own column, the
 //          RoPE partner column, other accumulators) from LDS and writes 4
 //          consecutive columns per thread, so global stores are coalesced.
 #include <algorithm>
-#include <cstdlib>
 #include <type_traits>
 
 #include "common.h"
@@ -1182,27 +1194,6 @@ static bool gemm_in_ok(int d) { return d == TH_BF16 || d == TH_F32 || d == TH_F8
 
 static bool aligned(const void* p, int bytes) { return ((uintptr_t)p % bytes) == 0; }
 
-// TH_GEMM_MAINLOOP=0|1|2 caps the bf16 main loop at register-staged (0),
-// direct-to-LDS (1) or persistent (2, the default); a shape still takes a
-// simpler loop when the faster one does not apply to it.
-static int forced_main_loop() {
-  static const int v = [] {
-    const char* e = getenv("TH_GEMM_MAINLOOP");
-    return (e && e[0] >= '0' && e[0] <= '2') ? e[0] - '0' : -1;
-  }();
-  return v;
-}
-
-// TH_GEMM_WAVES=4 keeps the 256-row persistent tiles on four waves per block
-// (one per SIMD); the default is eight.
-static int persistent_waves() {
-  static const int v = [] {
-    const char* e = getenv("TH_GEMM_WAVES");
-    return (e && e[0] == '4') ? 4 : 8;
-  }();
-  return v;
-}
-
 }  // namespace th
 
 using namespace th;
@@ -1290,39 +1281,23 @@ static void launch_bf16_pk(const GemmK& k, hipStream_t s) {
   const int tiles = k.tiles_m * k.tiles_n;
   const int cus = device_cus();
   const int grid = cus > 0 && tiles > cus ? cus : tiles;
-  const int nw = BM == 256 ? persistent_waves() : 4;
   auto go = [&](auto nacc) {
     constexpr int NA = decltype(nacc)::value;
     if constexpr (BNC % NA == 0 && (BNC / NA / 2) % 32 == 0) {
-      constexpr int NW8 = BM == 256 ? 8 : 4;  // eight waves only for 256-row tiles
+      constexpr int NW = BM == 256 ? 8 : 4;  // eight waves (two per SIMD) only for 256-row tiles
       if constexpr (NA == 2) {
         if (k.asplit) {
-          if (nw == 8) {
-            if (k.sumsq)
-              hipLaunchKernelGGL((gemm_bf16_pk_kernel<BM, BNC, true, NW8, 2, true>), dim3(grid), dim3(64 * NW8), 0, s, k);
-            else
-              hipLaunchKernelGGL((gemm_bf16_pk_kernel<BM, BNC, false, NW8, 2, true>), dim3(grid), dim3(64 * NW8), 0, s,
-                                 k);
-          } else {
-            if (k.sumsq)
-              hipLaunchKernelGGL((gemm_bf16_pk_kernel<BM, BNC, true, 4, 2, true>), dim3(grid), dim3(256), 0, s, k);
-            else
-              hipLaunchKernelGGL((gemm_bf16_pk_kernel<BM, BNC, false, 4, 2, true>), dim3(grid), dim3(256), 0, s, k);
-          }
+          if (k.sumsq)
+            hipLaunchKernelGGL((gemm_bf16_pk_kernel<BM, BNC, true, NW, 2, true>), dim3(grid), dim3(64 * NW), 0, s, k);
+          else
+            hipLaunchKernelGGL((gemm_bf16_pk_kernel<BM, BNC, false, NW, 2, true>), dim3(grid), dim3(64 * NW), 0, s, k);
           return;
         }
       }
-      if (nw == 8) {
-        if (k.sumsq)
-          hipLaunchKernelGGL((gemm_bf16_pk_kernel<BM, BNC, true, NW8, NA>), dim3(grid), dim3(64 * NW8), 0, s, k);
-        else
-          hipLaunchKernelGGL((gemm_bf16_pk_kernel<BM, BNC, false, NW8, NA>), dim3(grid), dim3(64 * NW8), 0, s, k);
-      } else {
-        if (k.sumsq)
-          hipLaunchKernelGGL((gemm_bf16_pk_kernel<BM, BNC, true, 4, NA>), dim3(grid), dim3(256), 0, s, k);
-        else
-          hipLaunchKernelGGL((gemm_bf16_pk_kernel<BM, BNC, false, 4, NA>), dim3(grid), dim3(256), 0, s, k);
-      }
+      if (k.sumsq)
+        hipLaunchKernelGGL((gemm_bf16_pk_kernel<BM, BNC, true, NW, NA>), dim3(grid), dim3(64 * NW), 0, s, k);
+      else
+        hipLaunchKernelGGL((gemm_bf16_pk_kernel<BM, BNC, false, NW, NA>), dim3(grid), dim3(64 * NW), 0, s, k);
     } else {
       launch_bf16_dl<BM, BNC>(k, s);  // no per-wave split of this column tile (the host selects none such)
     }
@@ -1375,6 +1350,11 @@ extern "C" int th_gemm(const th_gemm_desc* d, void* stream) {
   TH_CHECK_ARG(d->n_out >= 1 && d->n_out <= TH_MAX_OUT, "th_gemm: n_out=%d out of range", d->n_out);
   TH_CHECK_ARG(d->n_extra >= 0 && d->n_extra <= TH_MAX_EXTRA, "th_gemm: n_extra=%d out of range", d->n_extra);
   TH_CHECK_ARG(d->rscale_mask == 0 || d->sumsq, "th_gemm: rscale_mask set without sumsq");
+  if (d->lhs_gain != nullptr && !fp8) {
+    set_error("th_gemm: lhs_gain is implemented for TH_F8E4M3 weights only");
+    return TH_ERR_UNSUPPORTED;
+  }
+  TH_CHECK_ARG(d->lhs_gain == nullptr || aligned(d->lhs_gain, 16), "th_gemm: lhs_gain must be 16-byte aligned");
   const int bn = choose_bn(d->N, d->n_acc, d->in_dtype);
   GemmK k{};
   k.A = d->lhs;
@@ -1441,6 +1421,18 @@ extern "C" int th_gemm(const th_gemm_desc* d, void* stream) {
     }
   }
   k.n_out = d->n_out;
+  if (fp8) {
+    // the e4m3 epilogues gather one rotation partner per column group: every
+    // fused-RoPE output must rotate the same accumulator
+    int rope_acc = -1;
+    for (int o = 0; o < d->n_out; ++o) {
+      if (d->out[o].op != TH_EPI_ROPE) continue;
+      TH_CHECK_ARG(rope_acc < 0 || rope_acc == d->out[o].a,
+                   "th_gemm: fp8 weights: TH_EPI_ROPE outputs on different accumulators (%d, %d)", rope_acc,
+                   d->out[o].a);
+      rope_acc = d->out[o].a;
+    }
+  }
   if (need_rope) {
     TH_CHECK_ARG(d->rope_cos && d->rope_sin, "th_gemm: RoPE output without cos/sin tables");
     TH_CHECK_ARG(d->rope_head_dim >= 4 && d->rope_head_dim % 8 == 0 && d->N % d->rope_head_dim == 0,
@@ -1453,6 +1445,7 @@ extern "C" int th_gemm(const th_gemm_desc* d, void* stream) {
   k.hd = d->rope_head_dim > 0 ? d->rope_head_dim : 1;
   k.period = d->rope_period > 0 ? d->rope_period : 1;
   k.sumsq_out = d->sumsq_out;
+  k.gain = d->lhs_gain;
   if (!device_ready()) {
     set_error("th_gemm: th_init was not called for the current device");
     return TH_ERR_NOT_INIT;
@@ -1501,9 +1494,7 @@ extern "C" int th_gemm(const th_gemm_desc* d, void* stream) {
       wave_epi &= split;
     }
     MainLoop ml = MainLoop::staged;
-    const int force = forced_main_loop();
     if (direct) ml = wave_epi ? MainLoop::persistent : MainLoop::direct;
-    if (force >= 0 && force < (int)ml) ml = (MainLoop)force;
     if (bm == 64 && ml == MainLoop::persistent) ml = MainLoop::direct;  // 64-row tiles: direct loop only
     if (bm == 64 && ml == MainLoop::staged) {  // the staged loop has no 64-row tile
       k.tiles_m = (int)cdiv(d->M, 128);

@@ -31,7 +31,6 @@
 //                           (and, from the first column block, partial row sums
 //                           of squares);
 //   gemm_fp8_reduce_kernel  one thread per output element, same sums and ops.
-#include <cstdlib>
 #include <type_traits>
 
 #include "common.h"
@@ -40,6 +39,11 @@
 namespace th {
 
 typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
+typedef __attribute__((ext_vector_type(4))) uint32_t u32x4_t;
+
+// K capacity of the activation-gain staging of gemm_fp8_lds_kernel (fp32
+// values in LDS); the launch splits K so no split covers more.
+constexpr int FP8_GAIN_K = 4096;
 
 __device__ __forceinline__ bf16x8_t fp8x8_to_bf16x8(uint32_t lo, uint32_t hi) {
   union {
@@ -111,6 +115,27 @@ __global__ void __launch_bounds__(256) gemm_fp8_splitk_kernel(Fp8K p) {
         }
       }
     }
+    if (p.k.gain) {
+      // activation-side RMSNorm gain: the sum of squares is taken first, from
+      // the unscaled row, then the operands become bf16(x * g)
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int64_t k = kc + 32 * u;
+        if (k >= ke) continue;
+        const float4* gp = (const float4*)(p.k.gain + k + 16 * h);
+        const float4 g4[4] = {gp[0], gp[1], gp[2], gp[3]};
+        const float* g = (const float*)g4;
+#pragma unroll
+        for (int t = 0; t < TM; ++t)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float x0 = (float)af[u][t][0][e], x1 = (float)af[u][t][1][e];
+            if (do_ss) ss[t] += x0 * x0 + x1 * x1;
+            af[u][t][0][e] = (__bf16)(x0 * g[e]);
+            af[u][t][1][e] = (__bf16)(x1 * g[8 + e]);
+          }
+      }
+    }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
 #pragma unroll
@@ -122,7 +147,7 @@ __global__ void __launch_bounds__(256) gemm_fp8_splitk_kernel(Fp8K p) {
           acc[t][g] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[u][t][1], b1, acc[t][g], 0, 0, 0);
         }
       }
-      if (do_ss) {
+      if (do_ss && !p.k.gain) {
 #pragma unroll
         for (int t = 0; t < TM; ++t)
 #pragma unroll
@@ -362,7 +387,12 @@ __device__ __forceinline__ void fp8_tile_out(const Fp8K& p, int t, int tid, cons
 // chunk c in slot c ^ (r % 16), so the 32-row operand reads (one chunk per
 // lane) hit distinct banks; the permutation is applied on the load side and
 // the direct loads write 1 KiB (1024 / (2 KS) rows) linearly per instruction.
-template <int TM, int NG, int KS>  // 32-row tiles of M (M <= 32 TM); 32-column groups per wave; K per slice
+// With GAIN (an activation-side RMSNorm gain, p.k.gain): the workgroup's
+// gains (at most FP8_GAIN_K of them) are staged in LDS behind the slices;
+// once a wave's own direct loads of a slice have landed, each lane rescales
+// the 16-byte chunks it loaded (x -> bf16(x * g[k])) and adds their unscaled
+// squares to its rows' sums, before the barrier that publishes the slice.
+template <int TM, int NG, int KS, bool GAIN>  // 32-row tiles of M (M <= 32 TM); 32-column groups per wave; K per slice
 __global__ void __launch_bounds__(256, 2) gemm_fp8_lds_kernel(Fp8K p) {
   constexpr int ROWS = 32 * TM;
   constexpr int RB = 2 * KS;           // bytes per activation row of a slice
@@ -375,7 +405,15 @@ __global__ void __launch_bounds__(256, 2) gemm_fp8_lds_kernel(Fp8K p) {
   constexpr int WLD = NCH * NG;        // weight loads per wave per slice
   constexpr int PARTS = 256 / ROWS;    // threads per row in the sum of squares
   constexpr int CPP = LPR / PARTS;     // 16-byte chunks per such thread and slice
-  __shared__ __attribute__((aligned(16))) char sa[NBUF * SLB];
+  constexpr int GK = GAIN ? FP8_GAIN_K : 0;  // staged gains (fp32) behind the slice buffers
+  static_assert(!GAIN || (LPR == 16 && GK >= ROWS), "gain staging assumes 16 chunks per row");
+  __shared__ __attribute__((aligned(16))) char sa[NBUF * SLB + 4 * GK];
+  float* const gl = (float*)(sa + NBUF * SLB);
+  // LDS byte addresses for the gain path's accesses, which are written as
+  // inline ds_read / ds_write with their own lgkmcnt waits: the compiler
+  // cannot tell which slice bytes the in-flight direct loads write and would
+  // otherwise wait for all of them before every such access.
+  const uint32_t sa_lds = (uint32_t)(uintptr_t)(lds_ptr_t)sa;
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -410,6 +448,21 @@ __global__ void __launch_bounds__(256, 2) gemm_fp8_lds_kernel(Fp8K p) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[t][g][r] = 0.f;
   float ss = 0.f;
+  float ssq[GAIN ? ALD : 1];  // GAIN: unscaled squares of the rows this lane loads
+#pragma unroll
+  for (int q = 0; q < (GAIN ? ALD : 1); ++q) ssq[q] = 0.f;
+  // GAIN: this workgroup's gains, read into registers before the first
+  // slices are issued (their loads are the oldest, so the first step's wait
+  // covers them), written to LDS before the first barrier
+  f32x4_t greg[GAIN ? GK / 1024 : 1];
+  const int nk = nsl * KS;
+  if constexpr (GAIN) {
+#pragma unroll
+    for (int i = 0; i < GK / 1024; ++i) {
+      const int64_t at = min((int64_t)(1024 * i + 4 * tid), (int64_t)nk - 4);  // in bounds, kept only below nk
+      greg[i] = *(const f32x4_t*)(p.k.gain + kb + at);
+    }
+  }
 
   // slice j goes to LDS buffer j % NBUF and weight slot j % NBUF
   // workgroups start their K walk at different slices (rotated), so the
@@ -451,7 +504,7 @@ __global__ void __launch_bounds__(256, 2) gemm_fp8_lds_kernel(Fp8K p) {
         }
       }
     }
-    if (do_ss) {
+    if (do_ss && !GAIN) {
       const int row = tid / PARTS, part = tid % PARTS;
       const char* ar = sa + SL * SLB + row * RB;
 #pragma unroll
@@ -465,6 +518,45 @@ __global__ void __launch_bounds__(256, 2) gemm_fp8_lds_kernel(Fp8K p) {
       }
     }
   };
+  // GAIN: the chunks this lane loaded into slice buffer SL (rows RPI (ALD wave
+  // + q) + lane / LPR, source chunk (lane % LPR) ^ (row % 16)), rescaled in
+  // place; their unscaled squares go to ssq (rows past M are re-reads: dropped).
+  auto scale_own = [&](int j0, auto slot) {
+    constexpr int SL = decltype(slot)::value;
+    const int j = j0 + rot < nsl ? j0 + rot : j0 + rot - nsl;
+    const uint32_t ad = sa_lds + SL * SLB + ALD * wave * 1024 + lane * 16;
+#pragma unroll
+    for (int q = 0; q < ALD; ++q) {
+      const int r = RPI * (ALD * wave + q) + lane / LPR;
+      const int c = (lane % LPR) ^ (r & 15);
+      const uint32_t ga_at = sa_lds + NBUF * SLB + 4 * (j * KS + 8 * c);
+      u32x4_t v;
+      f32x4_t ga, gb;
+      asm volatile(
+          "ds_read_b128 %0, %3\n\t"
+          "ds_read_b128 %1, %4\n\t"
+          "ds_read_b128 %2, %4 offset:16\n\t"
+          "s_waitcnt lgkmcnt(0)"
+          : "=v"(v), "=v"(ga), "=v"(gb)
+          : "v"(ad + q * 1024), "v"(ga_at)
+          : "memory");
+      const float g[8] = {ga[0], ga[1], ga[2], ga[3], gb[0], gb[1], gb[2], gb[3]};
+      uint32_t w[4] = {v[0], v[1], v[2], v[3]};
+      float sq = 0.f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float lo = __uint_as_float(w[e] << 16), hi = __uint_as_float(w[e] & 0xffff0000u);
+        sq += lo * lo + hi * hi;
+        const bf16x2_t pr = {(__bf16)(lo * g[2 * e]), (__bf16)(hi * g[2 * e + 1])};  // round to nearest even
+        w[e] = __builtin_bit_cast(uint32_t, pr);
+      }
+      if (r < p.M) ssq[q] += sq;
+      const u32x4_t o = {w[0], w[1], w[2], w[3]};
+      asm volatile("ds_write_b128 %0, %1" : : "v"(ad + q * 1024), "v"(o) : "memory");
+    }
+    // the rescaled chunks are written before the barrier publishes them
+    asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory");
+  };
   // Every step issues one slice (past the end: the last slice again, an L2
   // re-read into a buffer nobody reads), so the in-flight count is the same
   // at every wait and the compiler needs no waits of its own.
@@ -473,6 +565,7 @@ __global__ void __launch_bounds__(256, 2) gemm_fp8_lds_kernel(Fp8K p) {
     // slice j has landed (only slice j + 1 may still be in flight) and every
     // wave is done with slice j - 1, whose buffer slice j + 2 reuses
     wait_vmcnt<ALD + WLD>();
+    if constexpr (GAIN) scale_own(j, slot);
     barrier_keep_loads();
     issue(min(j + 2, nsl - 1), std::integral_constant<int, (SL + 2) % NBUF>());
     compute(slot);
@@ -480,6 +573,18 @@ __global__ void __launch_bounds__(256, 2) gemm_fp8_lds_kernel(Fp8K p) {
 
   issue(0, std::integral_constant<int, 0>());
   issue(min(1, nsl - 1), std::integral_constant<int, 1>());
+  if constexpr (GAIN) {
+    // the gain loads were issued before both slices: waiting for all but the
+    // slices' loads waits for them alone
+    wait_vmcnt<2 * (ALD + WLD)>();
+#pragma unroll
+    for (int i = 0; i < GK / 1024; ++i)
+      if (1024 * i + 4 * tid < nk)
+        asm volatile("ds_write_b128 %0, %1" : : "v"(sa_lds + NBUF * SLB + 4 * (1024 * i + 4 * tid)), "v"(greg[i])
+                     : "memory");
+    asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory");
+    barrier_keep_loads();  // every wave's gains are in LDS before any wave rescales with them
+  }
   // whole trips of NBUF steps, then at most two more: no step of a trip is
   // conditional, so the compiler sees one in-flight pattern at every wait
   int j = 0;
@@ -492,6 +597,21 @@ __global__ void __launch_bounds__(256, 2) gemm_fp8_lds_kernel(Fp8K p) {
   if (j + 1 < nsl) step(j + 1, std::integral_constant<int, 1>());
   wait_vmcnt<0>();  // no direct-to-LDS load may land after the workgroup ends
 
+  if constexpr (GAIN) {
+    // every wave is past the last barrier, so nobody reads the staged gains
+    // any more: their space collects the row sums, handed to thread PARTS row
+    if (do_ss) {
+#pragma unroll
+      for (int q = 0; q < ALD; ++q) {
+        float v = ssq[q];
+#pragma unroll
+        for (int o = 1; o < LPR; o <<= 1) v += __shfl_xor(v, o);
+        if (lane % LPR == 0) gl[RPI * (ALD * wave + q) + lane / LPR] = v;
+      }
+    }
+    __syncthreads();
+    ss = (do_ss && tid % PARTS == 0) ? gl[tid / PARTS] : 0.f;
+  }
   if (do_ss) {
 #pragma unroll
     for (int o = 1; o < PARTS; o <<= 1) ss += __shfl_xor(ss, o);
@@ -616,30 +736,24 @@ __global__ void __launch_bounds__(256) gemm_fp8_reduce4_kernel(Fp8K p) {
 // Split count: about one workgroup per CU, each wave at least 256 of K.
 static int fp8_groups(int64_t Npk) { return Npk % 64 == 0 ? 2 : 1; }
 
-static int fp8_env(const char* name) {
-  const char* e = getenv(name);
-  return e ? atoi(e) : 0;
-}
-
 // The shared-activation kernel: one workgroup per packed tile of 128 columns
 // (bn = 128 / n_acc), K in whole 128-wide slices. Split count: about one
 // workgroup per CU, a single split once the tiles alone nearly fill the GPU
 // (that launch finishes its tiles itself, without the reduce kernel).
-// TH_FP8_SPLITS overrides the count.
 static bool fp8_lds_ok(int64_t Npk, int64_t K, int bn, int n_acc) {
   return K % 128 == 0 && (n_acc == 1 || n_acc == 2) && bn * n_acc == 128 && Npk % 128 == 0;
 }
 
 static int fp8_lds_splits(int64_t Npk, int64_t K) {
-  static const int forced = fp8_env("TH_FP8_SPLITS");
   const int64_t nsl = K / 128;
-  if (forced > 0) return (int)std::min((int64_t)forced, nsl);
+  // a split covers at most FP8_GAIN_K of K (the gain staging's capacity)
+  const int64_t smin = cdiv(K, FP8_GAIN_K);
   const int64_t cus = device_cus() > 0 ? device_cus() : 256;
   const int64_t nb = Npk / 128;
-  if (4 * nb >= 3 * cus) return 1;
+  if (4 * nb >= 3 * cus) return (int)smin;
   // as many splits as keep the launch within one round of one workgroup per CU
   const int64_t s = std::min(std::max((int64_t)1, cus / nb), std::min(nsl, (int64_t)16));
-  return (int)std::max((int64_t)1, s);
+  return (int)std::max(smin, s);
 }
 
 static int fp8_splits(int64_t Npk, int64_t K) {
@@ -694,12 +808,21 @@ int launch_gemm_fp8(const GemmK& k, int64_t Npk, const float* scale, float* ws, 
     const dim3 g1((unsigned)(Npk / 128), (unsigned)p.splits);
     // (128-wide slices measured as fast as or faster than 256-wide ones at the
     // Llama-3-8B decode shapes, so only they are instantiated)
-    if (k.M <= 32)
-      hipLaunchKernelGGL((gemm_fp8_lds_kernel<1, 1, 128>), g1, dim3(256), 0, stream, p);
-    else if (k.M <= 64)
-      hipLaunchKernelGGL((gemm_fp8_lds_kernel<2, 1, 128>), g1, dim3(256), 0, stream, p);
-    else
-      hipLaunchKernelGGL((gemm_fp8_lds_kernel<4, 1, 128>), g1, dim3(256), 0, stream, p);
+    if (k.gain) {
+      if (k.M <= 32)
+        hipLaunchKernelGGL((gemm_fp8_lds_kernel<1, 1, 128, true>), g1, dim3(256), 0, stream, p);
+      else if (k.M <= 64)
+        hipLaunchKernelGGL((gemm_fp8_lds_kernel<2, 1, 128, true>), g1, dim3(256), 0, stream, p);
+      else
+        hipLaunchKernelGGL((gemm_fp8_lds_kernel<4, 1, 128, true>), g1, dim3(256), 0, stream, p);
+    } else {
+      if (k.M <= 32)
+        hipLaunchKernelGGL((gemm_fp8_lds_kernel<1, 1, 128, false>), g1, dim3(256), 0, stream, p);
+      else if (k.M <= 64)
+        hipLaunchKernelGGL((gemm_fp8_lds_kernel<2, 1, 128, false>), g1, dim3(256), 0, stream, p);
+      else
+        hipLaunchKernelGGL((gemm_fp8_lds_kernel<4, 1, 128, false>), g1, dim3(256), 0, stream, p);
+    }
     TH_CHECK_LAUNCH();
     if (!p.fused) {
       if (vec)

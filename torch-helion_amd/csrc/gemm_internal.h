@@ -37,6 +37,7 @@ struct GemmK {
   int asplit;  // persistent kernel: each wave's column half is one whole accumulator (n_acc == 2)
   EpiOutK out[TH_MAX_OUT];
   float* sumsq_out;
+  const float* gain;  // optional [K]: products use lhs[m, k] * gain[k] (fp8 path); sumsq stays unscaled
 };
 
 // fp8-weight path (gemm_fp8.hip)

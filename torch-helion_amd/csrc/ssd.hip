@@ -17,7 +17,6 @@
 // (already centred, reference optimizer/passes.py:501-525); only differences of
 // it are used here, so its centring offset cancels.
 #include <algorithm>
-#include <cstdlib>
 
 #include "common.h"
 
@@ -839,15 +838,6 @@ int ssd_init_device() {
   return TH_OK;
 }
 
-// TH_SSD_VALU=1 keeps the fp32 VALU kernels for bf16 inputs too.
-static bool ssd_force_valu() {
-  static const bool v = [] {
-    const char* e = getenv("TH_SSD_VALU");
-    return e && e[0] == '1';
-  }();
-  return v;
-}
-
 }  // namespace th
 
 using namespace th;
@@ -912,7 +902,7 @@ extern "C" int th_ssd_chunked(const th_ssd_desc* d, void* stream) {
   const bool mfma = d->dtype == TH_BF16 && (k.P == 32 || k.P == 64 || k.P == 128) &&
                     (k.N == 32 || k.N == 64 || k.N == 128) && k.Q % 32 == 0 && d->ld_x % 8 == 0 &&
                     d->ld_b % 8 == 0 && d->ld_c % 8 == 0 && al16(d->x) && al16(d->b) && al16(d->c) &&
-                    out2_lds(k.Q, k.P) <= kMaxLds && !ssd_force_valu();
+                    out2_lds(k.Q, k.P) <= kMaxLds;
   if (mfma) {
     const int64_t bhc = (int64_t)k.B * k.H * k.nc;
     uint4* hf = (uint4*)(d->workspace + bhc * k.P * k.N + ssd_tot_floats(bhc));

@@ -13,7 +13,7 @@ from pathlib import Path
 
 from .build import LIB_PATH
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 # th_status
 TH_OK = 0
@@ -61,6 +61,7 @@ class GemmDesc(C.Structure):
         ("out", EpiOut * MAX_OUT),
         ("sumsq_out", _p),
         ("rhs_scale", _p), ("workspace", _p), ("workspace_bytes", _i64),
+        ("lhs_gain", _p),
     ]
 
 

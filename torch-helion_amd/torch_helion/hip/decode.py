@@ -6,19 +6,23 @@ cache and its OpGraph no fp8 type); this runner is the decode configuration of
 the BASELINE (Llama-3-8B-shaped block, batch 64, cache 4096) built from the same
 kernel library. A step is five library calls:
 
-  k0  th_gemm e4m3   [q | k | v] = (x r) [Wq' | Wk' | Wv'],  r = RMS row scale,
-                     W' = diag(g1) W; three column-window outputs: q = rope_pos(.),
-                     k = rope_pos(.) and v written straight into the caches at
-                     position ``pos`` (the output row stride is the cache's
-                     sequence stride)
+  k0  th_gemm e4m3   [q | k | v] = r (x g1) [Wq | Wk | Wv],  r = RMS row scale of x;
+                     three column-window outputs: q = rope_pos(.), k = rope_pos(.)
+                     and v written straight into the caches at position ``pos``
+                     (the output row stride is the cache's sequence stride)
   k1  th_attention_decode over keys 0..pos
   k2  th_gemm e4m3   x1 = x + attn Wo
-  k3  th_gemm e4m3   act = silu((x1 r2) Wg') * ((x1 r2) Wu'),  Wg' = diag(g2) Wg
+  k3  th_gemm e4m3   act = silu(r2 (x1 g2) Wg) * (r2 (x1 g2) Wu)
   k4  th_gemm e4m3   out = x1 + act Wd
 
-The norm gains are folded into the weights before quantisation (the same fold
-the prefill pipeline makes, reference optimizer/param_transforms.py:18-20), so
-the step computes exactly the block with weights ``effective_weights()``.
+Every weight is the model's own ``W`` quantised per output channel,
+``q = e4m3(W / s_n)`` with ``s_n = max_k |W[k, n]| / 448``. The RMSNorm gains
+stay on the activation side (``lhs_gain``: the GEMM multiplies x by g as it
+stages it, after taking the row's sum of squares), so the step computes the
+block whose weights are the dequantised ``q s_n`` and whose norm gains are the
+model's: ``effective_weights()``. (Folding the gain into the weights before
+quantising, as the prefill pipeline folds it into bf16 weights, would quantise
+a different matrix.)
 """
 
 from __future__ import annotations
@@ -67,17 +71,12 @@ class DecodeBlock:
         self.B, self.max_len = batch, max_len
         sd = {k: v.detach().float().cpu() for k, v in state_dict.items()}
         g1, g2 = sd["input_norm.weight"], sd["post_norm.weight"]
+        self._eff: dict[str, torch.Tensor] = {"input_norm.weight": g1.clone(), "post_norm.weight": g2.clone()}
 
-        def folded(name: str, gain: torch.Tensor | None) -> torch.Tensor:
-            w = sd[name].T.contiguous()                     # nn.Linear [out, in] -> [K, N]
-            return w * gain[:, None] if gain is not None else w
-
-        self._eff: dict[str, torch.Tensor] = {}
-
-        def proj(names: list[str], gain: torch.Tensor | None, concat: bool = False) -> _Proj:
+        def proj(names: list[str], concat: bool = False) -> _Proj:
             """One accumulator per weight, or (concat) one accumulator over the weights'
             columns side by side; per-output-channel scales either way."""
-            qs = [quantize_e4m3(folded(n, gain)) for n in names]
+            qs = [quantize_e4m3(sd[n].T.contiguous()) for n in names]   # nn.Linear [out, in] -> [K, N]
             for n, (q, s) in zip(names, qs):
                 self._eff[n] = (q.float() * s[None, :]).T.contiguous()   # [out, in], what the step multiplies by
             if concat:
@@ -87,12 +86,14 @@ class DecodeBlock:
             scale = torch.stack([s for _, s in qs]).to(self.device).contiguous()
             return _Proj(packed, scale, n_, k_, len(qs))
 
-        self.wqkv = proj(["attn.q_proj.weight", "attn.k_proj.weight", "attn.v_proj.weight"], g1, concat=True)
-        self.wo = proj(["attn.o_proj.weight"], None)
-        self.wgu = proj(["mlp.gate_proj.weight", "mlp.up_proj.weight"], g2)
-        self.wd = proj(["mlp.down_proj.weight"], None)
+        self.wqkv = proj(["attn.q_proj.weight", "attn.k_proj.weight", "attn.v_proj.weight"], concat=True)
+        self.wo = proj(["attn.o_proj.weight"])
+        self.wgu = proj(["mlp.gate_proj.weight", "mlp.up_proj.weight"])
+        self.wd = proj(["mlp.down_proj.weight"])
 
         dev, B = self.device, batch
+        self.g1 = g1.to(dev).contiguous()
+        self.g2 = g2.to(dev).contiguous()
         bf = torch.bfloat16
         self.k_cache = torch.zeros(B, max_len, kv_heads, self.hd, dtype=bf, device=dev)
         self.v_cache = torch.zeros_like(self.k_cache)
@@ -116,12 +117,9 @@ class DecodeBlock:
 
     # ------------------------------------------------------------------
     def effective_weights(self) -> dict[str, torch.Tensor]:
-        """The weights the step multiplies by, as an fp32 state dict with unit norm
-        gains (the gains live inside the folded, dequantised projections)."""
-        w = dict(self._eff)
-        w["input_norm.weight"] = torch.ones(self.D)
-        w["post_norm.weight"] = torch.ones(self.D)
-        return w
+        """The weights the step multiplies by, as an fp32 state dict: the dequantised
+        projections ``q s_n`` and the model's norm gains."""
+        return dict(self._eff)
 
     def _gemm(self, p: _Proj, lhs: torch.Tensor, outs: list[ops.EpiSpec], **kw) -> None:
         ops.gemm(ops.GemmCall(lhs.shape[0], p.n, p.k, p.n_acc, lhs, p.packed, outs, in_dtype=_FP8,
@@ -146,12 +144,13 @@ class DecodeBlock:
         self._gemm(self.wqkv, x, [ops.EpiSpec(E.EPI_ROPE, self.q, a=0, cols=(0, qw)),
                                   ops.EpiSpec(E.EPI_ROPE, kslot, a=0, cols=(qw, qw + kvw)),
                                   ops.EpiSpec(E.EPI_ACC, vslot, a=0, cols=(qw + kvw, qw + 2 * kvw))],
-                   rscale_mask=0b1, **norm, **rope)
+                   rscale_mask=0b1, lhs_gain=self.g1, **norm, **rope)
         ops.attention_decode(self.q, self.k_cache, self.v_cache, self.attn, scale=1.0 / math.sqrt(self.hd),
                              fixed_len=pos + 1, workspace=self.attn_ws)
         self._gemm(self.wo, self.attn, [ops.EpiSpec(E.EPI_ADD, self.x1, e=0), ops.EpiSpec(E.EPI_ADD, self.x1_32, e=0)],
                    extras=[x])
-        self._gemm(self.wgu, self.x1, [ops.EpiSpec(E.EPI_SWIGLU, self.act, a=0, b=1)], rscale_mask=0b11, **norm)
+        self._gemm(self.wgu, self.x1, [ops.EpiSpec(E.EPI_SWIGLU, self.act, a=0, b=1)], rscale_mask=0b11,
+                   lhs_gain=self.g2, **norm)
         self._gemm(self.wd, self.act, [ops.EpiSpec(E.EPI_ADD, self.out, e=0), ops.EpiSpec(E.EPI_ADD, self.out32, e=0)],
                    extras=[self.x1_32])
         return self.out

@@ -105,6 +105,7 @@ class GemmCall:
     in_dtype: torch.dtype | None = None        # torch.float8_e4m3fn: bf16 lhs x e4m3 packed rhs
     rhs_scale: torch.Tensor | None = None      # fp8: [n_acc, N] fp32 per-column scales
     workspace: torch.Tensor | None = None      # fp8: gemm_workspace_bytes(...) bytes
+    lhs_gain: torch.Tensor | None = None       # fp8: [K] fp32, products use lhs * gain (RMSNorm gain)
 
     def descriptor(self) -> abi.GemmDesc:
         d = abi.GemmDesc()
@@ -143,6 +144,10 @@ class GemmCall:
                 e.col_begin, e.col_end = o.cols
         if self.sumsq_out is not None:
             d.sumsq_out = self.sumsq_out.data_ptr()
+        if self.lhs_gain is not None:
+            if self.lhs_gain.dtype != torch.float32 or not self.lhs_gain.is_contiguous() or self.lhs_gain.numel() != self.K:
+                raise abi.HipBackendError("th_gemm", abi.TH_ERR_INVALID, "lhs_gain must be contiguous fp32 [K]")
+            d.lhs_gain = self.lhs_gain.data_ptr()
         return d
 
 
