@@ -156,6 +156,19 @@ int64_t th_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t n_acc, 
 /* One OpIR gemm KernelSpec. */
 int th_gemm(const th_gemm_desc* desc, void* stream);
 
+/* th_gemm that allocates nothing and takes no workspace. No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops such as the decode step, harnesses
+ * that forbid hipMalloc). With TH_F8E4M3 weights the split-K partial sums live
+ * in a file-scope device array of TH_GEMM_NOALLOC_SCRATCH_BYTES per GPU (held
+ * until the process ends); desc->workspace is ignored, and sizes that need
+ * more (th_gemm_workspace_bytes) are refused with TH_ERR_INVALID. Every call on
+ * one GPU shares that array and nothing in it needs to start at zero, so calls
+ * that overlap on one GPU (on concurrent streams) race; calls in stream order
+ * do not. bf16 / fp32 weights need no scratch: the call is th_gemm. */
+#define TH_GEMM_NOALLOC_SCRATCH_BYTES (32 << 20)
+int th_gemm_noalloc(const th_gemm_desc* desc, void* stream);
+
 /* ------------------------------------------------------------ RMSNorm
  * The stand-alone normalisation kernel (gemm kind with gemms=[] and sumsq;
  * reference: optimizer/partition.py:165-177, optimizer/passes.py:357-370):

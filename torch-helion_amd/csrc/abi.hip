@@ -56,7 +56,9 @@ extern "C" int th_init(int device) {
                   prop.gcnArchName);
     return TH_ERR_UNSUPPORTED;
   }
-  const int st = th::ssd_init_device();
+  int st = th::ssd_init_device();
+  if (st != TH_OK) return st;
+  st = th::fp8_scratch_init_device(device);
   if (st != TH_OK) return st;
   th::g_cus[device] = prop.multiProcessorCount;
   th::g_ready[device] = true;

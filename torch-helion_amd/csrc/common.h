@@ -80,6 +80,7 @@ void set_error(const char* fmt, ...);
 bool device_ready();  // th_init was called for the current device
 int device_cus();     // compute units of the current device (0 before th_init)
 int ssd_init_device();  // per-device set-up of the scan kernels (called by th_init)
+int fp8_scratch_init_device(int device);  // per-device address of th_gemm_noalloc's scratch (th_init)
 
 #define TH_CHECK_ARG(cond, ...)            \
   do {                                     \

@@ -852,4 +852,43 @@ int launch_gemm_fp8(const GemmK& k, int64_t Npk, const float* scale, float* ws, 
   return TH_OK;
 }
 
+// ------------------------------------------------------------ no-alloc entry
+// Scratch memory of th_gemm_noalloc: the e4m3 path's split-K partial sums (and
+// partial row sums of squares) in a file-scope device array, one copy per GPU,
+// held until the process ends. Host code never passes the array's name to a
+// kernel or a copy (that is a host-side stand-in, not a device address): each
+// device's address comes from hipGetSymbolAddress at th_init.
+static __device__ __align__(256) float scratch[TH_GEMM_NOALLOC_SCRATCH_BYTES / 4];
+static void* g_scratch[64];
+
+int fp8_scratch_init_device(int device) {
+  void* ptr = nullptr;
+  TH_CHECK_HIP(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+  g_scratch[device] = ptr;
+  return TH_OK;
+}
+
 }  // namespace th
+
+using namespace th;
+
+extern "C" int th_gemm_noalloc(const th_gemm_desc* d, void* stream) {
+  TH_CHECK_ARG(d != nullptr, "th_gemm_noalloc: null descriptor");
+  // bf16 / fp32 weights use no scratch memory: the call is th_gemm itself
+  if (d->in_dtype != TH_F8E4M3) return th_gemm(d, stream);
+  const int64_t need = th_gemm_workspace_bytes(d->M, d->N, d->K, d->n_acc, d->in_dtype);
+  TH_CHECK_ARG(need <= (int64_t)TH_GEMM_NOALLOC_SCRATCH_BYTES,
+               "th_gemm_noalloc: M=%lld N=%lld K=%lld n_acc=%d need %lld bytes of scratch, above the fixed %lld "
+               "(use th_gemm with a workspace)",
+               (long long)d->M, (long long)d->N, (long long)d->K, d->n_acc, (long long)need,
+               (long long)TH_GEMM_NOALLOC_SCRATCH_BYTES);
+  int dev = -1;
+  if (!device_ready() || hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64 || g_scratch[dev] == nullptr) {
+    set_error("th_gemm_noalloc: th_init was not called for the current device");
+    return TH_ERR_NOT_INIT;
+  }
+  th_gemm_desc c = *d;
+  c.workspace = (float*)g_scratch[dev];
+  c.workspace_bytes = TH_GEMM_NOALLOC_SCRATCH_BYTES;
+  return th_gemm(&c, stream);
+}

@@ -29,6 +29,7 @@ TH_F32, TH_BF16, TH_F16, TH_F8E4M3, TH_I32, TH_I64 = range(6)
 EPI_ACC, EPI_ROPE, EPI_ROPE_PAIR, EPI_SILU, EPI_SWIGLU, EPI_ADD, EPI_SOFTPLUS_ADD, EPI_MUL = range(8)
 
 MAX_ACC, MAX_OUT, MAX_EXTRA = 4, 6, 4
+GEMM_NOALLOC_SCRATCH_BYTES = 32 << 20
 VM_MAX_IN, VM_MAX_OPS, VM_MAX_OUT = 16, 96, 8
 
 # th_vm_code
@@ -154,6 +155,7 @@ SIGNATURES: dict[str, tuple] = {
     "th_gemm_pack_rhs": (_i32, [C.POINTER(_p), C.POINTER(_i64), _i32, _i64, _i64, _i32, _i32, _p, _p]),
     "th_gemm_workspace_bytes": (_i64, [_i64, _i64, _i64, _i32, _i32]),
     "th_gemm": (_i32, [C.POINTER(GemmDesc), _p]),
+    "th_gemm_noalloc": (_i32, [C.POINTER(GemmDesc), _p]),
     "th_rmsnorm": (_i32, [C.POINTER(RmsNormDesc), _p]),
     "th_attention_prefill": (_i32, [C.POINTER(AttnDesc), _p]),
     "th_attention_decode_workspace_bytes": (_i64, [_i32, _i32, _i32, _i32, _i32, _i32]),

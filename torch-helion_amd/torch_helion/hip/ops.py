@@ -164,6 +164,14 @@ def gemm(call: GemmCall, kernel: str | None = None) -> None:
     abi.check(lib.th_gemm(C.byref(d), _stream(call.lhs)), "th_gemm", kernel)
 
 
+def gemm_noalloc(call: GemmCall, kernel: str | None = None) -> None:
+    """th_gemm_noalloc: the same GEMM with the library's fixed per-GPU scratch in place of a
+    workspace (``call.workspace`` is ignored); allocates nothing."""
+    lib = _lib(call.lhs)
+    d = call.descriptor()
+    abi.check(lib.th_gemm_noalloc(C.byref(d), _stream(call.lhs)), "th_gemm_noalloc", kernel)
+
+
 # --------------------------------------------------------------- RMSNorm
 def rmsnorm(x: torch.Tensor, gain: torch.Tensor, eps: float, out: torch.Tensor, inv_k: float | None = None,
             kernel: str | None = None, out32: torch.Tensor | None = None) -> torch.Tensor:
