@@ -102,6 +102,10 @@ class OpGraph:
         self.outputs: list[str] = []
         self.params: dict[str, torch.Tensor] = {}
         self.metadata: dict[str, Any] = {}
+        # const name -> (gain [K], weight [K, N]) for weights made by folding an
+        # RMSNorm gain into a GEMM operand: the unfolded factors, so a backend
+        # can apply the gain to the activations instead (not serialised)
+        self.fold_sources: dict[str, tuple[torch.Tensor, torch.Tensor]] = {}
         self._counter = 0
 
     # ------------------------------------------------------------ building
@@ -258,5 +262,6 @@ class OpGraph:
         g = OpGraph.from_dict(self.to_dict())
         g.metadata = dict(self.metadata)
         g.params = dict(self.params)
+        g.fold_sources = dict(self.fold_sources)
         g._counter = self._counter
         return g

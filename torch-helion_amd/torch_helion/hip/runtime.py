@@ -46,8 +46,15 @@ class DeviceProgram:
 
     def __init__(self, program: Program, params: dict[str, torch.Tensor], device: int | torch.device = 0,
                  fuse_rope: bool = True, fp32_outputs: bool = True, residual_fp32: bool = True,
-                 merge_siblings: bool = False) -> None:
+                 merge_siblings: bool = False,
+                 fold_sources: dict[str, tuple[torch.Tensor, torch.Tensor]] | None = None) -> None:
         self.program = program
+        # RMSNorm gains folded into weights by the front end, to be taken back
+        # out (weight const -> (gain, unfolded weight)): such GEMMs read the
+        # activations normalised WITH the gain by th_rmsnorm and the model's own
+        # weights, so the gain never meets the weights in bf16
+        self.fold_sources = fold_sources or {}
+        self._normed: dict[tuple, torch.Tensor] = {}
         self.device = torch.device("cuda", device) if isinstance(device, int) else torch.device(device)
         if self.device.type != "cuda":
             raise abi.HipBackendError("DeviceProgram", abi.TH_ERR_INVALID, f"device {device} is not a HIP device")
@@ -233,10 +240,17 @@ class DeviceProgram:
         return Launch(spec.name, "attention", run, "th_attention_prefill", kw)
 
     # gemm -----------------------------------------------------------------
-    def _pack(self, spec: KernelSpec, rhs_args: list[str], in_dtype: torch.dtype) -> Callable[[], torch.Tensor]:
+    def _pack(self, spec: KernelSpec, rhs_args: list[str], in_dtype: torch.dtype,
+              unfold: bool = False) -> Callable[[], torch.Tensor]:
         """Packed rhs for these weight arguments: packed once if all are params,
-        else re-packed into a workspace at every run."""
+        else re-packed into a workspace at every run. ``unfold``: the weights the
+        front end folded a norm gain into, taken without the gain."""
         tens = [spec.arg(r).tensor for r in rhs_args]
+        if unfold:
+            srcs = [self.fold_sources[t][1].to(self.device) for t in tens]
+            packed = ops.pack_rhs([x if x.dtype in (torch.float32, torch.bfloat16) else x.float() for x in srcs],
+                                  in_dtype)
+            return lambda: packed
         srcs = [self.buffers[t] for t in tens]
         if all(t in self.program.params for t in tens):
             srcs = [s if s.dtype in (torch.float32, torch.bfloat16) else s.float() for s in srcs]
@@ -366,7 +380,12 @@ class DeviceProgram:
                 extras.append(o.extra)
         if len(extras) > abi.MAX_EXTRA:
             return None
-        get_packed = self._pack(spec, [rhs_of[i] for i in used], in_dtype)
+        norm_launch, normed = None, None
+        gain = self._unfold_gain(spec, plan, used)
+        if gain is not None:
+            norm_launch, normed = self._normed_lhs(spec, lhs_t, gain, plan.rscale)
+            lhs = normed
+        get_packed = self._pack(spec, [rhs_of[i] for i in used], in_dtype, unfold=gain is not None)
         extra_bufs = [self.operand(spec.arg(x).tensor) for x in extras]
         epi = []
         for o, op, a, b, key in outs:
@@ -381,19 +400,58 @@ class DeviceProgram:
             if plan.scaled.get(i, False):
                 mask |= 1 << slot[i]
         inv_k, eps = plan.rscale if plan.rscale else (0.0, 0.0)
+        sumsq = plan.rscale is not None
+        if normed is not None:   # the row scale is inside the normalised lhs
+            mask, sumsq = 0, False
         rope = next(iter(rope_tables.values())) if rope_tables else None
         info = {"n_acc": len(used), "ops": [op for _, op, *_ in outs], "rscale": plan.rscale is not None,
-                "rope_fused": any(op == abi.EPI_ROPE for _, op, *_ in outs)}
+                "rope_fused": any(op == abi.EPI_ROPE for _, op, *_ in outs), "gain_on_activation": normed is not None}
 
         def run() -> None:
-            call = ops.GemmCall(T, N, K, len(used), lhs, get_packed(), epi, sumsq=plan.rscale is not None,
+            call = ops.GemmCall(T, N, K, len(used), lhs, get_packed(), epi, sumsq=sumsq,
                                 rscale_mask=mask, inv_k=inv_k, eps=eps, extras=extra_bufs)
             if rope is not None:
                 call.rope_cos, call.rope_sin, call.rope_period, call.rope_head_dim = rope[0], rope[1], rope[2], rope[3]
             ops.gemm(call, kernel=spec.name)
 
         self.plans[spec.name] = info
-        return [Launch(spec.name, "gemm", run, "th_gemm", info)]
+        launches = [Launch(spec.name, "gemm", run, "th_gemm", info)]
+        return [norm_launch] + launches if norm_launch is not None else launches
+
+    def _unfold_gain(self, spec: KernelSpec, plan: EpiloguePlan, used: list[int]) -> torch.Tensor | None:
+        """The norm gain to take back out of this kernel's weights: every used weight is
+        a fold of the same gain, every used accumulator carries the row scale, and the
+        lhs is bf16. None otherwise (the kernel then runs as folded)."""
+        if not self.fold_sources or plan.rscale is None or not used:
+            return None
+        if self.buffers[spec.arg("lhs").tensor].dtype != torch.bfloat16:
+            return None
+        tens = [spec.arg(spec.gemms[i].rhs).tensor for i in used]
+        if any(t not in self.fold_sources for t in tens) or not all(plan.scaled.get(i, False) for i in used):
+            return None
+        g0 = self.fold_sources[tens[0]][0]
+        if any(not torch.equal(self.fold_sources[t][0], g0) for t in tens[1:]):
+            return None
+        return g0
+
+    def _normed_lhs(self, spec: KernelSpec, lhs_t: str, gain: torch.Tensor, rscale) -> tuple[Launch | None, torch.Tensor]:
+        """bf16 ``x * r * g`` of this lhs (x read from its fp32 shadow when it has one),
+        made by one th_rmsnorm launch before the first kernel that needs it and shared
+        by the later ones (sibling projections of the same normalised input)."""
+        inv_k, eps = rscale
+        key = (lhs_t, gain.data_ptr(), float(inv_k), float(eps))
+        if key in self._normed:
+            return None, self._normed[key]
+        x = self.operand(lhs_t)
+        out = torch.empty(x.shape, dtype=torch.bfloat16, device=self.device)
+        gvec = gain.float().reshape(-1).to(self.device).contiguous()
+        self._normed[key] = out
+
+        def run() -> None:
+            ops.rmsnorm(x, gvec, eps, out, inv_k=inv_k, kernel=f"{spec.name} (normalised lhs)")
+
+        # (a launch of the kernel that first needs it: its time counts with that kernel's)
+        return Launch(spec.name, "gemm", run, "th_rmsnorm", {"inv_k": inv_k, "eps": eps, "normalised_lhs": True}), out
 
     # sibling merge --------------------------------------------------------
     # GEMM kernels that multiply the same lhs by weights (projections of one

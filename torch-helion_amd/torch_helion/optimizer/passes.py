@@ -379,6 +379,7 @@ def lower_rmsnorm(g: OpGraph) -> int:
         for mm, _via in users:
             w = mm.inputs[1]
             wg = g.add_const(pt.fold_gain_into_weight(gval, g.value(w)), name=g.fresh_name(w + "_norm"))
+            g.fold_sources[wg.name] = (gval, g.value(w))
             flat = TensorType(_twod(mm.type.shape), mm.type.dtype)
             new_mm = g.add("matmul", [x2d, wg.name], flat, origin=f"lower_rmsnorm({mm.name})")
             bc = g.add("broadcast", [r], flat, {"dim": 1, "shape": list(flat.shape)})

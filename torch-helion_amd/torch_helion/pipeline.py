@@ -145,9 +145,13 @@ def compile_model(model: torch.nn.Module, example_args: Sequence[Any], config: C
         if config.backend == "hip":
             from .hip.runtime import DeviceProgram
 
+            if config.norm_gain not in ("fold", "activation"):
+                raise ValueError(f"CompileConfig.norm_gain must be 'fold' or 'activation', not {config.norm_gain!r}")
             device_program = DeviceProgram(program, graph.params, config.device, fuse_rope=config.fuse_rope,
                                            fp32_outputs=config.fp32_outputs, residual_fp32=config.residual_fp32,
-                                           merge_siblings=config.merge_siblings)
+                                           merge_siblings=config.merge_siblings,
+                                           fold_sources=graph.fold_sources if config.norm_gain == "activation"
+                                           else None)
             rw.write_json("kernels/launches.json", [{"kernel": l.kernel, "entry": l.entry, "info": l.info}
                                                     for l in device_program.launches])
 
