@@ -454,7 +454,8 @@ def _attn_ref(q, k, v, B, S, Hq, Hkv, hd, scale, causal):
 
 
 @pytest.mark.parametrize("B,S,Hq,Hkv,hd,causal", [(2, 200, 4, 2, 128, True), (1, 256, 8, 8, 64, False),
-                                                  (2, 384, 8, 2, 128, False), (1, 130, 4, 1, 64, True)])
+                                                  (2, 384, 8, 2, 128, False), (1, 130, 4, 1, 64, True),
+                                                  (8, 320, 8, 2, 128, True)])
 def test_attention_bf16(gpu, B, S, Hq, Hkv, hd, causal):
     from torch_helion.hip import ops
 

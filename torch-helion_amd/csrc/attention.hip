@@ -24,6 +24,7 @@ struct AttnK {
   uint16_t* o;
   int64_t ldq, ldk, ldv, ldo;
   int B, Sq, Skv, Hq, Hkv, group, nqb, causal, off;
+  int xcd_map;  // (B * Hkv) % 8 == 0: every (batch, kv head) served by one XCD
   float scale_log2;
 };
 
@@ -64,9 +65,27 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_bf16_kernel(AttnK p) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int hl = lane >> 5, col = lane & 31;
   const int bh_count = p.B * p.Hq;
-  const int qb = p.nqb - 1 - (int)(blockIdx.x / bh_count);
-  const int bh = (int)(blockIdx.x % bh_count);
-  const int b = bh / p.Hq, hq = bh - b * p.Hq, hk = hq / p.group;
+  // Workgroups are dealt round-robin to the 8 XCDs (workgroup i to XCD i % 8),
+  // each with its own L2. With xcd_map, XCD x owns (B Hkv / 8) whole (batch, kv
+  // head) pairs, so the q heads of a GQA group and all q blocks that read one
+  // K/V stream share one L2; within an XCD the q blocks still run longest first.
+  int qb, b, hq;
+  if (p.xcd_map) {
+    const int xcd = (int)(blockIdx.x & 7), slot = (int)(blockIdx.x >> 3);
+    const int per_qb = bh_count >> 3;  // one q block's workgroups per XCD
+    const int qi = slot / per_qb, inner = slot - qi * per_qb;
+    const int pl = inner / p.group;
+    const int pair = xcd * ((p.B * p.Hkv) >> 3) + pl;
+    b = pair / p.Hkv;
+    hq = (pair - b * p.Hkv) * p.group + (inner - pl * p.group);
+    qb = p.nqb - 1 - qi;
+  } else {
+    const int bh = (int)(blockIdx.x % bh_count);
+    qb = p.nqb - 1 - (int)(blockIdx.x / bh_count);
+    b = bh / p.Hq;
+    hq = bh - b * p.Hq;
+  }
+  const int hk = hq / p.group;
   const int q0 = qb * BQ;
   const int q0w = q0 + wave * 32;
   const int qrow = q0w + col;
@@ -359,6 +378,7 @@ extern "C" int th_attention_prefill(const th_attn_desc* d, void* stream) {
     k.nqb = (int)cdiv(d->seq_q, 128);
     k.causal = d->causal ? 1 : 0;
     k.off = d->seq_kv - d->seq_q;
+    k.xcd_map = (d->batch * d->heads_kv) % 8 == 0 ? 1 : 0;
     k.scale_log2 = d->scale * log2e;
     const dim3 grid((unsigned)(k.nqb * d->batch * d->heads_q));
     if (hd == 128)
