@@ -358,7 +358,7 @@ def bench_mamba_c4(args) -> dict:
                               "prefix), bf16 logits"})
     parity["ok"] = parity["max_rel_err"] <= parity["tolerance"] and parity["max_abs_err"] <= parity["max_abs_bar"]
     obj = {"us": us, "tokens_per_s": cfg.batch * cfg.seq / (us * 1e-6), "kernels": len(res.program.kernels),
-           "launches": len(dp.launches),
+           "launches": len(dp.launches), "intermediate_memory": dp.memory_report(),
            "mfma_frac": b["total_flops"] / (us * 1e-6) / (res.hw.peak_tflops["bfloat16"] * 1e12),
            "us_by_kind": {k: round(v, 1) for k, v in sorted(by_kind.items())},
            "lm_head": {"kernel": head_name, "us": round(head["us"], 1), "mfma_frac": round(head["frac"], 4)},

@@ -52,6 +52,7 @@ class CompileConfig:
                                                   # off: at C2/C4 the concatenated width adds a ragged tile column
                                                   # (288 blocks on 256 CUs) and costs more than the launches it saves
     cpu_flop_budget: float = 2e10                 # graphs above this skip CPU-side checks in "auto" mode
+    reuse_buffers: bool = True                    # intermediates share device buffers by liveness
     norm_gain: str = "fold"                       # "fold": RMSNorm gains folded into the GEMM weights (the
                                                   # reference's lowering); "activation": the device normalises
                                                   # the activations with the gain (th_rmsnorm, from the fp32

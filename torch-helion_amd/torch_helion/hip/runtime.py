@@ -3,7 +3,8 @@
 The device twin of the reference's interpreter loop (codegen/interpret.py:54-77):
 parameters are uploaded once (GEMM weights pre-packed into th_gemm's layout,
 RoPE tables compressed back to [S, head_dim] after checking their structure),
-every intermediate is allocated once from ``Program.tensors``, and each
+intermediates get device buffers from a liveness-based pool (a buffer is
+reused once the last kernel reading its tensor has run; memplan.py), and each
 KernelSpec becomes one or two C-ABI launches on the current stream, in
 program order. There is no host fallback: a kernel the library cannot run
 raises :class:`HipBackendError` naming it.
@@ -47,7 +48,8 @@ class DeviceProgram:
     def __init__(self, program: Program, params: dict[str, torch.Tensor], device: int | torch.device = 0,
                  fuse_rope: bool = True, fp32_outputs: bool = True, residual_fp32: bool = True,
                  merge_siblings: bool = False,
-                 fold_sources: dict[str, tuple[torch.Tensor, torch.Tensor]] | None = None) -> None:
+                 fold_sources: dict[str, tuple[torch.Tensor, torch.Tensor]] | None = None,
+                 reuse_buffers: bool = True) -> None:
         self.program = program
         # RMSNorm gains folded into weights by the front end, to be taken back
         # out (weight const -> (gain, unfolded weight)): such GEMMs read the
@@ -71,35 +73,45 @@ class DeviceProgram:
         for name in program.inputs:
             t = program.tensors[name]
             self.buffers[name] = torch.empty(t.shape, dtype=_TORCH_DT[t.dtype], device=self.device)
-        for k in program.kernels:
-            for o in k.outputs:
-                if o.tensor not in self.buffers:
-                    t = program.tensors[o.tensor]
-                    self.buffers[o.tensor] = torch.empty(t.shape, dtype=_TORCH_DT[t.dtype], device=self.device)
         # Residual operands produced inside the program get an fp32 shadow:
         # the producer also writes fp32 and every GEMM that adds it as an
         # epilogue operand reads the shadow, so the residual stream is rounded
         # to the activation dtype only where a GEMM consumes it as its LHS.
         # (The SSD's gate multiplies its output: it is read in its own dtype,
         # as the eager model does, and keeps the kernel's vector epilogue.)
-        self.shadow: dict[str, torch.Tensor] = {}
+        half = ("bfloat16", "float16")
         produced = {o.tensor for k in program.kernels for o in k.outputs}
         # a gathered table row is exact in the table's dtype: no shadow needed
         exact = {o.tensor for k in program.kernels if k.kind == "embedding" for o in k.outputs}
+        shadowed: set[str] = set()
         for k in program.kernels:
             if k.kind != "gemm" or not residual_fp32:
                 continue
             for a in k.args:
-                if (a.role == "extra" and a.tensor in produced and a.tensor not in self.shadow
-                        and a.tensor not in exact and self.buffers[a.tensor].dtype in (torch.bfloat16, torch.float16)):
-                    self.shadow[a.tensor] = torch.empty(self.buffers[a.tensor].shape, dtype=torch.float32,
-                                                        device=self.device)
+                if (a.role == "extra" and a.tensor in produced and a.tensor not in exact
+                        and program.tensors[a.tensor].dtype in half):
+                    shadowed.add(a.tensor)
         if fp32_outputs:
             # program outputs are also kept in fp32 (the epilogue computes them in
             # fp32; rounding to the declared dtype is only the storage step)
-            for o in program.outputs:
-                if o in produced and o not in self.shadow and o not in exact and self.buffers[o].dtype in (torch.bfloat16, torch.float16):
-                    self.shadow[o] = torch.empty(self.buffers[o].shape, dtype=torch.float32, device=self.device)
+            shadowed |= {o for o in program.outputs
+                         if o in produced and o not in exact and program.tensors[o].dtype in half}
+        self._shadowed = shadowed
+        self.shadow: dict[str, torch.Tensor] = {}
+        # Intermediates (and shadows, workspaces, normalised operands) come from a
+        # pool that recycles a buffer once the last kernel reading it has been
+        # bound: kernels run in program order on one stream. Program outputs keep
+        # buffers of their own. (Merged sibling launches write members' outputs
+        # ahead of their program position, so merging allocates everything.)
+        from .memplan import BufferPool, lifetimes
+
+        self.reuse = reuse_buffers and not merge_siblings
+        self._born, self._last = lifetimes(program)
+        self._pool = BufferPool(lambda n: torch.empty(n, dtype=torch.uint8, device=self.device)) if self.reuse else None
+        self._cur = 0
+        if not self.reuse:
+            for k in program.kernels:
+                self._bind_outputs(k)
         # program inputs read as token ids, with the size of the table they index
         self._vocab: dict[str, int] = {}
         for k in program.kernels:
@@ -107,13 +119,46 @@ class DeviceProgram:
                 ids = k.arg("ids").tensor
                 self._vocab[ids] = min(self._vocab.get(ids, k.attrs["vocab"]), k.attrs["vocab"])
         self._merge_groups, self._merged_away = self._plan_sibling_merges(program) if merge_siblings else ({}, set())
-        for k in program.kernels:
+        for i, k in enumerate(program.kernels):
+            self._cur = i
+            if self.reuse:
+                self._pool.release_before(i)
+                self._bind_outputs(k)
             if k.name in self._merged_away:
                 continue
             if k.name in self._merge_groups:
                 self.launches.extend(self._lower_gemm_merged(self._merge_groups[k.name]))
             else:
                 self.launches.extend(self._lower(k))
+
+    # ------------------------------------------------------------- memory
+    def _device_buffer(self, shape, dtype: torch.dtype, last: int) -> torch.Tensor:
+        """A tensor that nothing else uses through kernel ``last`` (pooled), or a fresh one."""
+        numel = 1
+        for s in shape:
+            numel *= int(s)
+        if self._pool is None or last >= len(self.program.kernels):
+            return torch.empty(tuple(shape), dtype=dtype, device=self.device)
+        nbytes = numel * torch.empty((), dtype=dtype).element_size()
+        return self._pool.alloc(nbytes, last)[:nbytes].view(dtype).view(tuple(shape))
+
+    def _bind_outputs(self, k: KernelSpec) -> None:
+        """Buffers (and fp32 shadows) for the tensors kernel ``k`` produces."""
+        for o in k.outputs:
+            name = o.tensor
+            if name in self.buffers:
+                continue
+            t = self.program.tensors[name]
+            last = self._last.get(name, self._cur)
+            self.buffers[name] = self._device_buffer(t.shape, _TORCH_DT[t.dtype], last)
+            if name in self._shadowed:
+                self.shadow[name] = self._device_buffer(t.shape, torch.float32, last)
+
+    def memory_report(self) -> dict[str, int]:
+        """Bytes of intermediate storage held, and what one buffer per tensor would hold."""
+        if self._pool is None:
+            return {"reuse": False}
+        return {"reuse": True, "pool_bytes": self._pool.block_bytes, "without_reuse_bytes": self._pool.requested_bytes}
 
     # -------------------------------------------------------------- running
     def set_inputs(self, inputs: dict[str, torch.Tensor] | list[torch.Tensor] | tuple) -> None:
@@ -191,7 +236,8 @@ class DeviceProgram:
         return self._host_params.get(name) if name in self.program.params else None
 
     def _workspace(self, numel: int, dtype=torch.float32) -> torch.Tensor:
-        w = torch.empty(numel, dtype=dtype, device=self.device)
+        """Scratch memory of the kernel being lowered (free again for the next kernel)."""
+        w = self._device_buffer((numel,), dtype, self._cur)
         self.workspaces.append(w)
         return w
 
@@ -443,7 +489,8 @@ class DeviceProgram:
         if key in self._normed:
             return None, self._normed[key]
         x = self.operand(lhs_t)
-        out = torch.empty(x.shape, dtype=torch.bfloat16, device=self.device)
+        # read only by kernels that read the lhs: the lhs's lifetime bounds it
+        out = self._device_buffer(x.shape, torch.bfloat16, self._last.get(lhs_t, self._cur))
         gvec = gain.float().reshape(-1).to(self.device).contiguous()
         self._normed[key] = out
 
@@ -599,8 +646,8 @@ class DeviceProgram:
 
 def run_program(program: Program, params: dict[str, torch.Tensor], inputs, device: int = 0) -> dict[str, torch.Tensor]:
     """Device twin of the reference's interpreter ``run_program``: every produced
-    tensor, on the device."""
-    dp = DeviceProgram(program, params, device)
+    tensor, on the device (each in a buffer of its own)."""
+    dp = DeviceProgram(program, params, device, reuse_buffers=False)
     dp.run(inputs)
     return dict(dp.buffers)
 
