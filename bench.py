@@ -40,7 +40,13 @@ sys.path.insert(0, str(REPO / "torch-helion_amd"))
 sys.path.insert(0, str(REPO))
 
 METRIC = "µs per block fwd (Llama-8B block, Mamba-2 layer); % of MFMA/HBM roofline"
-RESULTS = REPO / "gpurun_out" / "results"
+RESULTS = REPO / "gpurun_out" / "results"   # compile_model results dirs (--results-dir)
+
+
+def write_device_results(*a):
+    from torch_helion.pipeline import write_device_results as w
+
+    w(*a)
 
 # HBM bytes per launch of the C3 gate/up kernel (k4_gemm), from rocprofv3 --pmc passes:
 # FETCH_SIZE 2,825,776 KiB x 2.0 (the counter reads half of a calibrated 1 GiB copy's
@@ -129,6 +135,7 @@ def bench_llama_c3(args) -> dict:
     log(f"compiled in {time.time() - t0:.1f} s: {len(res.program.kernels)} kernels")
     dp = res.device_program
     b = bench_program(dp, x, res.hw, warmup=args.warmup, reps=args.steps)
+    write_device_results(res.run_dir, res.program, res.hw, b)
     us = b["us_median"]
     out_gpu = dp.outputs(fp32=False)[0][:1].float().cpu()
     torch.cuda.synchronize()
@@ -180,6 +187,7 @@ def bench_llama_c1(args) -> dict:
     res = compile_model(model, x, CompileConfig(run_name="bench_llama_c1", results_dir=RESULTS, backend="hip",
                                                 device_check=False, reference_check=True, planner_mode="exhaustive"))
     b = bench_program(res.device_program, x, res.hw, warmup=args.warmup, reps=args.steps)
+    write_device_results(res.run_dir, res.program, res.hw, b)
     us = b["us_median"]
     out = res.device_program.outputs()[0].float().cpu()
     w = {k: v.detach().double() for k, v in model.state_dict().items() if not k.startswith(("rope", "attn_bias"))}
@@ -214,6 +222,7 @@ def bench_mamba_c2(args) -> dict:
                                                 device_check=False, reference_check=False, verify_passes=False,
                                                 planner_mode="exhaustive", fp32_outputs=False, residual_fp32=False))
     b = bench_program(res.device_program, x, res.hw, warmup=args.warmup, reps=args.steps)
+    write_device_results(res.run_dir, res.program, res.hw, b)
     us = b["us_median"]
     out = res.device_program.outputs()[0].float().cpu()
     w = {k: v.detach().double() for k, v in model.state_dict().items()}
@@ -326,6 +335,7 @@ def bench_mamba_c4(args) -> dict:
     log(f"compiled in {time.time() - t0:.1f} s: {len(res.program.kernels)} kernels")
     dp = res.device_program
     b = bench_program(dp, (ids,), res.hw, warmup=min(args.warmup, 3), reps=min(args.steps, 10))
+    write_device_results(res.run_dir, res.program, res.hw, b)
     us = b["us_median"]
     by_kind: dict[str, float] = {}
     for v in b["kernels"].values():
@@ -390,14 +400,19 @@ def main() -> int:
     ap.add_argument("--no-mamba", action="store_true", help="skip the Mamba-2 layer (config 1) line")
     ap.add_argument("--no-decode", action="store_true", help="skip the fp8 decode-step (config 4) line")
     ap.add_argument("--no-backbone", action="store_true", help="skip the Mamba-2 backbone (config 3) line")
-    ap.add_argument("--only", choices=["c1", "c2", "c4", "c5"], default=None,
+    ap.add_argument("--only", choices=["c1", "c2", "c3", "c4", "c5"], default=None,
                     help="run one secondary workload alone and print its object (for profiling runs)")
+    ap.add_argument("--results-dir", type=Path, default=None, help="where compile_model writes results/<run>/")
     args = ap.parse_args()
+    if args.results_dir is not None:
+        global RESULTS
+        RESULTS = args.results_dir
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU; --gpus must be 1 (multi-GPU sharding is not built)"}))
         return 2
     if args.only:
-        fn = {"c1": bench_llama_c1, "c2": bench_mamba_c2, "c4": bench_mamba_c4, "c5": bench_decode_c5}[args.only]
+        fn = {"c1": bench_llama_c1, "c2": bench_mamba_c2, "c3": bench_llama_c3, "c4": bench_mamba_c4,
+              "c5": bench_decode_c5}[args.only]
         print(json.dumps({"workload": args.only, **fn(args)}), flush=True)
         return 0
     line = bench_llama_c3(args)

@@ -49,12 +49,39 @@ def launch_plan(spec: KernelSpec, program: Program) -> dict[str, Any]:
     return plan
 
 
+def readme(program: Program, plans: dict[str, dict[str, Any]]) -> str:
+    """kernels/README.md: what each launch plan is and how to run it (the reference's
+    kernels/README.md explains how to run each generated kernel through Loom)."""
+    lines = [f"# Kernels of `{program.name}`", "",
+             "Each `<kernel>.json` is the HIP launch plan of one OpIR KernelSpec: the C-ABI entry point of",
+             "`libth_hip.so` (declared in `include/th_hip.h`), the tile, every argument with its tensor, role,",
+             "shape and dtype, and for GEMMs the fused epilogue (catalogue ops, or the epilogue-VM fallback).",
+             "", "Run a plan on the GPU through the runtime, which binds device buffers and packs weights:", "",
+             "```python", "from torch_helion import CompileConfig, compile_model",
+             "res = compile_model(model, example_inputs, CompileConfig(backend=\"hip\"))",
+             "res.device_program.run(list(example_inputs))      # every kernel, in program order",
+             "[l for l in res.device_program.launches if l.kernel == \"k0_gemm\"]  # one kernel's C-ABI launches",
+             "```", "",
+             "A plan can also be driven from C with the descriptors of `include/th_hip.h` (one `th_*` call per",
+             "plan; the caller owns every buffer).", "",
+             "| kernel | kind | entry point | tiles | inputs -> outputs |", "|---|---|---|---|---|"]
+    for spec in program.kernels:
+        p = plans[spec.name]
+        ins = ", ".join(f"{a['role']}={a['tensor']}" for a in p["args"])
+        lines.append(f"| `{spec.name}` | {spec.kind} | `{p['entry']}` | {p['tiles']} | {ins} -> "
+                     f"{', '.join(p['outputs'])} |")
+    return "\n".join(lines) + "\n"
+
+
 def emit_program(program: Program, config, out_dir: Path) -> dict[str, Path]:
     out_dir = Path(out_dir)
     out_dir.mkdir(parents=True, exist_ok=True)
     files: dict[str, Path] = {}
+    plans: dict[str, dict[str, Any]] = {}
     for spec in program.kernels:
         p = out_dir / f"{spec.name}.json"
-        p.write_text(json.dumps(launch_plan(spec, program), indent=2, default=str))
+        plans[spec.name] = launch_plan(spec, program)
+        p.write_text(json.dumps(plans[spec.name], indent=2, default=str))
         files[spec.name] = p
+    (out_dir / "README.md").write_text(readme(program, plans))
     return files

@@ -30,6 +30,12 @@ class HardwareSpec:
     launch_overhead_us: float = 4.0
     raw: dict[str, Any] = field(default_factory=dict)
 
+    @property
+    def calibration(self) -> dict[str, Any]:
+        """Per-category efficiencies and launch overhead fitted to measured kernel times
+        (cost_models/calibrate.py); empty when the spec carries none."""
+        return self.raw.get("calibration", {})
+
     @staticmethod
     def load(path: str | Path | None = None) -> "HardwareSpec":
         p = Path(path) if path else DEFAULT_HW_SPEC
@@ -63,4 +69,5 @@ class HardwareSpec:
         return {"path": str(self.path), "name": self.name, "compute_units": self.compute_units, "xcds": self.xcds,
                 "clock_ghz": self.clock_ghz, "lds_bytes_per_cu": self.lds_bytes,
                 "hbm_bandwidth_gbs": self.hbm_bandwidth_gbs, "peak_tflops": self.peak_tflops,
-                "efficiency": self.efficiency, "launch_overhead_us": self.launch_overhead_us}
+                "efficiency": self.efficiency, "launch_overhead_us": self.launch_overhead_us,
+                "calibration": self.calibration}

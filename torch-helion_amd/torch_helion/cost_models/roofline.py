@@ -76,16 +76,39 @@ def gemm_tiles(N: int, n_acc: int, M: int, dtype: str) -> tuple[int, int]:
     return (256 if big else 128), bn
 
 
+def category(spec: KernelSpec, tensors: dict[str, TensorType]) -> str:
+    """Calibration category of a kernel: kernels of one category share an efficiency."""
+    dtype = _dtype(spec, tensors)
+    if spec.kind == "gemm":
+        if not spec.gemms:
+            return "norm"
+        return "gemm_fp32" if dtype == "float32" else "gemm_bf16"
+    if spec.kind == "attention":
+        return "attention_fp32" if dtype == "float32" else "attention"
+    if spec.kind in ("ssd", "ssd_chunked"):
+        return "ssd"
+    return spec.kind
+
+
 def _compose(hw: HardwareSpec, flops: float, nbytes: float, mfma_flops: float, blocks: int, dtype: str,
-             tiles: dict[str, int], detail: dict[str, Any]) -> CostBreakdown:
-    eff_m = hw.efficiency.get("mfma", 0.6)
-    eff_h = hw.efficiency.get("hbm", 0.7)
+             tiles: dict[str, int], detail: dict[str, Any], cat: str) -> CostBreakdown:
+    """Time of the binding roofline. With a calibration fitted for ``cat``: ideal time at
+    100% of peak over the fitted efficiency plus the fitted launch overhead; without one,
+    the hardware spec's generic MFMA / HBM efficiencies and overhead."""
+    calib = hw.calibration
+    fitted = calib.get("efficiency", {}).get(cat)
+    eff_m = fitted if fitted else hw.efficiency.get("mfma", 0.6)
+    eff_h = fitted if fitted else hw.efficiency.get("hbm", 0.7)
+    overhead = calib.get("launch_overhead_us", hw.launch_overhead_us) if fitted else hw.launch_overhead_us
     waves = max(1, math.ceil(blocks / hw.compute_units)) if blocks else 1
     per_block = mfma_flops / max(blocks, 1)
     t_mfma = waves * per_block / (hw.peak_flops(dtype) / hw.compute_units * eff_m) * 1e6 if mfma_flops else 0.0
     t_hbm = nbytes / (hw.hbm_bytes_per_s() * eff_h) * 1e6
-    us = max(t_mfma, t_hbm) + hw.launch_overhead_us
+    us = max(t_mfma, t_hbm) + overhead
+    if fitted:
+        us += waves * calib.get("tile_us", {}).get(cat, 0.0)
     bound = "mfma" if t_mfma >= t_hbm else "hbm"
+    detail = {**detail, "category": cat, "calibrated": bool(fitted)}
     return CostBreakdown(us, flops, nbytes, bound, tiles, blocks, waves, t_mfma, t_hbm, detail)
 
 
@@ -99,7 +122,7 @@ def gemm_cost(spec: KernelSpec, tensors: dict[str, TensorType], hw: HardwareSpec
     extras = [a for a in spec.args if a.role == "extra"]
     nbytes = T * K * eb + n_acc * K * N * eb + sum(_bytes(tensors[a.tensor]) for a in extras) + len(spec.outputs) * T * N * eb
     if n_acc == 0:  # stand-alone normalisation: HBM bound
-        return _compose(hw, 3.0 * T * K, nbytes, 0.0, 0, dtype, {"tile_t": 4}, {"n_acc": 0})
+        return _compose(hw, 3.0 * T * K, nbytes, 0.0, 0, dtype, {"tile_t": 4}, {"n_acc": 0}, "norm")
     flops = 2.0 * T * N * K * n_acc
     bm, bn = gemm_tiles(N, n_acc, T, dtype)
     tiles_m, tiles_n = math.ceil(T / bm), math.ceil(N / bn)
@@ -107,7 +130,8 @@ def gemm_cost(spec: KernelSpec, tensors: dict[str, TensorType], hw: HardwareSpec
     mfma = 2.0 * tiles_m * bm * tiles_n * bn * n_acc * kq
     return _compose(hw, flops, nbytes, mfma, tiles_m * tiles_n, dtype,
                     {"tile_t": bm, "tile_n": bn, "tile_k": 16 if dtype == "float32" else 64},
-                    {"n_acc": n_acc, "sumsq": spec.sumsq, "extras": len(extras), "outputs": len(spec.outputs)})
+                    {"n_acc": n_acc, "sumsq": spec.sumsq, "extras": len(extras), "outputs": len(spec.outputs)},
+                    "gemm_fp32" if dtype == "float32" else "gemm_bf16")
 
 
 def attention_cost(spec: KernelSpec, tensors: dict[str, TensorType], hw: HardwareSpec) -> CostBreakdown:
@@ -126,7 +150,8 @@ def attention_cost(spec: KernelSpec, tensors: dict[str, TensorType], hw: Hardwar
     blocks = b * h * qb
     kv_tiles = sum(math.ceil(min(skv, (i + 1) * 128 + skv - s) / 64) for i in range(qb)) if a.get("causal") else qb * math.ceil(skv / 64)
     mfma = 4.0 * b * h * 128 * 64 * d * kv_tiles
-    return _compose(hw, flops, nbytes, mfma, blocks, dtype, {"tile_m": 128, "tile_n": 64}, {"kv_heads": hk})
+    return _compose(hw, flops, nbytes, mfma, blocks, dtype, {"tile_m": 128, "tile_n": 64}, {"kv_heads": hk},
+                    "attention_fp32" if dtype == "float32" else "attention")
 
 
 def ssd_cost(spec: KernelSpec, tensors: dict[str, TensorType], hw: HardwareSpec) -> CostBreakdown:
@@ -139,7 +164,7 @@ def ssd_cost(spec: KernelSpec, tensors: dict[str, TensorType], hw: HardwareSpec)
     flops = 2.0 * b * h * s * (q * n + q * p + 2 * n * p)
     nbytes = sum(_bytes(tensors[x.tensor]) for x in spec.args) + len(spec.outputs) * b * s * h * p * eb
     blocks = b * h * max(1, math.ceil(s / q))
-    return _compose(hw, flops, nbytes, flops, blocks, dtype, {"chunk": q}, {})
+    return _compose(hw, flops, nbytes, flops, blocks, dtype, {"chunk": q}, {}, "ssd")
 
 
 def elementwise_cost(spec: KernelSpec, tensors: dict[str, TensorType], hw: HardwareSpec) -> CostBreakdown:
@@ -147,7 +172,7 @@ def elementwise_cost(spec: KernelSpec, tensors: dict[str, TensorType], hw: Hardw
     nbytes = sum(_bytes(tensors[x.tensor]) for x in spec.args) + sum(_bytes(tensors[o.tensor]) for o in spec.outputs)
     a = spec.attrs
     flops = 2.0 * a.get("batch", 1) * a.get("seq", 1) * a.get("width", 1) * a.get("kernel", 1)
-    return _compose(hw, flops, nbytes, 0.0, 0, dtype, {}, {})
+    return _compose(hw, flops, nbytes, 0.0, 0, dtype, {}, {}, spec.kind)
 
 
 def gather_cost(spec: KernelSpec, tensors: dict[str, TensorType], hw: HardwareSpec) -> CostBreakdown:
@@ -155,7 +180,7 @@ def gather_cost(spec: KernelSpec, tensors: dict[str, TensorType], hw: HardwareSp
     dtype = _dtype(spec, tensors)
     out = tensors[spec.outputs[0].tensor]
     nbytes = 2 * _bytes(out) + _bytes(tensors[spec.arg("ids").tensor])
-    return _compose(hw, 0.0, nbytes, 0.0, 0, dtype, {}, {})
+    return _compose(hw, 0.0, nbytes, 0.0, 0, dtype, {}, {}, "embedding")
 
 
 def kernel_cost(spec: KernelSpec, tensors: dict[str, TensorType], hw: HardwareSpec, tiles: dict[str, int] | None = None) -> CostBreakdown:

@@ -185,7 +185,7 @@ def compile_model(model: torch.nn.Module, example_args: Sequence[Any], config: C
         with stage("bench"):
             res.bench = bench_program(device_program, example_args, hw, warmup=config.bench_warmup,
                                       reps=config.bench_reps)
-            rw.write_json("11_bench.json", res.bench)
+            write_device_results(rw.run_dir, program, hw, res.bench)
     rw.write_json("timings.json", timings)
     return res
 
@@ -230,6 +230,43 @@ def plan_report(result: PlanResult, hw: HardwareSpec, config: CompileConfig) -> 
         lines.append(f"| {c.index} | {len(c.program.kernels) if c.program else '-'} | {est} | {'yes' if c.legal else 'no'} | {note} |")
     lines += ["", "## Chosen program", "", "```", result.program.summary(), "```"]
     return "\n".join(lines)
+
+
+def write_device_results(run_dir: Path, program: Program, hw: HardwareSpec, bench: dict[str, Any]) -> None:
+    """11_bench.json (the measurement) and 10_device_results.{json,md}: per kernel the measured
+    µs next to the cost model's prediction (calibrated where the hardware spec carries a fit),
+    the achieved rate and its fraction of the roofline. 10_* takes the place of the
+    reference's 10_loom_results.json (Loom's optimum per kernel)."""
+    from .cost_models.roofline import category, kernel_cost
+
+    rw = ResultsWriter(run_dir)
+    rw.write_json("11_bench.json", bench)
+    specs = {k.name: k for k in program.kernels}
+    rows = []
+    for name, m in bench["kernels"].items():
+        members = [specs[n] for n in name.split("+") if n in specs]
+        pred = sum(kernel_cost(sp, program.tensors, hw).us for sp in members)
+        rows.append({"kernel": name, "kind": m["kind"], "category": category(members[0], program.tensors),
+                     "entries": m["entries"], "measured_us": m["us"], "predicted_us": pred,
+                     "measured_over_predicted": m["us"] / pred if pred else None, "bound": m.get("bound"),
+                     "achieved": m.get("achieved_tflops", m.get("achieved_gbs")),
+                     "unit": "TFLOP/s" if "achieved_tflops" in m else "GB/s", "frac": m.get("frac")})
+    total_pred = sum(r["predicted_us"] for r in rows)
+    out = {"hw": hw.name, "calibrated": bool(hw.calibration), "forward_us_median": bench["us_median"],
+           "sum_kernel_us": bench.get("sum_kernel_us"), "predicted_total_us": total_pred, "kernels": rows}
+    rw.write_json("10_device_results.json", out)
+    lines = [f"# Device results ({program.name})", "",
+             f"Forward {bench['us_median']:,.1f} µs (graph replay, median); the cost model "
+             f"({'calibrated' if hw.calibration else 'uncalibrated'}) predicts {total_pred:,.1f} µs.", "",
+             "| kernel | category | measured µs | predicted µs | measured/predicted | achieved | roofline |",
+             "|---|---|---:|---:|---:|---:|---:|"]
+    for r in rows:
+        ratio = f"{r['measured_over_predicted']:.2f}" if r["measured_over_predicted"] else "-"
+        ach = f"{r['achieved']:,.0f} {r['unit']}" if r["achieved"] is not None else "-"
+        frac = f"{100 * r['frac']:.1f}%" if r["frac"] is not None else "-"
+        lines.append(f"| {r['kernel']} | {r['category']} | {r['measured_us']:,.1f} | {r['predicted_us']:,.1f} | "
+                     f"{ratio} | {ach} | {frac} |")
+    rw.write_text("10_device_results.md", "\n".join(lines) + "\n")
 
 
 def cost_report_json(program: Program, hw: HardwareSpec, config: CompileConfig) -> dict[str, Any]:
