@@ -252,7 +252,6 @@ def bench_decode_c5(args) -> dict:
     pos = cfg.seq - 1
     model = build_llama_block(cfg, seed=0)
     sd = {k: v for k, v in model.state_dict().items() if not k.startswith(("rope", "attn_bias"))}
-    del model
     dev = torch.device("cuda", 0)
     blk = DecodeBlock(sd, hidden=cfg.hidden, heads=cfg.heads, kv_heads=cfg.n_kv, intermediate=cfg.intermediate,
                       eps=cfg.eps, rope_theta=cfg.rope_theta, batch=cfg.batch, max_len=cfg.seq, device=dev)
@@ -310,7 +309,44 @@ def bench_decode_c5(args) -> dict:
                                           "the decode step in bf16 torch ops on the dequantised weights "
                                           "(oracle.llama.decode_step; the reference has no decode path), whole batch",
                                           1.0)
+    del blk
+    obj["compiled"] = _decode_compiled(args, model, cfg, pos, x, kc, vc, nbytes, kw)
     return obj
+
+
+def _decode_compiled(args, model, cfg, pos, x, kc, vc, nbytes, kw) -> dict:
+    """The same decode step through compile_model: LlamaDecodeBlock (the block's weights
+    quantised per output channel, the model's RoPE rows at pos) -> OpIR with e4m3 weight
+    tensors and an attention_decode kernel -> DeviceProgram, graph-replayed."""
+    import torch
+    from oracle.llama import decode_step
+    from targets.llama_decode import PROJECTIONS, LlamaDecodeBlock
+    from torch_helion import CompileConfig, compile_model
+    from torch_helion.hip.bench import bench_program
+
+    m = LlamaDecodeBlock(model, pos).eval()
+    t0 = time.time()
+    res = compile_model(m, (x.cpu(), kc, vc), CompileConfig(run_name="bench_decode_c5", results_dir=RESULTS,
+                                                            backend="hip", device_check=False, reference_check=False,
+                                                            verify_passes=False, planner_mode="greedy"))
+    log(f"decode step compiled in {time.time() - t0:.1f} s: {len(res.program.kernels)} kernels")
+    dp = res.device_program
+    b = bench_program(dp, (x, kc, vc), res.hw, warmup=args.warmup, reps=args.steps)
+    write_device_results(res.run_dir, res.program, res.hw, b)
+    us = b["us_median"]
+    dp.run([x, kc, vc])
+    torch.cuda.synchronize()
+    out = dp.outputs(fp32=True)[0].double().cpu()
+    w = {name: getattr(m, f"{s}_q").float() * getattr(m, f"{s}_s")[:, None] for s, name in PROJECTIONS.items()}
+    w["input_norm.weight"], w["post_norm.weight"] = m.g1, m.g2
+    rope = (m.rope_cos.expand(pos + 1, -1), m.rope_sin.expand(pos + 1, -1))
+    ref = decode_step(x.cpu(), w, kc, vc, pos, rope=rope, **kw)[0]
+    ref_b = decode_step(x.cpu(), w, kc, vc, pos, rope=rope, storage=torch.bfloat16, **kw)[0]
+    return {"us": us, "tokens_per_s": cfg.batch / (us * 1e-6), "kernels": len(res.program.kernels),
+            "launches": len(dp.launches), "frac": nbytes / (us * 1e-6) / 1e9 / 8000.0,
+            "per_kernel_us": {k: round(v["us"], 2) for k, v in b["kernels"].items()},
+            "parity": {**_parity(out, ref, ref_b), "against": "oracle.llama.decode_step float64, the model's "
+                       "dequantised weights and RoPE rows"}}
 
 
 # ------------------------------------------------------------------------ C4

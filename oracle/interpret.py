@@ -6,9 +6,11 @@ attention and scan kinds) with the op semantics of optimizer/evaluate.py:36-147,
 written independently of the product's interpreter and computing in float64
 by default. New kinds follow their defining formulas: causal / grouped-KV
 attention, ``ssd_chunked`` (the O(S) recurrence of oracle.mamba),
-``conv1d`` (a direct sum over the kernel taps) and ``embedding`` (row
+``conv1d`` (a direct sum over the kernel taps), ``embedding`` (row
 indexing of the table: ``out[t] = table[ids[t]]``, what torch.nn.Embedding
-defines).
+defines) and ``attention_decode`` (one query per sequence against a cache's
+first ``pos`` rows plus the new key/value); gemm weights may be e4m3 with
+per-column scales and an activation-side norm gain.
 
 ``storage="declared"`` rounds every kernel output to the dtype the Program
 declares for it, i.e. what a device that stores intermediates in their
@@ -130,12 +132,28 @@ def run_kernel(spec, env: dict[str, torch.Tensor], dtype=torch.float64) -> dict[
     vals: dict[str, torch.Tensor] = {}
     if spec.kind == "gemm":
         lhs = args["lhs"]
+        # e4m3 weights: W = q * s per output column ("<rhs>_scale"); an activation-side norm
+        # gain (role "gain") scales the lhs columns of the products only, not the sum of squares
+        a_lhs = lhs * args["gain"] if "gain" in args else lhs
         for g in spec.gemms:
-            vals[g.acc] = lhs @ args[g.rhs]
+            w = args[g.rhs]
+            if g.rhs + "_scale" in args:
+                w = w * args[g.rhs + "_scale"]
+            vals[g.acc] = a_lhs @ w
         if spec.sumsq:
             vals["sumsq"] = (lhs * lhs).sum(-1, keepdim=True)
     elif spec.kind == "attention":
         return {spec.outputs[0].tensor: attention(args["q"], args["k"], args["v"], spec.attrs)}
+    elif spec.kind == "attention_decode":
+        # keys/values: the cache's first pos rows of each sequence, then the new token's
+        a = spec.attrs
+        b, L, pos = a["batch"], a["max_len"], a["pos"]
+        kw = a["kv_heads"] * a["head_dim"]
+        keys = torch.cat([args["k_cache"].reshape(b, L, kw)[:, :pos], args["k_new"].reshape(b, 1, kw)], 1)
+        vals_ = torch.cat([args["v_cache"].reshape(b, L, kw)[:, :pos], args["v_new"].reshape(b, 1, kw)], 1)
+        out = [attention(args["q"].reshape(b, -1)[i:i + 1], keys[i], vals_[i],
+                         {**a, "batch": 1, "seq": 1, "seq_kv": pos + 1, "causal": False}) for i in range(b)]
+        return {spec.outputs[0].tensor: torch.cat(out, 0)}
     elif spec.kind == "ssd":
         vals["acc"] = ssd_quadratic(*(args[r] for r in ("c", "b", "x", "cum", "dt", "mask", "dskip")), spec.attrs)
     elif spec.kind == "ssd_chunked":

@@ -295,6 +295,59 @@ def test_decode_step_fp8_vs_oracle(gpu, which):
     assert torch.equal(blk.k_cache[:, :pos].cpu(), kc[:, :pos])
 
 
+@pytest.mark.parametrize("which", ["small", "c5"])
+def test_compile_model_decode_fp8_vs_oracle(gpu, tmp_path, which):
+    """The decode step through compile_model: a LlamaDecodeBlock (e4m3 weights quantised as the
+    BASELINE specifies, gains on the activations) compiles to a Program with e4m3 weight
+    tensors and an attention_decode kernel; on the device its output (fp32 copy) and the new
+    key/value rows, written straight into the cache inputs at pos, meet the same bars as the
+    hand-assembled step against the oracle's decode step on the spec weights."""
+    from oracle.llama import decode_step
+    from targets.llama_block import LlamaBlockConfig, build_llama_block, config_c5
+    from targets.llama_decode import PROJECTIONS, LlamaDecodeBlock
+
+    if which == "c5":
+        cfg, pos = config_c5(), 4096
+    else:
+        cfg, pos = LlamaBlockConfig(batch=4, seq=80, hidden=256, heads=4, kv_heads=2, intermediate=512, causal=True,
+                                    dtype=torch.bfloat16, rope_theta=500000.0), 77
+    announce(f"e2e compile_model decode fp8 {which} pos={pos}")
+    sd, x, kc, vc = _decode_case(cfg, pos, seed=3)
+    m = LlamaDecodeBlock(build_llama_block(cfg, seed=3), pos).eval()
+    w_spec = _spec_quantised(sd)
+    for short, name in PROJECTIONS.items():
+        deq = getattr(m, f"{short}_q").float() * getattr(m, f"{short}_s")[:, None]
+        assert torch.equal(deq, w_spec[name]), name
+    res = _compile(m, (x, kc, vc), tmp_path, f"decode_{which}", device_check=False, reference_check=False,
+                   verify_passes=False)
+    prog = res.program
+    assert [k.kind for k in prog.kernels].count("attention_decode") == 1
+    assert all(prog.tensors[k.arg(g.rhs).tensor].dtype == "float8_e4m3fn" for k in prog.kernels
+               if k.kind == "gemm" for g in k.gemms)
+    dp = res.device_program
+    dp.run([x, kc, vc])
+    torch.cuda.synchronize()
+    out, k_dev, v_dev = (t.double().cpu() for t in dp.outputs(fp32=True))
+    rope = (m.rope_cos.expand(pos + 1, -1), m.rope_sin.expand(pos + 1, -1))
+    kw = dict(heads=cfg.heads, kv_heads=cfg.n_kv, eps=cfg.eps, theta=cfg.rope_theta, rope=rope)
+    ref, kn, vn = decode_step(x, w_spec, kc, vc, pos, **kw)
+    ref_b, kn_b, vn_b = decode_step(x, w_spec, kc, vc, pos, storage=torch.bfloat16, **kw)
+    floor = (ref_b - ref).abs().max().item()
+    rel = ((out - ref).abs().max() / ref.abs().max()).item()
+    mx = (out - ref).abs().max().item()
+    print(f"decode {which}: normalised {rel:.3e}, max-abs {mx:.4f}, bf16 floor {floor:.4f}", flush=True)
+    assert rel < 2e-2, rel
+    assert mx <= 2 * floor, (mx, floor)
+    for got, want, want_b in ((k_dev, kn, kn_b), (v_dev, vn, vn_b)):
+        err = (got - want).abs().max().item()
+        assert err <= 2 * (want_b - want).abs().max().item(), err
+    # the new rows live in the cache inputs at pos; the rows before pos are untouched
+    L, hk, hd = cfg.seq, cfg.n_kv, cfg.head_dim
+    k_cache = dp.tensor("k_cache").view(cfg.batch, L, hk, hd)
+    assert torch.equal(k_cache[:, pos].double().cpu(), k_dev)
+    assert torch.equal(k_cache[:, :pos].cpu(), kc[:, :pos])
+
+
 def _lm_check(res, model, cfg, ids, prefix: int, layers=None):
     """Logits of the HIP program (fp32 copy) for sequence 0's first ``prefix`` tokens
     against the oracle's model_forward in float64 on those tokens alone (the model is

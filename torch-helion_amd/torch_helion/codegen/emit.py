@@ -21,7 +21,8 @@ class CodegenError(RuntimeError):
     pass
 
 
-_ENTRY = {"gemm": "th_gemm", "attention": "th_attention_prefill", "ssd": "th_ssd_chunked",
+_ENTRY = {"gemm": "th_gemm", "attention": "th_attention_prefill", "attention_decode": "th_attention_decode",
+          "ssd": "th_ssd_chunked",
           "ssd_chunked": "th_ssd_chunked", "conv1d": "th_conv1d_causal", "embedding": "th_embedding"}
 
 

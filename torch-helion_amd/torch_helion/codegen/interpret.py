@@ -22,12 +22,22 @@ def run_kernel(spec: KernelSpec, env: dict[str, torch.Tensor]) -> dict[str, torc
     vals: dict[str, torch.Tensor] = {}
     if spec.kind == "gemm":
         lhs = args["lhs"]
+        # e4m3 weights carry per-column scales (arg "<rhs>_scale"); an activation-side
+        # RMSNorm gain (role "gain") multiplies the lhs columns, the sum of squares does not see it
+        a_lhs = lhs * args["gain"] if "gain" in args else lhs
         for g in spec.gemms:
-            vals[g.acc] = lhs @ args[g.rhs]
+            w = args[g.rhs]
+            if g.rhs + "_scale" in args:
+                w = w * args[g.rhs + "_scale"]
+            vals[g.acc] = a_lhs @ w
         if spec.sumsq:
             vals["sumsq"] = (lhs * lhs).sum(-1, keepdim=True)
     elif spec.kind == "attention":
         return {spec.outputs[0].tensor: eval_op("attention", [args["q"], args["k"], args["v"]], spec.attrs)}
+    elif spec.kind == "attention_decode":
+        return {spec.outputs[0].tensor: eval_op("attention_decode", [args[r] for r in
+                                                                   ("q", "k_cache", "v_cache", "k_new", "v_new")],
+                                                spec.attrs)}
     elif spec.kind in _ROLES:
         vals["acc"] = eval_op(spec.kind, [args[r] for r in _ROLES[spec.kind]], spec.attrs)
         if spec.kind == "embedding":

@@ -82,6 +82,8 @@ def category(spec: KernelSpec, tensors: dict[str, TensorType]) -> str:
     if spec.kind == "gemm":
         if not spec.gemms:
             return "norm"
+        if tensors[spec.arg(spec.gemms[0].rhs).tensor].dtype == "float8_e4m3fn":
+            return "gemm_fp8"
         return "gemm_fp32" if dtype == "float32" else "gemm_bf16"
     if spec.kind == "attention":
         return "attention_fp32" if dtype == "float32" else "attention"
@@ -119,10 +121,17 @@ def gemm_cost(spec: KernelSpec, tensors: dict[str, TensorType], hw: HardwareSpec
     dtype = _dtype(spec, tensors)
     eb = DTYPE_BYTES.get(dtype, 4)
     n_acc = fused_acc_count(spec) if spec.gemms else 0
-    extras = [a for a in spec.args if a.role == "extra"]
-    nbytes = T * K * eb + n_acc * K * N * eb + sum(_bytes(tensors[a.tensor]) for a in extras) + len(spec.outputs) * T * N * eb
+    extras = [a for a in spec.args if a.role in ("extra", "scale", "gain")]
+    # weight bytes at the weight's own type (e4m3 weights: one byte per element)
+    wb = DTYPE_BYTES.get(tensors[spec.arg(spec.gemms[0].rhs).tensor].dtype, eb) if spec.gemms else eb
+    nbytes = T * K * eb + n_acc * K * N * wb + sum(_bytes(tensors[a.tensor]) for a in extras) + len(spec.outputs) * T * N * eb
     if n_acc == 0:  # stand-alone normalisation: HBM bound
         return _compose(hw, 3.0 * T * K, nbytes, 0.0, 0, dtype, {"tile_t": 4}, {"n_acc": 0}, "norm")
+    if wb == 1:
+        # e4m3 weights (decode): a weight stream, bound by HBM; the MFMA term is the products at fp8 rate
+        flops = 2.0 * T * N * K * n_acc
+        return _compose(hw, flops, nbytes, flops, math.ceil(N / 64), "float8_e4m3fn", {"tile_n": 64},
+                        {"n_acc": n_acc, "weights": "float8_e4m3fn"}, "gemm_fp8")
     flops = 2.0 * T * N * K * n_acc
     bm, bn = gemm_tiles(N, n_acc, T, dtype)
     tiles_m, tiles_n = math.ceil(T / bm), math.ceil(N / bn)
@@ -152,6 +161,20 @@ def attention_cost(spec: KernelSpec, tensors: dict[str, TensorType], hw: Hardwar
     mfma = 4.0 * b * h * 128 * 64 * d * kv_tiles
     return _compose(hw, flops, nbytes, mfma, blocks, dtype, {"tile_m": 128, "tile_n": 64}, {"kv_heads": hk},
                     "attention_fp32" if dtype == "float32" else "attention")
+
+
+def attention_decode_cost(spec: KernelSpec, tensors: dict[str, TensorType], hw: HardwareSpec) -> CostBreakdown:
+    """One query row per (sequence, head) against pos cached rows plus the new one: the
+    cache read dominates (HBM bound)."""
+    a = spec.attrs
+    b, h, d, pos = a["batch"], a["heads"], a["head_dim"], a["pos"]
+    hk = a.get("kv_heads", h)
+    dtype = _dtype(spec, tensors)
+    eb = DTYPE_BYTES.get(dtype, 4)
+    n = pos + 1
+    flops = 4.0 * b * h * n * d
+    nbytes = (2 * b * h * d + 2 * b * n * hk * d) * eb
+    return _compose(hw, flops, nbytes, 0.0, b * hk, dtype, {}, {"kv_heads": hk, "keys": n}, "attention_decode")
 
 
 def ssd_cost(spec: KernelSpec, tensors: dict[str, TensorType], hw: HardwareSpec) -> CostBreakdown:
@@ -188,6 +211,8 @@ def kernel_cost(spec: KernelSpec, tensors: dict[str, TensorType], hw: HardwareSp
         return gemm_cost(spec, tensors, hw)
     if spec.kind == "attention":
         return attention_cost(spec, tensors, hw)
+    if spec.kind == "attention_decode":
+        return attention_decode_cost(spec, tensors, hw)
     if spec.kind in ("ssd", "ssd_chunked"):
         return ssd_cost(spec, tensors, hw)
     if spec.kind == "conv1d":

@@ -25,6 +25,7 @@ from .epilogue import (EpiloguePlan, build_trees, is_rotated_copy, match_epilogu
 
 _TORCH_DT = {"float32": torch.float32, "bfloat16": torch.bfloat16, "float16": torch.float16,
              "int64": torch.int64, "int32": torch.int32, "float8_e4m3fn": torch.float8_e4m3fn}
+_FP8 = torch.float8_e4m3fn
 
 
 def _err(kernel: str, msg: str) -> abi.HipBackendError:
@@ -96,6 +97,10 @@ class DeviceProgram:
             # fp32; rounding to the declared dtype is only the storage step)
             shadowed |= {o for o in program.outputs
                          if o in produced and o not in exact and program.tensors[o].dtype in half}
+        # decode programs: outputs the device writes straight into a cache input at
+        # row ``pos`` of each sequence (the new token's key/value), kept in the cache's dtype
+        self._slots = dict(program.metadata.get("cache_slots", {}))
+        shadowed -= set(self._slots)
         self._shadowed = shadowed
         self.shadow: dict[str, torch.Tensor] = {}
         # Intermediates (and shadows, workspaces, normalised operands) come from a
@@ -149,10 +154,23 @@ class DeviceProgram:
             if name in self.buffers:
                 continue
             t = self.program.tensors[name]
+            if name in self._slots:
+                self.buffers[name] = self._cache_row(name)
+                continue
             last = self._last.get(name, self._cur)
             self.buffers[name] = self._device_buffer(t.shape, _TORCH_DT[t.dtype], last)
             if name in self._shadowed:
                 self.shadow[name] = self._device_buffer(t.shape, torch.float32, last)
+
+    def _cache_row(self, name: str) -> torch.Tensor:
+        """Row ``pos`` of every sequence of the cache input a cache-slot output lives in:
+        a [batch, width] view whose row stride is the cache's sequence stride."""
+        slot, dec = self._slots[name], self.program.metadata["decode"]
+        cache = self.buffers[slot["cache"]]
+        b, L, pos = dec["batch"], dec["max_len"], slot["pos"]
+        if not 0 <= pos < L or cache.shape[0] != b * L:
+            raise _err(name, f"cache slot at pos {pos} outside the cache {tuple(cache.shape)} (batch {b}, max_len {L})")
+        return cache.view(b, L, cache.shape[1])[:, pos]
 
     def memory_report(self) -> dict[str, int]:
         """Bytes of intermediate storage held, and what one buffer per tensor would hold."""
@@ -246,6 +264,8 @@ class DeviceProgram:
             return self._lower_gemm(spec)
         if spec.kind == "attention":
             return [self._lower_attention(spec)]
+        if spec.kind == "attention_decode":
+            return [self._lower_attention_decode(spec)]
         if spec.kind in ("ssd", "ssd_chunked"):
             from .ssd import lower_ssd
             return lower_ssd(self, spec)
@@ -285,6 +305,32 @@ class DeviceProgram:
 
         return Launch(spec.name, "attention", run, "th_attention_prefill", kw)
 
+    def _lower_attention_decode(self, spec: KernelSpec) -> Launch:
+        """Keys/values 0..pos-1 from the caches and the new token's at pos: the new key and
+        value must be cache-slot outputs (written into the caches at row pos by their
+        producer), so one th_attention_decode over rows 0..pos reads them all."""
+        a = spec.attrs
+        b, L, pos, hk, hd = a["batch"], a["max_len"], a["pos"], a["kv_heads"], a["head_dim"]
+        caches = []
+        for new, cache in (("k_new", "k_cache"), ("v_new", "v_cache")):
+            t_new, t_cache = spec.arg(new).tensor, spec.arg(cache).tensor
+            slot = self._slots.get(t_new)
+            if slot is None or slot["cache"] != t_cache or slot["pos"] != pos:
+                raise _err(spec.name, f"{new} ({t_new}) is not written into {t_cache} at row {pos}: "
+                                      "attention_decode needs the program's cache_slots")
+            caches.append(self.buffers[t_cache].view(b, L, hk, hd))
+        q = self.buffers[spec.arg("q").tensor]
+        out = self.buffers[spec.outputs[0].tensor]
+        ws_bytes = ops.attention_decode_workspace_bytes(b, a["heads"], hk, hd, L)
+        ws = self._workspace(max(ws_bytes // 4, 1))
+        kw = dict(scale=float(a["scale"]), fixed_len=pos + 1)
+
+        def run() -> None:
+            ops.attention_decode(q, caches[0], caches[1], out, workspace=ws, kernel=spec.name, **kw)
+
+        return Launch(spec.name, "attention_decode", run, "th_attention_decode",
+                      {"batch": b, "heads_q": a["heads"], "heads_kv": hk, "head_dim": hd, "keys": pos + 1})
+
     # gemm -----------------------------------------------------------------
     def _pack(self, spec: KernelSpec, rhs_args: list[str], in_dtype: torch.dtype,
               unfold: bool = False) -> Callable[[], torch.Tensor]:
@@ -298,6 +344,11 @@ class DeviceProgram:
                                   in_dtype)
             return lambda: packed
         srcs = [self.buffers[t] for t in tens]
+        if in_dtype == _FP8:
+            if not all(t in self.program.params and s.dtype == _FP8 for t, s in zip(tens, srcs)):
+                raise _err(spec.name, "e4m3 products need e4m3 parameter weights")
+            packed = ops.pack_rhs(srcs, _FP8)
+            return lambda: packed
         if all(t in self.program.params for t in tens):
             srcs = [s if s.dtype in (torch.float32, torch.bfloat16) else s.float() for s in srcs]
             if in_dtype == torch.float32:
@@ -365,8 +416,15 @@ class DeviceProgram:
         T, N, K = spec.grid["rows"], spec.grid["cols"], spec.k_extent
         lhs_t = spec.arg("lhs").tensor
         lhs = self.buffers[lhs_t]
-        in_dtype = lhs.dtype
         rhs_of = {i: g.rhs for i, g in enumerate(spec.gemms)}
+        # e4m3 weights (decode programs): bf16 lhs x e4m3 rhs with per-column scales
+        fp8 = [self.program.tensors[spec.arg(g.rhs).tensor].dtype == "float8_e4m3fn" for g in spec.gemms]
+        if any(fp8) and not all(fp8):
+            raise _err(spec.name, "a kernel mixes e4m3 and higher-precision weights")
+        fp8 = all(fp8)
+        if fp8 and lhs.dtype != torch.bfloat16:
+            raise _err(spec.name, "e4m3 weights need a bf16 lhs")
+        in_dtype = _FP8 if fp8 else lhs.dtype
         outs = []
         rope_tables: dict[tuple[str, str], tuple[torch.Tensor, torch.Tensor, int, int]] = {}
         for o in plan.outs:
@@ -382,13 +440,17 @@ class DeviceProgram:
                     return None
                 rp, period = geo
                 wa, wb = self._host(spec.arg(rhs_of[a]).tensor), self._host(spec.arg(rhs_of[b]).tensor)
+                if fp8 and wa is not None and wb is not None:
+                    # compare the dequantised weights: values and scales are both rotated
+                    wa, wb = (self._host(spec.arg(rhs_of[i]).tensor).float()
+                              * self._host(spec.arg(rhs_of[i] + "_scale").tensor).float()[None, :] for i in (a, b))
                 # the tables repeat every half head (cos = cat(f, f)), so the head
                 # dim is the multiple of their period for which w_b is w_a rotated
                 hd, fused = period, False
                 if self.fuse_rope and wa is not None and wb is not None:
                     cand = period
                     while cand <= N and N % cand == 0:
-                        if is_rotated_copy(wa, wb, cand):
+                        if is_rotated_copy(wa.float(), wb.float(), cand):
                             hd, fused = cand, True
                             break
                         cand *= 2
@@ -452,10 +514,23 @@ class DeviceProgram:
         rope = next(iter(rope_tables.values())) if rope_tables else None
         info = {"n_acc": len(used), "ops": [op for _, op, *_ in outs], "rscale": plan.rscale is not None,
                 "rope_fused": any(op == abi.EPI_ROPE for _, op, *_ in outs), "gain_on_activation": normed is not None}
+        fp8_kw: dict[str, Any] = {}
+        if fp8:
+            scale_t = [rhs_of[i] + "_scale" for i in used]
+            names = {x.name for x in spec.args}
+            if any(x not in names for x in scale_t):
+                raise _err(spec.name, "e4m3 weights without their <rhs>_scale arguments")
+            scale = torch.stack([self.buffers[spec.arg(x).tensor].float().reshape(-1) for x in scale_t]).contiguous()
+            ws = self._workspace(max(ops.gemm_workspace_bytes(T, N, K, len(used), _FP8), 16), torch.uint8)
+            fp8_kw = dict(in_dtype=_FP8, rhs_scale=scale, workspace=ws)
+            if "gain" in names:
+                # activation-side norm gain: the products see lhs * g, the sum of squares lhs
+                fp8_kw["lhs_gain"] = self.buffers[spec.arg("gain").tensor].float().reshape(-1).contiguous()
+            info.update({"weights": "float8_e4m3fn", "lhs_gain": "gain" in names})
 
         def run() -> None:
             call = ops.GemmCall(T, N, K, len(used), lhs, get_packed(), epi, sumsq=sumsq,
-                                rscale_mask=mask, inv_k=inv_k, eps=eps, extras=extra_bufs)
+                                rscale_mask=mask, inv_k=inv_k, eps=eps, extras=extra_bufs, **fp8_kw)
             if rope is not None:
                 call.rope_cos, call.rope_sin, call.rope_period, call.rope_head_dim = rope[0], rope[1], rope[2], rope[3]
             ops.gemm(call, kernel=spec.name)

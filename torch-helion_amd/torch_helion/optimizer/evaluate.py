@@ -188,11 +188,27 @@ _OPS: dict[str, Callable[[list[torch.Tensor], dict[str, Any]], torch.Tensor]] = 
     "ssd": _ssd,
     "ssd_chunked": _ssd_chunked,
     "attention": lambda xs, a: attention_ref(xs[0], xs[1], xs[2], a),
+    "attention_decode": lambda xs, a: attention_decode_ref(*xs, a),
     "conv1d": lambda xs, a: conv1d_ref(xs[0], xs[1], a),
     "conv1d_raw": _conv1d_raw,
     "pad": _pad,
     "embedding": lambda xs, a: F.embedding(xs[1].long(), xs[0]),
 }
+
+
+def attention_decode_ref(q, k_cache, v_cache, k_new, v_new, a: dict[str, Any]) -> torch.Tensor:
+    """One query per sequence against the cache's first ``pos`` keys plus the new one:
+    q [B, H*d]; caches [B*L, Hkv*d] (token-major, L = max_len); k_new, v_new [B, Hkv*d]."""
+    b, h, hk, d, pos = a["batch"], a["heads"], a["kv_heads"], a["head_dim"], a["pos"]
+    kc = k_cache.reshape(b, a["max_len"], hk * d)[:, :pos]
+    vc = v_cache.reshape(b, a["max_len"], hk * d)[:, :pos]
+    keys = torch.cat([kc, k_new.reshape(b, 1, hk * d)], 1)
+    vals = torch.cat([vc, v_new.reshape(b, 1, hk * d)], 1)
+    attrs = {"batch": b, "seq": 1, "seq_kv": pos + 1, "heads": h, "kv_heads": hk, "head_dim": d,
+             "scale": a["scale"], "causal": False}
+    qs = q.reshape(b, 1, h * d)
+    outs = [attention_ref(qs[i], keys[i], vals[i], {**attrs, "batch": 1}) for i in range(b)]
+    return torch.cat(outs, 0)
 
 
 def eval_op(op: str, args: list[torch.Tensor], attrs: dict[str, Any]) -> torch.Tensor:

@@ -201,6 +201,13 @@ def match_head_split(prov: Provenance, transpose_last: bool = False, allow_group
         cands = [(bb, bh // bb, True) for bb in range(1, bh + 1) if bh % bb == 0]
     else:
         return None
+    # a token-major base has B*S rows ([B*S, N], or [B, S, N]): with S = 1 a merged
+    # [B*H, 1, d] view reads the same flat offsets for every split of B*H, so the
+    # base's own row structure decides between them
+    if len(prov.base_shape) >= 2:
+        rows = math.prod(prov.base_shape[:-1])
+        lead = prov.base_shape[0] if len(prov.base_shape) == 3 else None
+        cands = [c for c in cands if c[0] * s == rows and (lead is None or c[0] == lead)] or cands
     for b, h, merged in cands:
         kv_opts = [h]
         if allow_grouped:

@@ -452,6 +452,9 @@ def match_attention(g: OpGraph) -> int:
         if dv is None or core(dv) != core(dq) or dv.get("kv_heads") != dk.get("kv_heads"):
             continue
         b, sq, h, d = core(dq)
+        # the last layout node of bmm2's single-user chain that reads it in token-major
+        # [T, H*d] order (with S = 1 an earlier view of the chain already does, and
+        # converting that one would leave the rest of the chain reading a 2-D tensor)
         final = None
         cur = bmm2
         while True:
@@ -462,7 +465,6 @@ def match_attention(g: OpGraph) -> int:
             prov = trace_layout(g, cur.name)
             if prov.base == bmm2.name and is_head_merge(prov, b, sq, h, d):
                 final = cur
-                break
         if final is None:
             continue
         attrs = {"batch": b, "seq": sq, "heads": h, "head_dim": d, "scale": scale}

@@ -96,6 +96,12 @@ def eager_reference(model: torch.nn.Module, args: Sequence[Any], batch_slice: in
 
 def compile_model(model: torch.nn.Module, example_args: Sequence[Any], config: CompileConfig | None = None) -> CompileResult:
     config = config or CompileConfig()
+    if getattr(model, "is_decode_step", False):
+        # a decode step (one token per sequence against a KV cache, e4m3 weights): its OpIR
+        # is derived from the block's own S = 1 capture (torch_helion/decode.py)
+        from .decode import compile_decode
+
+        return compile_decode(model, example_args, config)
     rw = ResultsWriter(config.run_dir)
     timings: dict[str, float] = {}
 
