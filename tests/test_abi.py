@@ -255,11 +255,11 @@ def test_lhs_gain_only_for_fp8(lib):
 
 def test_gemm_noalloc_refuses_oversized_scratch(lib):
     """th_gemm_noalloc checks the fixed scratch size before anything else (here, before the
-    missing device): 128 rows x 24576 e4m3 columns at K = 16384 need more than it holds."""
+    missing device): 128 rows x 4096 e4m3 columns at K = 131072 need more than it holds."""
     from torch_helion.hip import abi
 
-    d = _gemm_desc(in_dtype=abi.TH_F8E4M3, rhs_scale=16384, M=128, N=24576, K=16384, ld_lhs=16384)
-    assert lib.th_gemm_workspace_bytes(128, 24576, 16384, 1, abi.TH_F8E4M3) > abi.GEMM_NOALLOC_SCRATCH_BYTES
+    d = _gemm_desc(in_dtype=abi.TH_F8E4M3, rhs_scale=16384, M=128, N=4096, K=131072, ld_lhs=131072)
+    assert lib.th_gemm_workspace_bytes(128, 4096, 131072, 1, abi.TH_F8E4M3) > abi.GEMM_NOALLOC_SCRATCH_BYTES
     assert lib.th_gemm_noalloc(C.byref(d), None) == abi.TH_ERR_INVALID
     assert "scratch" in abi.last_error(lib), abi.last_error(lib)
     assert lib.th_gemm_noalloc(None, None) == abi.TH_ERR_INVALID

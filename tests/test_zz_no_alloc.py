@@ -78,7 +78,7 @@ def test_noalloc_refuses_sizes_beyond_its_scratch(gpu):
     from torch_helion.hip import abi, ops
 
     lib = abi.load()
-    M, N, K = 128, 24576, 16384
+    M, N, K = 128, 4096, 131072
     assert lib.th_gemm_workspace_bytes(M, N, K, 1, abi.TH_F8E4M3) > abi.GEMM_NOALLOC_SCRATCH_BYTES
     x = torch.zeros(M, K, dtype=torch.bfloat16, device=gpu)
     packed = torch.zeros(lib.th_gemm_packed_bytes(N, K, 1, abi.TH_F8E4M3), dtype=torch.uint8, device=gpu)

@@ -11,13 +11,17 @@
 // v_mfma_f32_32x32x16_bf16 with fp32 accumulation.
 //
 // Main path (K a multiple of 128, n_acc 1 or 2, bn = 128 / n_acc):
-//   gemm_fp8_lds_kernel     one workgroup per (128-column packed tile, K split);
-//                           the four waves own 32 columns each and share the
-//                           activation slices, which stream through three
-//                           rotating LDS buffers by direct loads while each
-//                           wave's weights (contiguous KiB blocks of the
-//                           fragment-major packing) go to registers; a single
-//                           split finishes its tiles in the kernel;
+//   fp8_gain_prep_kernel    with an activation-side RMSNorm gain: the rows
+//                           scaled once, bf16(x g), and their unscaled sums
+//                           of squares, into the workspace;
+//   gemm_fp8_lds_kernel     one workgroup of eight waves per (128-column packed
+//                           tile, K split); four column groups of 32 x two K
+//                           halves, sharing the activation slices, which
+//                           stream through rotating LDS buffers by direct
+//                           loads while each wave's weights (contiguous KiB
+//                           blocks of the fragment-major packing) go to
+//                           registers; a single split finishes its tiles in
+//                           the kernel;
 //   gemm_fp8_reduce4_kernel with several splits: sums them in a fixed order
 //                           (deterministic), 4 columns per thread, and applies
 //                           s_i[n], the RMS row scale and the fused output ops.
@@ -32,6 +36,7 @@
 //                           of squares);
 //   gemm_fp8_reduce_kernel  one thread per output element, same sums and ops.
 #include <type_traits>
+#include <utility>
 
 #include "common.h"
 #include "gemm_internal.h"
@@ -41,9 +46,12 @@ namespace th {
 typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
 typedef __attribute__((ext_vector_type(4))) uint32_t u32x4_t;
 
-// K capacity of the activation-gain staging of gemm_fp8_lds_kernel (fp32
-// values in LDS); the launch splits K so no split covers more.
-constexpr int FP8_GAIN_K = 4096;
+// f(integral_constant<int, I>) for I = 0, 1, ... in order (compile-time slot indices)
+template <int... I, class F>
+__device__ __forceinline__ void unroll_seq(std::integer_sequence<int, I...>, F&& f) {
+  (f(std::integral_constant<int, I>()), ...);
+}
+
 
 __device__ __forceinline__ bf16x8_t fp8x8_to_bf16x8(uint32_t lo, uint32_t hi) {
   union {
@@ -358,11 +366,11 @@ __device__ __forceinline__ void fp8_emit4(const Fp8K& p, int64_t m, int64_t n4, 
 // tl[m][i bn + j] (row stride ld floats), with the tile's per-column scales
 // at sc[i bn + j]; rrs holds the M row scales. One thread per (row, 4
 // columns).
-__device__ __forceinline__ void fp8_tile_out(const Fp8K& p, int t, int tid, const float* tl, int ld, const float* sc,
-                                             const float* rrs) {
+__device__ __forceinline__ void fp8_tile_out(const Fp8K& p, int t, int tid, int nthr, const float* tl, int ld,
+                                             const float* sc, const float* rrs) {
   const int M = (int)p.M, bn = (int)p.bn, q4 = bn >> 2;
   const int64_t n0 = (int64_t)t * bn;
-  for (int e = tid; e < M * q4; e += 256) {
+  for (int e = tid; e < M * q4; e += nthr) {
     const int m = e / q4;
     const int64_t n4 = n0 + ((e - m * q4) << 2);
     if (n4 >= p.N) continue;
@@ -376,58 +384,57 @@ __device__ __forceinline__ void fp8_tile_out(const Fp8K& p, int t, int tid, cons
   }
 }
 
-// grid (Npk / (128 NG), splits). The four waves of a workgroup own 32 NG
-// packed columns each and share the workgroup's K range: activation slices
-// (KS of K for all 32 TM rows) stream into NBUF rotating LDS buffers by
-// direct loads, cooperatively, while each wave loads its own weights (NG KiB
-// per 32-K chunk, fragment-major) into registers. Both streams run NBUF - 1
-// slices ahead of the MFMAs, so a wave keeps 2 (ALD + WLD) loads in flight;
-// one barrier per slice frees the buffer the next slice lands in.
+// grid (Npk / (128 NG), splits), eight waves per workgroup. Waves w and
+// w + 4 own the same 32 NG packed columns and take the two K halves of every
+// slice (intra-workgroup split-K, summed in LDS at the end), so two waves
+// share each SIMD: one wave's LDS round trips and barrier waits overlap the
+// other's MFMAs (one wave per SIMD leaves the MFMA pipe mostly idle).
+// Activation slices (KS of K for all 32 TM rows) stream into NBUF rotating
+// LDS buffers by direct loads, cooperatively, while each wave loads its own
+// weights (NG KiB per 32-K chunk, fragment-major) into registers, both P
+// slices ahead of the MFMAs; one barrier per slice frees the buffer slice
+// j + P lands in.
 // LDS slice layout: row r (one activation row, 2 KS bytes) holds its 16-byte
 // chunk c in slot c ^ (r % 16), so the 32-row operand reads (one chunk per
 // lane) hit distinct banks; the permutation is applied on the load side and
 // the direct loads write 1 KiB (1024 / (2 KS) rows) linearly per instruction.
-// With GAIN (an activation-side RMSNorm gain, p.k.gain): the workgroup's
-// gains (at most FP8_GAIN_K of them) are staged in LDS behind the slices;
-// once a wave's own direct loads of a slice have landed, each lane rescales
-// the 16-byte chunks it loaded (x -> bf16(x * g[k])) and adds their unscaled
-// squares to its rows' sums, before the barrier that publishes the slice.
-template <int TM, int NG, int KS, bool GAIN>  // 32-row tiles of M (M <= 32 TM); 32-column groups per wave; K per slice
-__global__ void __launch_bounds__(256, 2) gemm_fp8_lds_kernel(Fp8K p) {
+// An activation-side RMSNorm gain never reaches this kernel: the launcher
+// first scales the rows once (fp8_gain_prep_kernel) and hands over their sums
+// of squares (p.ss_pre), instead of every workgroup rescaling the same rows.
+template <int TM, int NG, int KS>  // 32-row tiles of M (M <= 32 TM); 32-column groups per wave; K per slice
+__global__ void __launch_bounds__(512) gemm_fp8_lds_kernel(Fp8K p) {
   constexpr int ROWS = 32 * TM;
   constexpr int RB = 2 * KS;           // bytes per activation row of a slice
   constexpr int SLB = ROWS * RB;       // bytes per activation slice
-  constexpr int NBUF = 3;
-  constexpr int ALD = SLB / 1024 / 4;  // activation loads per wave per slice
+  constexpr int NWV = 8;               // waves per workgroup: 4 column groups x 2 K halves
+  constexpr int NT = 64 * NWV;         // threads per workgroup
+  constexpr int P = 2;                 // slices in flight ahead of the MFMAs (measured best of 2, 3, 5)
+  constexpr int NBUF = P + 1;          // slice buffers (LDS) and weight register slots
+  constexpr int ALD = SLB / 1024 / NWV;  // activation loads per wave per slice
   constexpr int RPI = 1024 / RB;       // rows per activation load
   constexpr int LPR = RB / 16;         // lanes per row in an activation load
   constexpr int NCH = KS / 32;         // 32-K chunks per slice
-  constexpr int WLD = NCH * NG;        // weight loads per wave per slice
-  constexpr int PARTS = 256 / ROWS;    // threads per row in the sum of squares
+  constexpr int NCHH = NCH / 2;        // chunks per K half
+  constexpr int WLD = NCHH * NG;       // weight loads per wave per slice
+  constexpr int PARTS = NT / ROWS;     // threads per row in the sum of squares
   constexpr int CPP = LPR / PARTS;     // 16-byte chunks per such thread and slice
-  constexpr int GK = GAIN ? FP8_GAIN_K : 0;  // staged gains (fp32) behind the slice buffers
-  static_assert(!GAIN || (LPR == 16 && GK >= ROWS), "gain staging assumes 16 chunks per row");
-  __shared__ __attribute__((aligned(16))) char sa[NBUF * SLB + 4 * GK];
-  float* const gl = (float*)(sa + NBUF * SLB);
-  // LDS byte addresses for the gain path's accesses, which are written as
-  // inline ds_read / ds_write with their own lgkmcnt waits: the compiler
-  // cannot tell which slice bytes the in-flight direct loads write and would
-  // otherwise wait for all of them before every such access.
-  const uint32_t sa_lds = (uint32_t)(uintptr_t)(lds_ptr_t)sa;
+  static_assert(ALD >= 1 && NCH % 2 == 0 && CPP >= 1, "shape of the eight-wave pipeline");
+  __shared__ __attribute__((aligned(16))) char sa[NBUF * SLB];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int kh = wave >> 2, wc = wave & 3;  // K half, column group
   const int h = lane >> 5, c32 = lane & 31;
   const int split = blockIdx.y;
   const int64_t kb = (int64_t)split * p.ksplit;
   const int nsl = (int)((min(p.K, kb + p.ksplit) - kb) / KS);
   const int64_t nch = p.ldb / 32;
-  const int64_t g0 = ((int64_t)blockIdx.x * 4 + wave) * NG;  // first 32-row group of this wave
-  const uint8_t* bw = (const uint8_t*)p.B + (g0 * nch + kb / 32) * 1024 + 16 * lane;
+  const int64_t g0 = ((int64_t)blockIdx.x * 4 + wc) * NG;  // first 32-row group of this wave
+  const uint8_t* bw = (const uint8_t*)p.B + (g0 * nch + kb / 32 + kh * NCHH) * 1024 + 16 * lane;
   const char* abase = (const char*)p.A + kb * 2;
-  // row sums of squares: every workgroup when it finishes its tile itself,
-  // else the first column block of each split (for the reduce kernel)
-  const bool do_ss = p.k.sumsq && (p.fused || blockIdx.x == 0);
+  // row sums of squares (unless handed over): every workgroup when it
+  // finishes its tile itself, else the first column block of each split
+  const bool do_ss = p.k.sumsq && !p.ss_pre && (p.fused || blockIdx.x == 0);
 
   // activation load q of this wave fills slice rows RPI (ALD wave + q) + lane / LPR,
   // slot lane % LPR; rows past M re-read row M - 1 (their sums are dropped)
@@ -439,7 +446,7 @@ __global__ void __launch_bounds__(256, 2) gemm_fp8_lds_kernel(Fp8K p) {
     aoff[q] = (uint32_t)rr * (uint32_t)p.lda * 2u + (uint32_t)(((lane % LPR) ^ (r & 15)) << 4);
   }
 
-  uint4 wb[NBUF][NCH][NG];
+  uint4 wb[NBUF][NCHH][NG];
   f32x16_t acc[TM][NG];
 #pragma unroll
   for (int t = 0; t < TM; ++t)
@@ -448,23 +455,8 @@ __global__ void __launch_bounds__(256, 2) gemm_fp8_lds_kernel(Fp8K p) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[t][g][r] = 0.f;
   float ss = 0.f;
-  float ssq[GAIN ? ALD : 1];  // GAIN: unscaled squares of the rows this lane loads
-#pragma unroll
-  for (int q = 0; q < (GAIN ? ALD : 1); ++q) ssq[q] = 0.f;
-  // GAIN: this workgroup's gains, read into registers before the first
-  // slices are issued (their loads are the oldest, so the first step's wait
-  // covers them), written to LDS before the first barrier
-  f32x4_t greg[GAIN ? GK / 1024 : 1];
-  const int nk = nsl * KS;
-  if constexpr (GAIN) {
-#pragma unroll
-    for (int i = 0; i < GK / 1024; ++i) {
-      const int64_t at = min((int64_t)(1024 * i + 4 * tid), (int64_t)nk - 4);  // in bounds, kept only below nk
-      greg[i] = *(const f32x4_t*)(p.k.gain + kb + at);
-    }
-  }
 
-  // slice j goes to LDS buffer j % NBUF and weight slot j % NBUF
+  // slice j goes to LDS buffer j % NBUF and weight slot j % NBUF;
   // workgroups start their K walk at different slices (rotated), so the
   // weight streams of concurrent workgroups do not advance in lockstep
   const int rot = (int)((blockIdx.x * 5u) % (unsigned)nsl);
@@ -478,33 +470,44 @@ __global__ void __launch_bounds__(256, 2) gemm_fp8_lds_kernel(Fp8K p) {
       __builtin_amdgcn_global_load_lds((const void*)(asrc + aoff[q]), (lds_ptr_t)(ad + q * 1024), 16, 0, 0);
     const uint8_t* wsrc = bw + (int64_t)j * NCH * 1024;
 #pragma unroll
-    for (int c = 0; c < NCH; ++c)
+    for (int c = 0; c < NCHH; ++c)
 #pragma unroll
       for (int g = 0; g < NG; ++g) wb[SL][c][g] = *(const uint4*)(wsrc + ((int64_t)g * nch + c) * 1024);
   };
   auto compute = [&](auto slot) {
     constexpr int SL = decltype(slot)::value;
     const char* ab = sa + SL * SLB + c32 * RB;
+    // this wave's K half of the slice: chunks kh NCHH .. kh NCHH + NCHH - 1;
+    // every A fragment is read before the first MFMA
+    bf16x8_t a[NCHH][TM][2];
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) {
-      bf16x8_t a[TM][2];
+    for (int c = 0; c < NCHH; ++c)
 #pragma unroll
       for (int t = 0; t < TM; ++t) {
-        a[t][0] = *(const bf16x8_t*)(ab + t * 32 * RB + (((4 * c + 2 * h) ^ (c32 & 15)) << 4));
-        a[t][1] = *(const bf16x8_t*)(ab + t * 32 * RB + (((4 * c + 2 * h + 1) ^ (c32 & 15)) << 4));
+        const int cg = kh * NCHH + c;
+        a[c][t][0] = *(const bf16x8_t*)(ab + t * 32 * RB + (((4 * cg + 2 * h) ^ (c32 & 15)) << 4));
+        a[c][t][1] = *(const bf16x8_t*)(ab + t * 32 * RB + (((4 * cg + 2 * h + 1) ^ (c32 & 15)) << 4));
       }
+#pragma unroll
+    for (int c = 0; c < NCHH; ++c) {
 #pragma unroll
       for (int g = 0; g < NG; ++g) {
         const bf16x8_t b0 = fp8x8_to_bf16x8(wb[SL][c][g].x, wb[SL][c][g].y);
         const bf16x8_t b1 = fp8x8_to_bf16x8(wb[SL][c][g].z, wb[SL][c][g].w);
 #pragma unroll
         for (int t = 0; t < TM; ++t) {
-          acc[t][g] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[t][0], b0, acc[t][g], 0, 0, 0);
-          acc[t][g] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[t][1], b1, acc[t][g], 0, 0, 0);
+          acc[t][g] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[c][t][0], b0, acc[t][g], 0, 0, 0);
+          acc[t][g] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[c][t][1], b1, acc[t][g], 0, 0, 0);
         }
       }
     }
-    if (do_ss && !GAIN) {
+    // reads first, then the MFMAs (the scheduler would otherwise sink each
+    // read to its first use): at most 8 reads are outstanding for M <= 64
+    if constexpr (NCHH * TM * 2 <= 8) {
+      __builtin_amdgcn_sched_group_barrier(0x100, NCHH * TM * 2, 0);       // DS reads
+      __builtin_amdgcn_sched_group_barrier(0x008, NCHH * TM * 2 * NG, 0);  // MFMAs
+    }
+    if (do_ss) {
       const int row = tid / PARTS, part = tid % PARTS;
       const char* ar = sa + SL * SLB + row * RB;
 #pragma unroll
@@ -518,99 +521,52 @@ __global__ void __launch_bounds__(256, 2) gemm_fp8_lds_kernel(Fp8K p) {
       }
     }
   };
-  // GAIN: the chunks this lane loaded into slice buffer SL (rows RPI (ALD wave
-  // + q) + lane / LPR, source chunk (lane % LPR) ^ (row % 16)), rescaled in
-  // place; their unscaled squares go to ssq (rows past M are re-reads: dropped).
-  auto scale_own = [&](int j0, auto slot) {
-    constexpr int SL = decltype(slot)::value;
-    const int j = j0 + rot < nsl ? j0 + rot : j0 + rot - nsl;
-    const uint32_t ad = sa_lds + SL * SLB + ALD * wave * 1024 + lane * 16;
-#pragma unroll
-    for (int q = 0; q < ALD; ++q) {
-      const int r = RPI * (ALD * wave + q) + lane / LPR;
-      const int c = (lane % LPR) ^ (r & 15);
-      const uint32_t ga_at = sa_lds + NBUF * SLB + 4 * (j * KS + 8 * c);
-      u32x4_t v;
-      f32x4_t ga, gb;
-      asm volatile(
-          "ds_read_b128 %0, %3\n\t"
-          "ds_read_b128 %1, %4\n\t"
-          "ds_read_b128 %2, %4 offset:16\n\t"
-          "s_waitcnt lgkmcnt(0)"
-          : "=v"(v), "=v"(ga), "=v"(gb)
-          : "v"(ad + q * 1024), "v"(ga_at)
-          : "memory");
-      const float g[8] = {ga[0], ga[1], ga[2], ga[3], gb[0], gb[1], gb[2], gb[3]};
-      uint32_t w[4] = {v[0], v[1], v[2], v[3]};
-      float sq = 0.f;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float lo = __uint_as_float(w[e] << 16), hi = __uint_as_float(w[e] & 0xffff0000u);
-        sq += lo * lo + hi * hi;
-        const bf16x2_t pr = {(__bf16)(lo * g[2 * e]), (__bf16)(hi * g[2 * e + 1])};  // round to nearest even
-        w[e] = __builtin_bit_cast(uint32_t, pr);
-      }
-      if (r < p.M) ssq[q] += sq;
-      const u32x4_t o = {w[0], w[1], w[2], w[3]};
-      asm volatile("ds_write_b128 %0, %1" : : "v"(ad + q * 1024), "v"(o) : "memory");
-    }
-    // the rescaled chunks are written before the barrier publishes them
-    asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory");
-  };
   // Every step issues one slice (past the end: the last slice again, an L2
   // re-read into a buffer nobody reads), so the in-flight count is the same
   // at every wait and the compiler needs no waits of its own.
+  // A step past the last slice (j >= nsl, padding the last trip) waits and
+  // issues like the others but computes nothing: every trip is then the same
+  // straight-line code, and no conditional step makes the compiler drain all
+  // loads in flight at the loop's exit.
   auto step = [&](int j, auto slot) {
     constexpr int SL = decltype(slot)::value;
-    // slice j has landed (only slice j + 1 may still be in flight) and every
-    // wave is done with slice j - 1, whose buffer slice j + 2 reuses
-    wait_vmcnt<ALD + WLD>();
-    if constexpr (GAIN) scale_own(j, slot);
+    // slice j has landed (slices j + 1 .. j + P - 1 may still be in flight)
+    // and every wave is done with slice j - 1, whose buffer slice j + P reuses
+    wait_vmcnt<(P - 1) * (ALD + WLD)>();
     barrier_keep_loads();
-    issue(min(j + 2, nsl - 1), std::integral_constant<int, (SL + 2) % NBUF>());
-    compute(slot);
+    issue(min(j + P, nsl - 1), std::integral_constant<int, (SL + P) % NBUF>());
+    if (j < nsl) compute(slot);
   };
 
-  issue(0, std::integral_constant<int, 0>());
-  issue(min(1, nsl - 1), std::integral_constant<int, 1>());
-  if constexpr (GAIN) {
-    // the gain loads were issued before both slices: waiting for all but the
-    // slices' loads waits for them alone
-    wait_vmcnt<2 * (ALD + WLD)>();
-#pragma unroll
-    for (int i = 0; i < GK / 1024; ++i)
-      if (1024 * i + 4 * tid < nk)
-        asm volatile("ds_write_b128 %0, %1" : : "v"(sa_lds + NBUF * SLB + 4 * (1024 * i + 4 * tid)), "v"(greg[i])
-                     : "memory");
-    asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory");
-    barrier_keep_loads();  // every wave's gains are in LDS before any wave rescales with them
-  }
-  // whole trips of NBUF steps, then at most two more: no step of a trip is
-  // conditional, so the compiler sees one in-flight pattern at every wait
-  int j = 0;
-  for (; j + NBUF <= nsl; j += NBUF) {
-    step(j, std::integral_constant<int, 0>());
-    step(j + 1, std::integral_constant<int, 1>());
-    step(j + 2, std::integral_constant<int, 2>());
-  }
-  if (j < nsl) step(j, std::integral_constant<int, 0>());
-  if (j + 1 < nsl) step(j + 1, std::integral_constant<int, 1>());
+  unroll_seq(std::make_integer_sequence<int, P>(), [&](auto s) { issue(min((int)s, nsl - 1), s); });
+  // whole trips of NBUF steps (the last one padded): one in-flight pattern at every wait
+  for (int j = 0; j < nsl; j += NBUF)
+    unroll_seq(std::make_integer_sequence<int, NBUF>(), [&](auto s) { step(j + (int)s, s); });
   wait_vmcnt<0>();  // no direct-to-LDS load may land after the workgroup ends
 
-  if constexpr (GAIN) {
-    // every wave is past the last barrier, so nobody reads the staged gains
-    // any more: their space collects the row sums, handed to thread PARTS row
-    if (do_ss) {
+  // the two K halves meet: waves 4..7 hand their sums to waves 0..3 through
+  // the (now free) slice buffers, in a fixed order (half 0 + half 1)
+  static_assert(4 * TM * NG * 16 * 64 * 4 <= NBUF * SLB, "half sums fit the slice buffers");
+  {
+    float* xs = (float*)sa;
+    __syncthreads();  // every wave is done reading the slice buffers
+    if (kh == 1) {
 #pragma unroll
-      for (int q = 0; q < ALD; ++q) {
-        float v = ssq[q];
+      for (int t = 0; t < TM; ++t)
 #pragma unroll
-        for (int o = 1; o < LPR; o <<= 1) v += __shfl_xor(v, o);
-        if (lane % LPR == 0) gl[RPI * (ALD * wave + q) + lane / LPR] = v;
-      }
+        for (int g = 0; g < NG; ++g)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) xs[(((wc * TM + t) * NG + g) * 16 + r) * 64 + lane] = acc[t][g][r];
     }
     __syncthreads();
-    ss = (do_ss && tid % PARTS == 0) ? gl[tid / PARTS] : 0.f;
+    if (kh == 0) {
+#pragma unroll
+      for (int t = 0; t < TM; ++t)
+#pragma unroll
+        for (int g = 0; g < NG; ++g)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[t][g][r] += xs[(((wc * TM + t) * NG + g) * 16 + r) * 64 + lane];
+    }
   }
   if (do_ss) {
 #pragma unroll
@@ -618,17 +574,19 @@ __global__ void __launch_bounds__(256, 2) gemm_fp8_lds_kernel(Fp8K p) {
   }
   if (!p.fused) {
     float* part = p.part + (int64_t)split * p.M * p.Npk;
+    if (kh == 0) {
 #pragma unroll
-    for (int t = 0; t < TM; ++t)
+      for (int t = 0; t < TM; ++t)
 #pragma unroll
-      for (int g = 0; g < NG; ++g) {
-        const int64_t col = (g0 + g) * 32 + c32;
+        for (int g = 0; g < NG; ++g) {
+          const int64_t col = (g0 + g) * 32 + c32;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int m = 32 * t + 8 * (r >> 2) + 4 * h + (r & 3);
-          if (m < p.M) part[(int64_t)m * p.Npk + col] = acc[t][g][r];
+          for (int r = 0; r < 16; ++r) {
+            const int m = 32 * t + 8 * (r >> 2) + 4 * h + (r & 3);
+            if (m < p.M) part[(int64_t)m * p.Npk + col] = acc[t][g][r];
+          }
         }
-      }
+    }
     const int row = tid / PARTS;
     if (do_ss && tid % PARTS == 0 && row < p.M) p.sumsq_part[(int64_t)split * p.M + row] = ss;
     return;
@@ -644,31 +602,87 @@ __global__ void __launch_bounds__(256, 2) gemm_fp8_lds_kernel(Fp8K p) {
   float* rrs = tl + ROWS * LDT;
   float* scl = rrs + ROWS;  // the tile's 128 NG per-column scales, packed-column order
   __syncthreads();
-  for (int c = tid; c < 128 * NG; c += 256) {
+  for (int c = tid; c < 128 * NG; c += NT) {
     const int i = c / (int)p.bn, j = c - i * (int)p.bn;
     const int64_t n = (int64_t)blockIdx.x * p.bn + j;
     scl[c] = n < p.N ? p.scale[(int64_t)i * p.N + n] : 0.f;
   }
+  if (kh == 0) {
 #pragma unroll
-  for (int t = 0; t < TM; ++t)
+    for (int t = 0; t < TM; ++t)
 #pragma unroll
-    for (int g = 0; g < NG; ++g)
+      for (int g = 0; g < NG; ++g)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int m = 32 * t + 8 * (r >> 2) + 4 * h + (r & 3);
-        tl[m * LDT + (wave * NG + g) * 32 + c32] = acc[t][g][r];
-      }
+        for (int r = 0; r < 16; ++r) {
+          const int m = 32 * t + 8 * (r >> 2) + 4 * h + (r & 3);
+          tl[m * LDT + (wc * NG + g) * 32 + c32] = acc[t][g][r];
+        }
+  }
   if (tid % PARTS == 0 && tid / PARTS < p.M) {
     const int row = tid / PARTS;
     float rr = 1.f;
     if (p.k.sumsq) {
-      rr = rsqrtf(ss * p.k.inv_k + p.k.eps);
-      if (p.k.sumsq_out && blockIdx.x == 0) p.k.sumsq_out[row] = ss;
+      const float s = p.ss_pre ? p.sumsq_part[row] : ss;
+      rr = rsqrtf(s * p.k.inv_k + p.k.eps);
+      if (p.k.sumsq_out && blockIdx.x == 0) p.k.sumsq_out[row] = s;
     }
     rrs[row] = rr;
   }
   __syncthreads();
-  fp8_tile_out(p, (int)blockIdx.x, tid, tl, LDT, scl, rrs);
+  fp8_tile_out(p, (int)blockIdx.x, tid, NT, tl, LDT, scl, rrs);
+}
+
+// The activation-side RMSNorm gain, once per call: row m of the operand
+// becomes bf16(x[m, k] * g[k]) (fp32 product, round to nearest even) and the
+// row's sum of squares (of the unscaled x) goes to split 0's sum slot, the
+// other splits' slots to zero, where the kernels and the reduce pass read the
+// sums. One workgroup per row; a thread takes 8-element chunks 8 (tid + 256 u),
+// u < U, of each 8192-wide span, all of whose loads are issued before the
+// first is used (one memory round trip per span). K a multiple of 8, rows
+// 16-byte aligned.
+template <int U>
+__global__ void __launch_bounds__(256) fp8_gain_prep_kernel(const uint16_t* x, int64_t lda, const float* g, int64_t K,
+                                                            uint16_t* xg, float* ss, int64_t M, int splits) {
+  __shared__ float red[4];
+  const int64_t m = blockIdx.x;
+  const int tid = threadIdx.x;
+  const uint16_t* xr = x + m * lda;
+  uint16_t* yr = xg + m * K;
+  float acc = 0.f;
+  for (int64_t k0 = 0; k0 < K; k0 += 8 * 256 * U) {
+    u32x4_t v[U];
+    f32x4_t ga[U], gb[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t k = k0 + 8 * (tid + 256 * u);
+      if (k < K) {
+        v[u] = *(const u32x4_t*)(xr + k);
+        ga[u] = *(const f32x4_t*)(g + k);
+        gb[u] = *(const f32x4_t*)(g + k + 4);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t k = k0 + 8 * (tid + 256 * u);
+      if (k >= K) continue;
+      const float gg[8] = {ga[u][0], ga[u][1], ga[u][2], ga[u][3], gb[u][0], gb[u][1], gb[u][2], gb[u][3]};
+      u32x4_t o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float lo = __uint_as_float(v[u][e] << 16), hi = __uint_as_float(v[u][e] & 0xffff0000u);
+        acc += lo * lo + hi * hi;
+        const bf16x2_t pr = {(__bf16)(lo * gg[2 * e]), (__bf16)(hi * gg[2 * e + 1])};
+        o[e] = __builtin_bit_cast(uint32_t, pr);
+      }
+      *(u32x4_t*)(yr + k) = o;
+    }
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
+  if ((tid & 63) == 0) red[tid >> 6] = acc;
+  __syncthreads();
+  if (tid == 0) ss[m] = (red[0] + red[1]) + (red[2] + red[3]);
+  for (int s = 1 + tid; s < splits; s += 256) ss[(int64_t)s * M + m] = 0.f;
 }
 
 // acc_i(m, n) from the partials, scaled: s_i[n] * sum over splits.
@@ -746,14 +760,11 @@ static bool fp8_lds_ok(int64_t Npk, int64_t K, int bn, int n_acc) {
 
 static int fp8_lds_splits(int64_t Npk, int64_t K) {
   const int64_t nsl = K / 128;
-  // a split covers at most FP8_GAIN_K of K (the gain staging's capacity)
-  const int64_t smin = cdiv(K, FP8_GAIN_K);
   const int64_t cus = device_cus() > 0 ? device_cus() : 256;
   const int64_t nb = Npk / 128;
-  if (4 * nb >= 3 * cus) return (int)smin;
+  if (4 * nb >= 3 * cus) return 1;
   // as many splits as keep the launch within one round of one workgroup per CU
-  const int64_t s = std::min(std::max((int64_t)1, cus / nb), std::min(nsl, (int64_t)16));
-  return (int)std::max(smin, s);
+  return (int)std::min(std::max((int64_t)1, cus / nb), std::min(nsl, (int64_t)16));
 }
 
 static int fp8_splits(int64_t Npk, int64_t K) {
@@ -764,9 +775,15 @@ static int fp8_splits(int64_t Npk, int64_t K) {
   return (int)std::max((int64_t)1, std::min(s, (int64_t)64));
 }
 
+// Workspace: [splits][M][Npk] partial sums, [splits][M] partial row sums of
+// squares, then (shared-activation kernel) the gain-scaled operand bf16 [M][K],
+// 256-byte aligned.
+static int64_t fp8_gain_offset(int64_t M, int64_t Npk, int s) { return cdiv((int64_t)s * M * (Npk + 1) * 4, 256) * 256; }
+
 int64_t fp8_workspace_bytes(int64_t M, int64_t Npk, int64_t K, int bn, int n_acc) {
-  const int64_t s = fp8_lds_ok(Npk, K, bn, n_acc) ? fp8_lds_splits(Npk, K) : fp8_splits(Npk, K);
-  return s * M * (Npk + 1) * 4;
+  if (!fp8_lds_ok(Npk, K, bn, n_acc)) return (int64_t)fp8_splits(Npk, K) * M * (Npk + 1) * 4;
+  const int s = fp8_lds_splits(Npk, K);
+  return fp8_gain_offset(M, Npk, s) + M * K * 2;
 }
 
 int launch_gemm_fp8(const GemmK& k, int64_t Npk, const float* scale, float* ws, int64_t ws_bytes,
@@ -787,13 +804,27 @@ int launch_gemm_fp8(const GemmK& k, int64_t Npk, const float* scale, float* ws, 
   p.splits = lds ? fp8_lds_splits(Npk, k.K) : fp8_splits(Npk, k.K);
   p.ksplit = cdiv(cdiv(k.K, p.splits), 128) * 128;  // whole slices / four waves x a multiple of 32
   p.splits = (int)cdiv(k.K, p.ksplit);
-  const int64_t need = (int64_t)p.splits * k.M * (Npk + 1) * 4;
+  const int64_t need = lds ? fp8_gain_offset(k.M, Npk, p.splits) + k.M * k.K * 2
+                           : (int64_t)p.splits * k.M * (Npk + 1) * 4;
   TH_CHECK_ARG(ws && ws_bytes >= need, "th_gemm: fp8 weights need a workspace of %lld bytes (got %lld)",
                (long long)need, (long long)ws_bytes);
   p.part = ws;
   p.sumsq_part = k.sumsq ? ws + (int64_t)p.splits * k.M * Npk : nullptr;
   if (lds) {
     TH_CHECK_ARG(k.lda < (1 << 24), "th_gemm: fp8 lhs row stride must be under 2^24 elements");
+    if (k.gain) {
+      // the gain-scaled rows and their (unscaled) sums of squares, once
+      TH_CHECK_ARG(k.sumsq, "th_gemm: lhs_gain needs the row sum of squares (sumsq)");
+      TH_CHECK_ARG(k.lda % 8 == 0 && ((uintptr_t)k.A & 15) == 0,
+                   "th_gemm: lhs_gain needs 16-byte aligned lhs rows");
+      uint16_t* xg = (uint16_t*)((char*)ws + fp8_gain_offset(k.M, Npk, p.splits));
+      hipLaunchKernelGGL(fp8_gain_prep_kernel<4>, dim3((unsigned)k.M), dim3(256), 0, stream, (const uint16_t*)k.A,
+                         k.lda, k.gain, k.K, xg, p.sumsq_part, k.M, p.splits);
+      TH_CHECK_LAUNCH();
+      p.A = xg;
+      p.lda = k.K;
+      p.ss_pre = 1;
+    }
     // 4-column output groups: inside one tile and one RoPE half-head
     bool vec = k.N % 4 == 0 && (k.bn & (k.bn - 1)) == 0;
     for (int o = 0; o < k.n_out; ++o) {
@@ -806,23 +837,12 @@ int launch_gemm_fp8(const GemmK& k, int64_t Npk, const float* scale, float* ws, 
       if (k.out[o].op == TH_EPI_ROPE && k.bn % k.hd != 0) local = false;
     p.fused = local ? 1 : 0;
     const dim3 g1((unsigned)(Npk / 128), (unsigned)p.splits);
-    // (128-wide slices measured as fast as or faster than 256-wide ones at the
-    // Llama-3-8B decode shapes, so only they are instantiated)
-    if (k.gain) {
-      if (k.M <= 32)
-        hipLaunchKernelGGL((gemm_fp8_lds_kernel<1, 1, 128, true>), g1, dim3(256), 0, stream, p);
-      else if (k.M <= 64)
-        hipLaunchKernelGGL((gemm_fp8_lds_kernel<2, 1, 128, true>), g1, dim3(256), 0, stream, p);
-      else
-        hipLaunchKernelGGL((gemm_fp8_lds_kernel<4, 1, 128, true>), g1, dim3(256), 0, stream, p);
-    } else {
-      if (k.M <= 32)
-        hipLaunchKernelGGL((gemm_fp8_lds_kernel<1, 1, 128, false>), g1, dim3(256), 0, stream, p);
-      else if (k.M <= 64)
-        hipLaunchKernelGGL((gemm_fp8_lds_kernel<2, 1, 128, false>), g1, dim3(256), 0, stream, p);
-      else
-        hipLaunchKernelGGL((gemm_fp8_lds_kernel<4, 1, 128, false>), g1, dim3(256), 0, stream, p);
-    }
+    if (k.M <= 32)
+      hipLaunchKernelGGL((gemm_fp8_lds_kernel<1, 1, 128>), g1, dim3(512), 0, stream, p);
+    else if (k.M <= 64)
+      hipLaunchKernelGGL((gemm_fp8_lds_kernel<2, 1, 128>), g1, dim3(512), 0, stream, p);
+    else
+      hipLaunchKernelGGL((gemm_fp8_lds_kernel<4, 1, 128>), g1, dim3(512), 0, stream, p);
     TH_CHECK_LAUNCH();
     if (!p.fused) {
       if (vec)

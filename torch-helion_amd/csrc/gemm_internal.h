@@ -54,6 +54,7 @@ struct Fp8K {
   float* part;       // [splits][M][Npk]
   float* sumsq_part; // [splits][M]
   int fused;         // one split finishing its tiles in the main kernel (no reduce pass)
+  int ss_pre;        // row sums of squares already in sumsq_part (split 0; the others zero)
 };
 
 // 4 consecutive elements (one 8-byte bf16 / 16-byte fp32 access when vec,

@@ -471,7 +471,8 @@ class DeviceProgram:
                 if i >= 0 and i not in used:
                     used.append(i)
         used.sort()
-        if any(op == abi.EPI_ROPE for _, op, *_ in outs):
+        if any(op == abi.EPI_ROPE for _, op, *_ in outs) and not fp8:
+            # (e4m3 products rotate in the split reduction, which reads any column)
             bn = abi.load().th_gemm_acc_tile(N, min(len(used), abi.MAX_ACC), ops.th_dtype(in_dtype))
             hd = next(iter(rope_tables.values()))[3]
             if bn % hd:
