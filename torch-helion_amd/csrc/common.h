@@ -70,7 +70,9 @@ __device__ __forceinline__ void store_elem(void* p, int64_t i, int dtype, float 
     ((float*)p)[i] = v;
 }
 
-__device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + __expf(-x)); }
+// 1 / (1 + e^-x) with the hardware reciprocal (v_rcp_f32, 1 ulp) instead of an
+// IEEE division sequence: these run once per output element of GEMM epilogues
+__device__ __forceinline__ float sigmoidf_(float x) { return __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
 // log(1 + exp(x)) without a large-x guard: the OpIR softplus rewrite drops
 // torch's threshold, so this is the value the program defines.
 __device__ __forceinline__ float softplusf_(float x) { return __logf(1.f + __expf(x)); }
