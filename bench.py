@@ -265,15 +265,17 @@ def bench_decode_c5(args) -> dict:
         blk.replay()
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
-    # cold: a 512 MiB write before each timed replay evicts the 256 MiB last-level cache
-    flush = torch.empty(512 << 20, dtype=torch.uint8, device=dev)
+    # cold: a 512 MiB read before each timed replay evicts the 256 MiB last-level cache. A read,
+    # not a write: written lines would still be dirty when the replay starts, and their
+    # write-back (about 50 us at this size) would be timed as part of the step.
+    flush = torch.ones(64 << 20, dtype=torch.int64, device=dev)
     timed = {}
     for mode in ("warm", "cold"):
         starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
         ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
         for i in range(args.steps):
             if mode == "cold":
-                flush.fill_(i & 0xff)
+                flush.sum()
             starts[i].record(stream)
             blk.replay()
             ends[i].record(stream)

@@ -1,6 +1,7 @@
 """Summarise a ``rocprofv3 --kernel-trace`` database (rocpd SQLite output).
 
-    python -m torch_helion.hip.rocprof_summary RESULTS.db [--period P --reps R --labels k0,k1,... --match th::]
+    python -m torch_helion.hip.rocprof_summary RESULTS.db [--period P --reps R --labels k0,k1,... --match th::
+                                                           --skip N]
 
 Prints a markdown table of every kernel symbol (calls, average / total time,
 share of the traced kernel time). Several program kernels can share one
@@ -11,7 +12,9 @@ the per-kernel timing pass of ``torch_helion.hip.bench.bench_program`` ends
 every workload with exactly such repetitions of the program's launch list.
 Only dispatches whose symbol contains ``--match`` (default ``th::``, this
 library's kernels) enter the sequence view, so host copies and torch fills
-after the timed region do not shift it.
+after the timed region do not shift it. ``--skip N`` drops the last N of those
+matched dispatches first, so the window can end before a later leg of the same
+run (another launch list timed after the one of interest).
 """
 
 from __future__ import annotations
@@ -64,13 +67,16 @@ def main(argv=None) -> int:
     ap.add_argument("--reps", type=int, default=0)
     ap.add_argument("--labels", default="")
     ap.add_argument("--match", default="th::")
+    ap.add_argument("--skip", type=int, default=0)
     a = ap.parse_args(argv)
     rows = load(a.db)
     print(f"{len(rows)} kernel dispatches, {sum(e - s for _, s, e, _ in rows) / 1e6:.3f} ms of kernel time\n")
     print(table(rows))
     if a.period and a.reps:
-        print(f"\nlast {a.reps} repetitions of the {a.period}-launch sequence:\n")
+        skip = f" ending {a.skip} matched dispatches before the last" if a.skip else ""
+        print(f"\nlast {a.reps} repetitions of the {a.period}-launch sequence{skip}:\n")
         seq = [r for r in rows if a.match in r[0]]
+        seq = seq[:len(seq) - a.skip] if a.skip else seq
         print(sequence(seq, a.period, a.reps, a.labels.split(",") if a.labels else None))
     return 0
 
