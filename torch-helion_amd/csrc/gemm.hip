@@ -109,9 +109,9 @@ __device__ __forceinline__ void store8(void* p, int64_t off, int dtype, bool vec
 // the slice (extra rows, RoPE table rows) is loaded before the first use.
 // aoff / boff: slice columns where the op's accumulators a / b start.
 template <int OP, bool SUMSQ>
-__device__ __forceinline__ void epi_pair(const GemmK& p, const EpiOutK& eo, const float* wsl, int ws, int aoff,
-                                         int boff, const float* rsrow, int64_t row0, int64_t col_w, int r_l, int c8,
-                                         int np, int rp, int p0) {
+__device__ __forceinline__ void epi_pair(const GemmK& p, const EpiOutK& eo, int o2, const float* wsl,
+                                         int ws, int aoff, int boff, const float* rsrow, int64_t row0, int64_t col_w,
+                                         int r_l, int c8, int np, int rp, int p0) {
   constexpr bool USES_E = OP == TH_EPI_ADD || OP == TH_EPI_SOFTPLUS_ADD || OP == TH_EPI_MUL;
   constexpr bool USES_T = OP == TH_EPI_ROPE || OP == TH_EPI_ROPE_PAIR;
   const int ia = eo.a, ib = eo.b;
@@ -202,17 +202,31 @@ __device__ __forceinline__ void epi_pair(const GemmK& p, const EpiOutK& eo, cons
       }
     }
     store8(eo.ptr, gm * eo.ld + gc, eo.dtype, eo.vec8 != 0, valid, v);
+    if (o2 >= 0) {
+      const EpiOutK& e2 = p.out[o2];
+      store8(e2.ptr, gm * e2.ld + gc, e2.dtype, e2.vec8 != 0, valid, v);
+    }
   }
 }
 
+// o2 (or -1): the index of a second output with the same values (the fp32
+// copy of a bf16 output), stored from the same registers. (An index, not a
+// pointer: taking the address of a kernel-argument field would copy the
+// whole argument block to scratch memory.)
 template <int OP, bool SUMSQ>
-__device__ __forceinline__ void epi_slice(const GemmK& p, const EpiOutK& eo, const float* wsl, int ws, int aoff,
-                                          int boff, const float* rsrow, int64_t row0, int64_t col_w, int r_l, int c8,
-                                          int np, int rp) {
+__device__ __forceinline__ void epi_slice(const GemmK& p, const EpiOutK& eo, int o2, const float* wsl,
+                                          int ws, int aoff, int boff, const float* rsrow, int64_t row0, int64_t col_w,
+                                          int r_l, int c8, int np, int rp) {
   // two passes at a time: their global operands load together, and at most 2 x 16
   // of them are live (np = 4 with all loaded up front spilled the 8-wave kernel)
-  epi_pair<OP, SUMSQ>(p, eo, wsl, ws, aoff, boff, rsrow, row0, col_w, r_l, c8, np, rp, 0);
-  if (np > 2) epi_pair<OP, SUMSQ>(p, eo, wsl, ws, aoff, boff, rsrow, row0, col_w, r_l, c8, np, rp, 2);
+  epi_pair<OP, SUMSQ>(p, eo, o2, wsl, ws, aoff, boff, rsrow, row0, col_w, r_l, c8, np, rp, 0);
+  if (np > 2) epi_pair<OP, SUMSQ>(p, eo, o2, wsl, ws, aoff, boff, rsrow, row0, col_w, r_l, c8, np, rp, 2);
+}
+
+// Outputs o and o + 1 compute the same values (same op, operands and column
+// window; only the destination differs).
+__device__ __forceinline__ bool same_values(const EpiOutK& x, const EpiOutK& y) {
+  return x.op == y.op && x.a == y.a && x.b == y.b && x.e == y.e && x.cb == y.cb && x.ce == y.ce;
 }
 
 // Evaluate every output op for the `rows` slab rows staged in LDS.
@@ -734,11 +748,14 @@ __global__ void __launch_bounds__(64 * NW, 1) gemm_bf16_pk_kernel(GemmK p) {
   // slot is c ^ g(R) with g(R) = (R & 7) ^ ((R >> 3) & 1) = (lane >> 3) ^ (wave & 1).
   const int lrow = lane >> 3;
   const uint32_t chunk = (uint32_t)(((lane & 7) ^ lrow ^ (wave & 1)) << 4);
-  uint32_t voa[LA], vob[LB];
+  // rhs load i reads rows LR i + 8 wave + lane / 8: a uniform step of LR rows
+  // per load on top of one per-lane offset (the packed rhs is padded to whole
+  // column tiles, so no row needs clamping)
+  uint32_t voa[LA];
 #pragma unroll
   for (int i = 0; i < LA; ++i) voa[i] = (uint32_t)((LR * i + 8 * wave + lrow) * p.lda * 2) + chunk;
-#pragma unroll
-  for (int i = 0; i < LB; ++i) vob[i] = (uint32_t)((LR * i + 8 * wave + lrow) * p.ldb * 2) + chunk;
+  const uint32_t vob0 = (uint32_t)((8 * wave + lrow) * p.ldb * 2) + chunk;
+  const int64_t bstep = (int64_t)LR * p.ldb * 2;
 
   // Operand rows of tile L: uniform base pointers (lhs rows m0.., rhs rows
   // tn*BNC..) plus the per-lane 32-bit offsets above. lhs rows past M re-read
@@ -756,15 +773,26 @@ __global__ void __launch_bounds__(64 * NW, 1) gemm_bf16_pk_kernel(GemmK p) {
   // Load i of K tile kt into stage st: i < LA fills lhs rows, the rest rhs
   // rows. global_load_lds: a wave issues these about 1.5x as fast as the
   // buffer-descriptor form.
+  // Every address is a uniform base (tile, K tile and, for the rhs, the load's
+  // row step) plus a 32-bit per-lane offset, which selects the load form with
+  // an SGPR base; the empty asm keeps the offset's zero extension next to its
+  // load, so the compiler does not hoist 64-bit per-lane addresses (two
+  // registers per load) out of the K loop.
   auto issue_one = [&](const char* ga, const char* gb, int kt, int st, int i) {
     char* sa = smem + st * STAGE;
     const int64_t kofs = (int64_t)kt * 128;
-    if (i < LA)
-      __builtin_amdgcn_global_load_lds((const void*)(ga + kofs + voa[i < LA ? i : 0]),
-                                       (lds_ptr_t)(sa + (NW * i + wave) * 1024), 16, 0, 0);
-    else
-      __builtin_amdgcn_global_load_lds((const void*)(gb + kofs + vob[i >= LA ? i - LA : 0]),
-                                       (lds_ptr_t)(sa + BM * 128 + (NW * (i - LA) + wave) * 1024), 16, 0, 0);
+    if (i < LA) {
+      uint32_t o = voa[i < LA ? i : 0];
+      asm volatile("" : "+v"(o));
+      __builtin_amdgcn_global_load_lds((const void*)(ga + kofs + o), (lds_ptr_t)(sa + (NW * i + wave) * 1024), 16,
+                                       0, 0);
+    } else {
+      uint32_t o = vob0;
+      asm volatile("" : "+v"(o));
+      const char* gbi = gb + kofs + (int64_t)(i >= LA ? i - LA : 0) * bstep;
+      __builtin_amdgcn_global_load_lds((const void*)(gbi + o), (lds_ptr_t)(sa + BM * 128 + (NW * (i - LA) + wave) * 1024),
+                                       16, 0, 0);
+    }
   };
   auto issue_tile = [&](const char* ga, const char* gb, int kt, int st) {
 #pragma unroll
@@ -958,11 +986,14 @@ __global__ void __launch_bounds__(64 * NW, 1) gemm_bf16_pk_kernel(GemmK p) {
         const int np = 1 << (q8log - 2), rp = 64 >> q8log;
         for (int o = 0; o < p.n_out; ++o) {
           const EpiOutK& eo = p.out[o];
+          // an fp32 copy right after its bf16 output is stored from the same values
+          const int o2 = o + 1 < p.n_out && same_values(eo, p.out[o + 1]) ? o + 1 : -1;
+          if (o2 >= 0) ++o;
           if (ASPLIT && eo.a != wn) continue;
           if (eo.ce <= col_w || eo.cb >= col_w + wcols) continue;  // the window misses this wave's columns
           const int aoff = ASPLIT ? 0 : eo.a * hbn, boff = ASPLIT ? 0 : eo.b * hbn;
 #define TH_EPI_CASE(OP_) \
-  case OP_: epi_slice<OP_, SUMSQ>(p, eo, wsl, WS, aoff, boff, rsrow, row0, col_w, r_l, c8, np, rp); break
+  case OP_: epi_slice<OP_, SUMSQ>(p, eo, o2, wsl, WS, aoff, boff, rsrow, row0, col_w, r_l, c8, np, rp); break
           switch (eo.op) {
             TH_EPI_CASE(TH_EPI_ACC);
             TH_EPI_CASE(TH_EPI_ROPE);
@@ -971,7 +1002,7 @@ __global__ void __launch_bounds__(64 * NW, 1) gemm_bf16_pk_kernel(GemmK p) {
             TH_EPI_CASE(TH_EPI_SWIGLU);
             TH_EPI_CASE(TH_EPI_ADD);
             TH_EPI_CASE(TH_EPI_SOFTPLUS_ADD);
-            default: epi_slice<TH_EPI_MUL, SUMSQ>(p, eo, wsl, WS, aoff, boff, rsrow, row0, col_w, r_l, c8, np, rp); break;
+            default: epi_slice<TH_EPI_MUL, SUMSQ>(p, eo, o2, wsl, WS, aoff, boff, rsrow, row0, col_w, r_l, c8, np, rp); break;
           }
 #undef TH_EPI_CASE
         }
