@@ -32,6 +32,21 @@ __device__ __forceinline__ void wait_lgkmcnt0() {
   __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4));
 }
 
+// Direct-to-LDS load of 16 bytes per lane (global_load_lds_dwordx4): lane l's
+// 16 bytes at base + voff land at LDS byte address lds + 16 l; base and lds
+// are wave-uniform. Inline assembly rather than __builtin_amdgcn_global_load_lds:
+// the compiler counts the builtin's LDS write among the LDS operations its own
+// waits cover, so each wait it inserts for an ordinary LDS read turns into a
+// wait for all of them (lgkmcnt(0)), exposing the latency of fragment reads
+// issued a step ahead of their MFMAs. The compiler does not track this load:
+// the caller waits for it (wait_vmcnt) before anything reads its destination
+// and before the workgroup ends.
+__device__ __forceinline__ void dma_load16(const void* base, uint32_t voff, uint32_t lds) {
+  // (one wait state between the M0 write and the load that reads it)
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "s"(lds)
+               : "memory", "m0");
+}
+
 // Workgroup barrier that leaves global loads in flight (__syncthreads, and
 // even an LDS-only workgroup fence once direct-to-LDS loads are pending,
 // drain all of them). The wavefront-scope fences only keep the compiler from

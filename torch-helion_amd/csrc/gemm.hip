@@ -774,25 +774,17 @@ __global__ void __launch_bounds__(64 * NW, 1) gemm_bf16_pk_kernel(GemmK p) {
   // rows. global_load_lds: a wave issues these about 1.5x as fast as the
   // buffer-descriptor form.
   // Every address is a uniform base (tile, K tile and, for the rhs, the load's
-  // row step) plus a 32-bit per-lane offset, which selects the load form with
-  // an SGPR base; the empty asm keeps the offset's zero extension next to its
-  // load, so the compiler does not hoist 64-bit per-lane addresses (two
-  // registers per load) out of the K loop.
+  // row step; SGPRs) plus a 32-bit per-lane offset (dma_load16: the compiler
+  // neither tracks these loads nor lets them turn its LDS-read waits into
+  // waits for every read; the explicit waits below cover them).
+  const uint32_t lds0 = (uint32_t)(uintptr_t)smem;
   auto issue_one = [&](const char* ga, const char* gb, int kt, int st, int i) {
-    char* sa = smem + st * STAGE;
+    const uint32_t sa = lds0 + st * STAGE;
     const int64_t kofs = (int64_t)kt * 128;
-    if (i < LA) {
-      uint32_t o = voa[i < LA ? i : 0];
-      asm volatile("" : "+v"(o));
-      __builtin_amdgcn_global_load_lds((const void*)(ga + kofs + o), (lds_ptr_t)(sa + (NW * i + wave) * 1024), 16,
-                                       0, 0);
-    } else {
-      uint32_t o = vob0;
-      asm volatile("" : "+v"(o));
-      const char* gbi = gb + kofs + (int64_t)(i >= LA ? i - LA : 0) * bstep;
-      __builtin_amdgcn_global_load_lds((const void*)(gbi + o), (lds_ptr_t)(sa + BM * 128 + (NW * (i - LA) + wave) * 1024),
-                                       16, 0, 0);
-    }
+    if (i < LA)
+      dma_load16(ga + kofs, voa[i < LA ? i : 0], sa + (NW * i + wave) * 1024);
+    else
+      dma_load16(gb + kofs + (int64_t)(i >= LA ? i - LA : 0) * bstep, vob0, sa + BM * 128 + (NW * (i - LA) + wave) * 1024);
   };
   auto issue_tile = [&](const char* ga, const char* gb, int kt, int st) {
 #pragma unroll
@@ -931,7 +923,10 @@ __global__ void __launch_bounds__(64 * NW, 1) gemm_bf16_pk_kernel(GemmK p) {
       }
     }
 
-    // Every wave is done with both stages; start the next tile's first K tile.
+    // Every wave is done with both stages (and its last loads, re-fetches into
+    // the stage the epilogue slices overlay, have landed); start the next
+    // tile's first K tile.
+    wait_vmcnt<0>();
     __syncthreads();
     const int Ln = L + (int)gridDim.x;
     const bool more = Ln < tiles;
@@ -1022,6 +1017,7 @@ __global__ void __launch_bounds__(64 * NW, 1) gemm_bf16_pk_kernel(GemmK p) {
     rsa = rsan;
     rsb = rsbn;
   }
+  wait_vmcnt<0>();  // no direct-to-LDS load may land after the workgroup ends
 #endif
 }
 
