@@ -123,28 +123,31 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_bf16_kernel(AttnK p) {
     kro[i] = (uint32_t)row * (uint32_t)p.ldk * 2u + (uint32_t)((slot ^ (row % KCH)) << 4);
     vro[i] = (uint32_t)row * (uint32_t)p.ldv * 2u + (uint32_t)((slot ^ vsw(row)) << 4);
   }
+  // (dma_load16: the compiler does not count these loads among the LDS
+  // operations its read waits cover; the full wait at the top of every tile
+  // covers them)
+  const uint32_t lds0 = (uint32_t)(uintptr_t)smem;
   auto issue = [&](int it, int st) {
     const int k0 = it * BKV;
-    char* sk = smem + st * STAGE;
+    const uint32_t sk = lds0 + st * STAGE;
+    const char* kb = kbase + (int64_t)k0 * p.ldk * 2;
+    const char* vb = vbase + (int64_t)k0 * p.ldv * 2;
     if (k0 + BKV <= p.Skv) {
-      const char* kb = kbase + (int64_t)k0 * p.ldk * 2;
-      const char* vb = vbase + (int64_t)k0 * p.ldv * 2;
 #pragma unroll
       for (int i = 0; i < NLOAD; ++i) {
         const int n = NLOAD * wave + i;
-        __builtin_amdgcn_global_load_lds((const void*)(kb + kro[i]), (lds_ptr_t)(sk + n * 1024), 16, 0, 0);
-        __builtin_amdgcn_global_load_lds((const void*)(vb + vro[i]), (lds_ptr_t)(sk + KT_BYTES + n * 1024), 16, 0, 0);
+        dma_load16(kb, kro[i], sk + n * 1024);
+        dma_load16(vb, vro[i], sk + KT_BYTES + n * 1024);
       }
     } else {
+      // ragged last tile: rows past the last key re-read the last key
 #pragma unroll
       for (int i = 0; i < NLOAD; ++i) {
         const int n = NLOAD * wave + i;
         const int row = RPI * n + lrow;
-        const int kv = min(k0 + row, p.Skv - 1);
-        __builtin_amdgcn_global_load_lds((const void*)(kbase + (int64_t)kv * p.ldk * 2 + ((slot ^ (row % KCH)) << 4)),
-                                         (lds_ptr_t)(sk + n * 1024), 16, 0, 0);
-        __builtin_amdgcn_global_load_lds((const void*)(vbase + (int64_t)kv * p.ldv * 2 + ((slot ^ vsw(row)) << 4)),
-                                         (lds_ptr_t)(sk + KT_BYTES + n * 1024), 16, 0, 0);
+        const uint32_t r = (uint32_t)min(row, p.Skv - 1 - k0);
+        dma_load16(kb, r * (uint32_t)p.ldk * 2u + (uint32_t)((slot ^ (row % KCH)) << 4), sk + n * 1024);
+        dma_load16(vb, r * (uint32_t)p.ldv * 2u + (uint32_t)((slot ^ vsw(row)) << 4), sk + KT_BYTES + n * 1024);
       }
     }
   };
