@@ -60,6 +60,16 @@ __device__ __forceinline__ void barrier_keep_loads() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// Workgroup barrier for reuse of LDS only: this wave's LDS accesses complete,
+// then the barrier. Unlike __syncthreads it does not wait for the wave's
+// global stores (on gfx9 a store counts in vmcnt until the memory system
+// acknowledges it, microseconds under load): an epilogue that stages tiles
+// through LDS keeps its stores draining while it moves on.
+__device__ __forceinline__ void lds_barrier() {
+  wait_lgkmcnt0();
+  barrier_keep_loads();
+}
+
 // ------------------------------------------------------------ bf16 helpers
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) {
   return __uint_as_float(((uint32_t)h) << 16);

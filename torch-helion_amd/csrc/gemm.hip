@@ -20,7 +20,7 @@
 //            layout (conflict-free ds_read_b128 of MFMA operands); the epilogue
 //            of tile t overlaps the first loads of tile t+1;
 //          * direct (gemm_bf16_dl_kernel, small grids): one block per output
-//            tile, 64/128/256-row tiles, the same direct loads in a 2-4 stage
+//            tile, 64/128/256-row tiles, the same direct loads in a 2-8 stage
 //            ring;
 //          * staged (gemm_bf16_kernel): register-staged loads, for K not a
 //            multiple of 64 or strides the 32-bit direct-load offsets cannot
@@ -503,14 +503,19 @@ __global__ void __launch_bounds__(256, 1) gemm_bf16_kernel(GemmK p) {
 // first fragments of tile kt+1 are read and the loads of tile kt+2 issued into
 // the stage everyone has just finished reading.
 
-// Wait until at most n tiles of PER loads each are still in flight (n < 4).
+// Wait until at most n tiles of PER loads each are still in flight (n < 8,
+// n PER < 64).
 template <int PER>
 __device__ __forceinline__ void wait_tiles(int n) {
   switch (n) {
     case 0: wait_vmcnt<0>(); break;
     case 1: wait_vmcnt<PER>(); break;
     case 2: wait_vmcnt<(2 * PER < 64 ? 2 * PER : 63)>(); break;
-    default: wait_vmcnt<(3 * PER < 64 ? 3 * PER : 63)>(); break;
+    case 3: wait_vmcnt<(3 * PER < 64 ? 3 * PER : 63)>(); break;
+    case 4: wait_vmcnt<(4 * PER < 64 ? 4 * PER : 63)>(); break;
+    case 5: wait_vmcnt<(5 * PER < 64 ? 5 * PER : 63)>(); break;
+    case 6: wait_vmcnt<(6 * PER < 64 ? 6 * PER : 63)>(); break;
+    default: wait_vmcnt<(7 * PER < 64 ? 7 * PER : 63)>(); break;
   }
 }
 
@@ -524,7 +529,7 @@ __global__ void __launch_bounds__(256, 1) gemm_bf16_dl_kernel(GemmK p) {
   constexpr int SROW = BNC + 8;
   constexpr int EPI_BYTES = WM * SROW * 4;
   constexpr int MAIN_BYTES = STAGES * STAGE;
-  static_assert(STAGES >= 2 && STAGES <= 4 && (STAGES - 1) * (LA + LB) < 64, "stage count");
+  static_assert(STAGES >= 2 && STAGES <= 8 && (STAGES - 1) * (LA + LB) < 64, "stage count");
   constexpr int BODY = MAIN_BYTES > EPI_BYTES ? MAIN_BYTES : EPI_BYTES;
   constexpr int NMF = TM * TN;
   __shared__ __attribute__((aligned(16))) char smem[BODY + BM * 4];
@@ -550,16 +555,16 @@ __global__ void __launch_bounds__(256, 1) gemm_bf16_dl_kernel(GemmK p) {
   for (int i = 0; i < LB; ++i) vob[i] = (uint32_t)((32 * i + 8 * wave + lrow) * p.ldb * 2) + chunk;
   const int nk = (int)(p.K / 64);
 
+  // (dma_load16: untracked by the compiler, covered by the wait_tiles below)
+  const uint32_t lds0 = (uint32_t)(uintptr_t)smem;
   auto issue_tile = [&](int kt, int st) {
-    char* sa = smem + st * STAGE;
-    char* sb = sa + BM * 128;
+    const uint32_t sa = lds0 + st * STAGE;
+    const uint32_t sb = sa + BM * 128;
     const int64_t kofs = (int64_t)kt * 128;
 #pragma unroll
-    for (int i = 0; i < LA; ++i)
-      __builtin_amdgcn_global_load_lds((const void*)(ga + kofs + voa[i]), (lds_ptr_t)(sa + (4 * i + wave) * 1024), 16, 0, 0);
+    for (int i = 0; i < LA; ++i) dma_load16(ga + kofs, voa[i], sa + (4 * i + wave) * 1024);
 #pragma unroll
-    for (int i = 0; i < LB; ++i)
-      __builtin_amdgcn_global_load_lds((const void*)(gb + kofs + vob[i]), (lds_ptr_t)(sb + (4 * i + wave) * 1024), 16, 0, 0);
+    for (int i = 0; i < LB; ++i) dma_load16(gb + kofs, vob[i], sb + (4 * i + wave) * 1024);
   };
 
   bf16x8_t fa[2][TM], fb[2][TN];
@@ -653,7 +658,8 @@ __global__ void __launch_bounds__(256, 1) gemm_bf16_dl_kernel(GemmK p) {
       }
     }
   }
-  __syncthreads();
+  // (barriers for LDS reuse only: the global stores drain meanwhile)
+  lds_barrier();
 
   float* slab = (float*)smem;
 #pragma unroll
@@ -670,9 +676,9 @@ __global__ void __launch_bounds__(256, 1) gemm_bf16_dl_kernel(GemmK p) {
             slab[row * SROW + col] = acc[t][u][r];
           }
     }
-    __syncthreads();
+    lds_barrier();
     epilogue_slab(p, slab, SROW, WM, rs + s * WM, m0 + s * WM, tni, tid);
-    __syncthreads();
+    if (s == 0) lds_barrier();
   }
 #endif
 }
@@ -857,7 +863,9 @@ __global__ void __launch_bounds__(64 * NW, 1) gemm_bf16_pk_kernel(GemmK p) {
       wait_vmcnt<HLD>();
     else
       wait_vmcnt<0>();
-    __syncthreads();
+    // (LDS-only barrier: a __syncthreads would also wait for the half K tile
+    // just issued; the previous tile's slice reads completed before the last one)
+    barrier_keep_loads();
     read_frags(0, 0, 0);
 #pragma unroll
     for (int j = 0; j < TM / 2; ++j) ss[j] = 0.f;
@@ -895,7 +903,7 @@ __global__ void __launch_bounds__(64 * NW, 1) gemm_bf16_pk_kernel(GemmK p) {
           __builtin_amdgcn_sched_barrier(0);
           if constexpr (STEADY) {
             wait_vmcnt<0>();
-            __syncthreads();
+            lds_barrier();
             read_frags(st ^ 1, 0, 0);
             __builtin_amdgcn_sched_barrier(0);
             mfmas_ld(slot, NMF / 2, NMF, rsa, rsb, min(kt + 2, nk - 1), st, 0, HLD);
@@ -927,7 +935,7 @@ __global__ void __launch_bounds__(64 * NW, 1) gemm_bf16_pk_kernel(GemmK p) {
     // the stage the epilogue slices overlay, have landed); start the next
     // tile's first K tile.
     wait_vmcnt<0>();
-    __syncthreads();
+    lds_barrier();
     const int Ln = L + (int)gridDim.x;
     const bool more = Ln < tiles;
     int tmn = 0, tnn = 0;
@@ -1008,7 +1016,7 @@ __global__ void __launch_bounds__(64 * NW, 1) gemm_bf16_pk_kernel(GemmK p) {
       }
     }
 
-    __syncthreads();  // every wave is done with its stage-1 slice
+    lds_barrier();  // every wave is done with its stage-1 slice (its stores drain meanwhile)
     if (!more) break;
     if (nk > 1) issue_half(rsan, rsbn, 1, 1);
     L = Ln;
@@ -1290,9 +1298,13 @@ static void launch_bf16(const GemmK& k, hipStream_t s) {
 }
 
 // 64-row tiles are for small problems: deeper pipelines there hide the
-// global-load latency that a short K loop cannot amortise.
+// global-load latency that a short K loop cannot amortise. Up to 144 KiB of
+// stages (eight for 64 x 64 tiles: a K of 512 is then in flight at once).
 template <int BM, int BNC>
-constexpr int dl_stages() { return BM > 64 ? 2 : (BNC <= 128 ? 4 : 3); }
+constexpr int dl_stages() {
+  constexpr int s = 147456 / ((BM + BNC) * 128);
+  return BM > 64 ? 2 : (s > 8 ? 8 : s);
+}
 
 template <int BM, int BNC>
 static void launch_bf16_dl(const GemmK& k, hipStream_t s) {
