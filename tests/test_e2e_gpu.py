@@ -182,6 +182,29 @@ def test_mamba_layer_c2_merged_in_projection(gpu, tmp_path):
     assert (a - b).abs().max().item() / a.abs().max().item() < 1e-2
 
 
+def test_mamba_layer_c2_merged_convs(gpu, tmp_path):
+    """merge_convs (the default): the x, B and C convolutions of the layer run as one th_conv1d_causal
+    launch over the xBC channels side by side (inputs and outputs are column windows of two shared
+    buffers); bit-identical to one launch per convolution, two launches fewer."""
+    from targets.mamba import build_mamba_block, config_c2
+
+    announce("e2e mamba C2 merged convolutions")
+    cfg = config_c2()
+    m = build_mamba_block(cfg, seed=0)
+    x = m.example_inputs(seed=0)
+    sep = _compile(m, x, tmp_path, "c2_convsep", merge_convs=False)
+    mer = _compile(m, x, tmp_path, "c2_convmer")
+    assert mer.validation["ok"], mer.validation
+    convs = [l for l in mer.device_program.launches if l.kind == "conv1d"]
+    assert len(convs) == 1 and len(convs[0].info["merged"]) == 3, [l.kernel for l in mer.device_program.launches]
+    assert convs[0].info["width"] == cfg.d_inner + 2 * cfg.d_bc
+    assert len(mer.device_program.launches) == len(sep.device_program.launches) - 2
+    for a, b in zip(sep.run(*x), mer.run(*x)):
+        assert torch.equal(a.cpu(), b.cpu())
+    a32, b32 = sep.device_program.outputs(fp32=True)[0], mer.device_program.outputs(fp32=True)[0]
+    assert torch.equal(a32.cpu(), b32.cpu())
+
+
 @pytest.mark.parametrize("which", ["llama_gqa_bf16", "mamba_c2_bf16"])
 def test_graph_replays_match_eager(gpu, tmp_path, which):
     """The captured HIP graph of a whole program reproduces the eager launch sequence bit for bit,

@@ -87,3 +87,29 @@ def test_pool_best_fit_and_release_order():
     pool.release_before(3)            # frees b (last read by kernel 2)
     e = pool.alloc(4096, last=4)
     assert e is b
+
+
+def test_conv_merge_groups_one_per_layer(tmp_path):
+    """Each Mamba-2 layer's x, B and C convolutions form one group (one launch over the
+    xBC channels side by side), whose members all feed that layer's SSD, with the
+    SSD after the group's last member; a conv whose input or output must keep its
+    own buffer (fp32 copy, program output) stays out."""
+    from torch_helion.hip.runtime import conv_merge_groups
+
+    program = _program(3, tmp_path)
+    kern = {k.name: k for k in program.kernels}
+    index = {k.name: i for i, k in enumerate(program.kernels)}
+    convs = [k.name for k in program.kernels if k.kind == "conv1d"]
+    groups = conv_merge_groups(program)
+    assert len(groups) == 3 and sorted(n for g in groups for n in g) == sorted(convs)
+    widths = sorted(program.tensors[kern[n].arg("x").tensor].shape[1] for n in groups[0])
+    assert widths == [16, 16, 128]  # B and C (ngroups x d_state), x (d_inner)
+    for g in groups:
+        ys = {kern[n].outputs[0].tensor for n in g}
+        ssd = [k for k in program.kernels if k.kind.startswith("ssd") and ys & {a.tensor for a in k.args}]
+        assert len(ssd) == 1 and ys <= {a.tensor for a in ssd[0].args}
+        assert index[ssd[0].name] > max(index[n] for n in g)
+    # an excluded input (say, one with an fp32 copy) keeps its conv out of the group
+    x0 = kern[groups[0][0]].arg("x").tensor
+    g2 = conv_merge_groups(program, {x0})
+    assert len(g2) == 3 and groups[0][0] not in [n for g in g2 for n in g]

@@ -53,6 +53,7 @@ class CompileConfig:
                                                   # (288 blocks on 256 CUs) and costs more than the launches it saves
     cpu_flop_budget: float = 2e10                 # graphs above this skip CPU-side checks in "auto" mode
     reuse_buffers: bool = True                    # intermediates share device buffers by liveness
+    merge_convs: bool = True                      # the depthwise convolutions feeding one SSD run as one launch
     norm_gain: str = "fold"                       # "fold": RMSNorm gains folded into the GEMM weights (the
                                                   # reference's lowering); "activation": the device normalises
                                                   # the activations with the gain (th_rmsnorm, from the fp32

@@ -43,6 +43,47 @@ class Launch:
     info: dict[str, Any] = field(default_factory=dict)
 
 
+def conv_merge_groups(program: Program, excluded: set[str] = frozenset()) -> list[list[str]]:
+    """Groups (kernel names, program order) of depthwise conv1d kernels that feed one
+    SSD kernel with the same (batch, seq, kernel, activation, dtypes): a Mamba-2
+    layer's x, B and C convolutions (the reference convolves them as one xBC
+    tensor, models/mamba.py:278-283; its partition splits them). A group runs as
+    one th_conv1d_causal launch over the members' channels side by side: the
+    GEMMs that produce the inputs write them as column windows of one
+    [tokens, sum of widths] buffer and the SSD reads the outputs as column windows
+    of another (GEMM outputs, the convolution and the SSD all take row strides).
+    A member's input is a GEMM output read by nothing else, its output is read
+    only by the SSD, neither is a program output nor in ``excluded`` (tensors
+    with fp32 copies or cache slots), and its width is a multiple of 8 (every
+    window starts 16-byte aligned); the SSD runs after the group's last member."""
+    producer = {o.tensor: k for k in program.kernels for o in k.outputs}
+    readers: dict[str, list[KernelSpec]] = {}
+    for k in program.kernels:
+        for a in k.args:
+            readers.setdefault(a.tensor, []).append(k)
+    index = {k.name: i for i, k in enumerate(program.kernels)}
+    barred = set(program.outputs) | set(excluded)
+    cands: dict[tuple, list[KernelSpec]] = {}
+    for k in program.kernels:
+        if k.kind != "conv1d" or k.epilogue or len(k.outputs) != 1 or k.outputs[0].value != "acc":
+            continue
+        x, y = k.arg("x").tensor, k.outputs[0].tensor
+        tx, ty = program.tensors[x], program.tensors[y]
+        pk, rx, ry = producer.get(x), readers.get(x, []), readers.get(y, [])
+        if (pk is None or pk.kind != "gemm" or len(tx.shape) != 2 or tuple(tx.shape) != tuple(ty.shape)
+                or int(tx.shape[1]) % 8 or {x, y} & barred or [r.name for r in rx] != [k.name]
+                or len({r.name for r in ry}) != 1 or ry[0].kind not in ("ssd", "ssd_chunked")):
+            continue
+        a = k.attrs
+        key = (a["batch"], a["seq"], a["kernel"], a.get("activation"), tx.dtype, ty.dtype, ry[0].name)
+        cands.setdefault(key, []).append(k)
+    groups = []
+    for key, ms in cands.items():
+        if len(ms) >= 2 and index[key[-1]] > max(index[k.name] for k in ms):
+            groups.append([k.name for k in ms])
+    return groups
+
+
 class DeviceProgram:
     """A Program lowered and bound for execution on ``device``."""
 
@@ -50,7 +91,7 @@ class DeviceProgram:
                  fuse_rope: bool = True, fp32_outputs: bool = True, residual_fp32: bool = True,
                  merge_siblings: bool = False,
                  fold_sources: dict[str, tuple[torch.Tensor, torch.Tensor]] | None = None,
-                 reuse_buffers: bool = True) -> None:
+                 reuse_buffers: bool = True, merge_convs: bool = True) -> None:
         self.program = program
         # RMSNorm gains folded into weights by the front end, to be taken back
         # out (weight const -> (gain, unfolded weight)): such GEMMs read the
@@ -103,6 +144,12 @@ class DeviceProgram:
         shadowed -= set(self._slots)
         self._shadowed = shadowed
         self.shadow: dict[str, torch.Tensor] = {}
+        # depthwise convolutions feeding one SSD run as one launch (see _plan_conv_merges)
+        self._conv_groups: dict[str, dict] = {}
+        self._conv_member: dict[str, dict] = {}
+        self._conv_window: dict[str, tuple[dict, str, int, int]] = {}
+        if merge_convs:
+            self._plan_conv_merges(program)
         # Intermediates (and shadows, workspaces, normalised operands) come from a
         # pool that recycles a buffer once the last kernel reading it has been
         # bound: kernels run in program order on one stream. Program outputs keep
@@ -131,6 +178,11 @@ class DeviceProgram:
                 self._bind_outputs(k)
             if k.name in self._merged_away:
                 continue
+            if k.name in self._conv_groups:
+                self.launches.append(self._lower_conv_group(self._conv_groups[k.name]))
+                continue
+            if k.name in self._conv_member:
+                continue  # runs with its group, at the group's last member
             if k.name in self._merge_groups:
                 self.launches.extend(self._lower_gemm_merged(self._merge_groups[k.name]))
             else:
@@ -154,6 +206,14 @@ class DeviceProgram:
             if name in self.buffers:
                 continue
             t = self.program.tensors[name]
+            if name in self._conv_window:
+                g, side, off, w = self._conv_window[name]
+                if side not in g:  # the group's [tokens, sum of widths] buffer, for all its windows' lifetimes
+                    last = g["pos"] if side == "x" else max(self._last.get(m.outputs[0].tensor, g["pos"])
+                                                            for m in g["members"])
+                    g[side] = self._device_buffer((g["rows"], g["width"]), _TORCH_DT[t.dtype], last)
+                self.buffers[name] = g[side][:, off:off + w]
+                continue
             if name in self._slots:
                 self.buffers[name] = self._cache_row(name)
                 continue
@@ -161,6 +221,43 @@ class DeviceProgram:
             self.buffers[name] = self._device_buffer(t.shape, _TORCH_DT[t.dtype], last)
             if name in self._shadowed:
                 self.shadow[name] = self._device_buffer(t.shape, torch.float32, last)
+
+    def _plan_conv_merges(self, program: Program) -> None:
+        """Bind the groups of conv_merge_groups: per group, the input and output
+        tensors become column windows of two [tokens, sum of widths] buffers
+        (allocated when the first window is bound)."""
+        index = {k.name: i for i, k in enumerate(program.kernels)}
+        kern = {k.name: k for k in program.kernels}
+        for names in conv_merge_groups(program, self._shadowed | set(self._slots)):
+            ms = [kern[n] for n in names]
+            pos = max(index[n] for n in names)
+            g = {"members": ms, "pos": pos, "rows": int(program.tensors[ms[0].arg("x").tensor].shape[0]), "width": 0}
+            for k in ms:
+                w = int(program.tensors[k.arg("x").tensor].shape[1])
+                self._conv_window[k.arg("x").tensor] = (g, "x", g["width"], w)
+                self._conv_window[k.outputs[0].tensor] = (g, "y", g["width"], w)
+                self._conv_member[k.name] = g
+                g["width"] += w
+            self._conv_groups[program.kernels[pos].name] = g
+
+    def _lower_conv_group(self, g: dict) -> Launch:
+        """One th_conv1d_causal launch for a group of _plan_conv_merges."""
+        ms = g["members"]
+        ws = []
+        for k in ms:
+            host_w = self._host(k.arg("w").tensor)
+            w = host_w if host_w is not None else self.buffers[k.arg("w").tensor]
+            ws.append(w.float().reshape(int(self.program.tensors[k.arg("x").tensor].shape[1]), -1))
+        w = torch.cat(ws, 0).contiguous().to(self.device)
+        a = ms[0].attrs
+        x, y, act = g["x"], g["y"], a.get("activation")
+        name = "+".join(k.name for k in ms)
+
+        def run() -> None:
+            ops.conv1d_causal(x, w, y, batch=a["batch"], seq=a["seq"], activation=act, kernel=name)
+
+        return Launch(name, "conv1d", run, "th_conv1d_causal",
+                      {"activation": act, "merged": [k.name for k in ms], "width": g["width"]})
 
     def _cache_row(self, name: str) -> torch.Tensor:
         """Row ``pos`` of every sequence of the cache input a cache-slot output lives in:

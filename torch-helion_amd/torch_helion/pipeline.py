@@ -157,7 +157,8 @@ def compile_model(model: torch.nn.Module, example_args: Sequence[Any], config: C
                                            fp32_outputs=config.fp32_outputs, residual_fp32=config.residual_fp32,
                                            merge_siblings=config.merge_siblings,
                                            fold_sources=graph.fold_sources if config.norm_gain == "activation"
-                                           else None, reuse_buffers=config.reuse_buffers)
+                                           else None, reuse_buffers=config.reuse_buffers,
+                                           merge_convs=config.merge_convs)
             rw.write_json("kernels/launches.json", [{"kernel": l.kernel, "entry": l.entry, "info": l.info}
                                                     for l in device_program.launches])
 
