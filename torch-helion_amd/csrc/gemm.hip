@@ -219,8 +219,8 @@ __device__ __forceinline__ void epi_slice(const GemmK& p, const EpiOutK& eo, int
                                           int r_l, int c8, int np, int rp) {
   // two passes at a time: their global operands load together, and at most 2 x 16
   // of them are live (np = 4 with all loaded up front spilled the 8-wave kernel)
-  epi_pair<OP, SUMSQ>(p, eo, o2, wsl, ws, aoff, boff, rsrow, row0, col_w, r_l, c8, np, rp, 0);
-  if (np > 2) epi_pair<OP, SUMSQ>(p, eo, o2, wsl, ws, aoff, boff, rsrow, row0, col_w, r_l, c8, np, rp, 2);
+  for (int p0 = 0; p0 < np; p0 += 2)
+    epi_pair<OP, SUMSQ>(p, eo, o2, wsl, ws, aoff, boff, rsrow, row0, col_w, r_l, c8, np, rp, p0);
 }
 
 // Outputs o and o + 1 compute the same values (same op, operands and column
@@ -229,9 +229,49 @@ __device__ __forceinline__ bool same_values(const EpiOutK& x, const EpiOutK& y) 
   return x.op == y.op && x.a == y.a && x.b == y.b && x.e == y.e && x.cb == y.cb && x.ce == y.ce;
 }
 
+// Every output op over `rows` staged rows of a whole column tile
+// (slab[r * srow + i * bn + j] = acc_i(row0 + r, tile_n * bn + j)), the
+// direct-loop kernel's epilogue when 256 threads tile it evenly: each thread
+// keeps one octet of columns (8 (tid % q8), q8 = bn / 8) and walks rows
+// tid / q8 + k 256 / q8 with the per-wave epilogue's passes (one 16-byte
+// store per pass, no per-element index division). Returns false (nothing
+// done) when the tile does not divide so.
+template <bool SUMSQ>
+__device__ __forceinline__ bool epilogue_octets(const GemmK& p, const float* slab, int srow, int rows, const float* rs,
+                                                int64_t row0, int tile_n, int tid) {
+  const int bn = p.bn, q8 = bn >> 3;
+  if ((bn & 7) != 0 || 256 % q8 != 0 || rows % (256 / q8) != 0) return false;
+  const int rstep = 256 / q8, np = rows / rstep;
+  const int r_l = tid / q8, c8 = (tid - r_l * q8) << 3;
+  const int64_t col0 = (int64_t)tile_n * bn;
+  for (int o = 0; o < p.n_out; ++o) {
+    const EpiOutK& eo = p.out[o];
+    // an fp32 copy right after its bf16 output is stored from the same values
+    const int o2 = o + 1 < p.n_out && same_values(eo, p.out[o + 1]) ? o + 1 : -1;
+    if (o2 >= 0) ++o;
+    if (eo.ce <= col0 || eo.cb >= col0 + bn) continue;  // the window misses this tile
+    const int aoff = eo.a * bn, boff = eo.b * bn;
+#define TH_EPI_CASE(OP_) \
+  case OP_: epi_slice<OP_, SUMSQ>(p, eo, o2, slab, srow, aoff, boff, rs, row0, col0, r_l, c8, np, rstep); break
+    switch (eo.op) {
+      TH_EPI_CASE(TH_EPI_ACC);
+      TH_EPI_CASE(TH_EPI_ROPE);
+      TH_EPI_CASE(TH_EPI_ROPE_PAIR);
+      TH_EPI_CASE(TH_EPI_SILU);
+      TH_EPI_CASE(TH_EPI_SWIGLU);
+      TH_EPI_CASE(TH_EPI_ADD);
+      TH_EPI_CASE(TH_EPI_SOFTPLUS_ADD);
+      default: epi_slice<TH_EPI_MUL, SUMSQ>(p, eo, o2, slab, srow, aoff, boff, rs, row0, col0, r_l, c8, np, rstep); break;
+    }
+#undef TH_EPI_CASE
+  }
+  return true;
+}
+
+
 // Evaluate every output op for the `rows` slab rows staged in LDS.
 // slab[r * srow + i * bn + j] = acc_i(row0 + r, tile_n * bn + j).
-__device__ void epilogue_slab(const GemmK& p, const float* slab, int srow, int rows,
+__device__ __forceinline__ void epilogue_slab(const GemmK& p, const float* slab, int srow, int rows,
                               const float* rs, int64_t row0, int tile_n, int tid) {
   const int bn = p.bn;
   const int q4 = bn >> 2;
@@ -677,7 +717,8 @@ __global__ void __launch_bounds__(256, 1) gemm_bf16_dl_kernel(GemmK p) {
           }
     }
     lds_barrier();
-    epilogue_slab(p, slab, SROW, WM, rs + s * WM, m0 + s * WM, tni, tid);
+    if (!epilogue_octets<SUMSQ>(p, slab, SROW, WM, rs + s * WM, m0 + s * WM, tni, tid))
+      epilogue_slab(p, slab, SROW, WM, rs + s * WM, m0 + s * WM, tni, tid);
     if (s == 0) lds_barrier();
   }
 #endif
