@@ -117,12 +117,19 @@ __device__ __forceinline__ void epi_pair(const GemmK& p, const EpiOutK& eo, int 
   const int ia = eo.a, ib = eo.b;
   const bool sa = SUMSQ && ((p.rscale_mask >> ia) & 1u);
   const bool sb = SUMSQ && ib >= 0 && ((p.rscale_mask >> ib) & 1u);
-  const int64_t gn = col_w + c8;
+  // columns fit 32 bits (N < 2^31): the window test and column offsets stay 32-bit
+  const int gn = (int)col_w + c8;
   // the output's column window (multiples of 8: an octet is wholly in or out)
-  const int valid = gn >= eo.cb && gn < eo.ce ? (int)min((int64_t)8, (int64_t)eo.ce - gn) : 0;
-  const int64_t gc = gn - eo.cb;  // output (and extra) column
+  const int valid = gn >= eo.cb && gn < eo.ce ? min(8, eo.ce - gn) : 0;
+  const int gc = gn - eo.cb;  // output (and extra) column
   float xe[2][8], ye[2][8];
   if constexpr (USES_E || USES_T) {
+    // RoPE table row of pass p0: one division per call, then a wrap per pass
+    int tr0 = 0, tcol = 0;
+    if constexpr (USES_T) {
+      tr0 = (int)((row0 + r_l + (int64_t)p0 * rp) % p.period);
+      tcol = gn % p.hd;
+    }
 #pragma unroll
     for (int pi = 0; pi < 2; ++pi) {
       const int ps = p0 + pi;
@@ -133,7 +140,9 @@ __device__ __forceinline__ void epi_pair(const GemmK& p, const EpiOutK& eo, int 
         load8(p.extra[e], gm * p.ld_extra[e] + gc, p.extra_dtype[e], p.extra_vec8[e] != 0, valid, xe[pi]);
       } else {
         // head_dim is a multiple of 8, so the octet lies inside one head
-        const int64_t toff = (int64_t)((int)gm % p.period) * p.hd + (int)gn % p.hd;
+        int tr = tr0 + pi * rp;
+        while (tr >= p.period) tr -= p.period;
+        const int64_t toff = (int64_t)tr * p.hd + tcol;
         const float4 c0 = *(const float4*)(p.rcos + toff), c1 = *(const float4*)(p.rcos + toff + 4);
         const float4 s0 = *(const float4*)(p.rsin + toff), s1 = *(const float4*)(p.rsin + toff + 4);
         xe[pi][0] = c0.x; xe[pi][1] = c0.y; xe[pi][2] = c0.z; xe[pi][3] = c0.w;
@@ -169,8 +178,9 @@ __device__ __forceinline__ void epi_pair(const GemmK& p, const EpiOutK& eo, int 
     } else if constexpr (OP == TH_EPI_SWIGLU) {
       const float4 b0 = *(const float4*)(srow + boff + c8), b1 = *(const float4*)(srow + boff + c8 + 4);
       float bb[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+      const float rb = sb ? rr : 1.f;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) v[i] = a[i] * sigmoidf_(a[i]) * (sb ? bb[i] * rr : bb[i]);
+      for (int i = 0; i < 8; ++i) v[i] = a[i] * sigmoidf_(a[i]) * (bb[i] * rb);
     } else if constexpr (OP == TH_EPI_ROPE || OP == TH_EPI_ROPE_PAIR) {
       float rot[8];
       if constexpr (OP == TH_EPI_ROPE) {
