@@ -170,8 +170,10 @@ def test_mamba_layer_c2_merged_in_projection(gpu, tmp_path):
     cfg = config_c2()
     m = build_mamba_block(cfg, seed=0)
     x = m.example_inputs(seed=0)
-    sep = _compile(m, x, tmp_path, "c2_sep", residual_fp32=False, fp32_outputs=False)
+    sep = _compile(m, x, tmp_path, "c2_sep", residual_fp32=False, fp32_outputs=False, merge_siblings=False)
     mer = _compile(m, x, tmp_path, "c2_mer", residual_fp32=False, fp32_outputs=False, merge_siblings=True)
+    auto = _compile(m, x, tmp_path, "c2_auto", residual_fp32=False, fp32_outputs=False)  # 2048 rows: merged
+    assert len(auto.device_program.launches) == len(mer.device_program.launches)
     assert mer.validation["ok"], mer.validation
     merged = [l for l in mer.device_program.launches if "+" in l.kernel]
     assert merged and len(merged[0].info["merged"]) == 3, [l.kernel for l in mer.device_program.launches]
@@ -192,8 +194,8 @@ def test_mamba_layer_c2_merged_convs(gpu, tmp_path):
     cfg = config_c2()
     m = build_mamba_block(cfg, seed=0)
     x = m.example_inputs(seed=0)
-    sep = _compile(m, x, tmp_path, "c2_convsep", merge_convs=False)
-    mer = _compile(m, x, tmp_path, "c2_convmer")
+    sep = _compile(m, x, tmp_path, "c2_convsep", merge_convs=False, merge_siblings=False)
+    mer = _compile(m, x, tmp_path, "c2_convmer", merge_siblings=False)
     assert mer.validation["ok"], mer.validation
     convs = [l for l in mer.device_program.launches if l.kind == "conv1d"]
     assert len(convs) == 1 and len(convs[0].info["merged"]) == 3, [l.kernel for l in mer.device_program.launches]

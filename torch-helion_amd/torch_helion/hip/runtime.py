@@ -89,7 +89,7 @@ class DeviceProgram:
 
     def __init__(self, program: Program, params: dict[str, torch.Tensor], device: int | torch.device = 0,
                  fuse_rope: bool = True, fp32_outputs: bool = True, residual_fp32: bool = True,
-                 merge_siblings: bool = False,
+                 merge_siblings: bool | None = False,
                  fold_sources: dict[str, tuple[torch.Tensor, torch.Tensor]] | None = None,
                  reuse_buffers: bool = True, merge_convs: bool = True) -> None:
         self.program = program
@@ -153,11 +153,12 @@ class DeviceProgram:
         # Intermediates (and shadows, workspaces, normalised operands) come from a
         # pool that recycles a buffer once the last kernel reading it has been
         # bound: kernels run in program order on one stream. Program outputs keep
-        # buffers of their own. (Merged sibling launches write members' outputs
-        # ahead of their program position, so merging allocates everything.)
+        # buffers of their own. (A merged sibling launch writes its members'
+        # outputs at the leader's position: they are bound there, each held to
+        # its own last reader.)
         from .memplan import BufferPool, lifetimes
 
-        self.reuse = reuse_buffers and not merge_siblings
+        self.reuse = reuse_buffers
         self._born, self._last = lifetimes(program)
         self._pool = BufferPool(lambda n: torch.empty(n, dtype=torch.uint8, device=self.device)) if self.reuse else None
         self._cur = 0
@@ -170,12 +171,16 @@ class DeviceProgram:
             if k.kind == "embedding" and k.arg("ids").tensor in program.inputs:
                 ids = k.arg("ids").tensor
                 self._vocab[ids] = min(self._vocab.get(ids, k.attrs["vocab"]), k.attrs["vocab"])
+        if merge_siblings is None:  # small row counts: launches, not tiles, set the time
+            merge_siblings = all(k.grid.get("rows", 0) <= 4096 for k in program.kernels if k.kind == "gemm")
         self._merge_groups, self._merged_away = self._plan_sibling_merges(program) if merge_siblings else ({}, set())
         for i, k in enumerate(program.kernels):
             self._cur = i
             if self.reuse:
                 self._pool.release_before(i)
                 self._bind_outputs(k)
+                for m in self._merge_groups.get(k.name, [])[1:]:
+                    self._bind_outputs(m[0])
             if k.name in self._merged_away:
                 continue
             if k.name in self._conv_groups:
@@ -686,7 +691,7 @@ class DeviceProgram:
         if k.kind != "gemm" or not k.gemms:
             return None
         lhs_t = k.arg("lhs").tensor
-        if self.buffers[lhs_t].dtype != torch.bfloat16 or k.grid["cols"] % 8:
+        if self.program.tensors[lhs_t].dtype != "bfloat16" or k.grid["cols"] % 8:
             return None
         plan = match_epilogue(k)
         if not plan.fused or not plan.outs:
@@ -695,6 +700,10 @@ class DeviceProgram:
             return None
         used = sorted({o.a for o in plan.outs})
         if any(k.arg(k.gemms[a].rhs).tensor not in self.program.params for a in used):
+            return None
+        # a weight with its norm gain folded in runs on the normalised activations
+        # and the unfolded weight (_lower_gemm_fused); the merged launch would not
+        if any(k.arg(k.gemms[a].rhs).tensor in self.fold_sources for a in used):
             return None
         flags = {bool(plan.scaled.get(a, False)) for a in used}
         if len(flags) != 1:
@@ -714,7 +723,7 @@ class DeviceProgram:
                 continue
             key, plan, used = m
             members = [(k, plan, used)]
-            n_out = sum(1 + (o.tensor in self.shadow) for o in plan.outs)
+            n_out = sum(1 + (o.tensor in self._shadowed) for o in plan.outs)
             extras = {k.arg(o.extra).tensor for o in plan.outs if o.extra is not None}
             for j, k2, m2 in keyed[i + 1:]:
                 if m2 is None or k2.name in away or m2[0] != key:
@@ -722,7 +731,7 @@ class DeviceProgram:
                 _, plan2, used2 = m2
                 ext2 = {k2.arg(o.extra).tensor for o in plan2.outs if o.extra is not None}
                 ready = all(t in program.params or produced_at.get(t, len(program.kernels)) < i for t in ext2)
-                n2 = n_out + sum(1 + (o.tensor in self.shadow) for o in plan2.outs)
+                n2 = n_out + sum(1 + (o.tensor in self._shadowed) for o in plan2.outs)
                 if not ready or n2 > abi.MAX_OUT or len(extras | ext2) > abi.MAX_EXTRA:
                     continue
                 members.append((k2, plan2, used2))
