@@ -42,50 +42,73 @@ struct SsdK {
 
 // Running sum of dA (or the given cum re-based) for chunk ``c`` into cl[0..Q),
 // dt into dts[0..Q); rows past the end of the sequence get dt = 0 and repeat
-// the last running sum. Needs 2*256 floats of scratch in ``tmp``.
-__device__ void chunk_running_sum(const SsdK& p, int b, int h, int c, float* cl, float* dts, float* tmp) {
+// the last running sum. In two parts so that a kernel can issue other loads
+// between this thread's loads and the scan that waits for them: the first
+// keeps the loaded words raw (a conversion there would wait for the load).
+// 256 threads.
+struct RunSumIn {
+  uint32_t dt, cum, base;  // bf16 in the low half or fp32 bits, by p.dtype
+  float a;                 // A[h] (the dA path)
+};
+
+__device__ __forceinline__ uint32_t load_raw(const void* q, int64_t i, int dtype) {
+  return dtype == TH_BF16 ? (uint32_t)((const uint16_t*)q)[i] : ((const uint32_t*)q)[i];
+}
+
+__device__ __forceinline__ float raw_f32(uint32_t w, int dtype) {
+  return __uint_as_float(dtype == TH_BF16 ? w << 16 : w);
+}
+
+__device__ __forceinline__ RunSumIn chunk_running_sum_load(const SsdK& p, int b, int h, int c) {
   const int tid = threadIdx.x;
   const int t0 = c * p.Q;
   const int rows = min(p.Q, p.S - t0);
-  float v = 0.f, dtv = 0.f;
-  if (tid < p.Q) {
-    const int l = min(tid, rows - 1);
-    const int64_t tok = (int64_t)b * p.S + t0 + l;
-    const float d = load_elem(p.dt, tok * p.lddt + (int64_t)h * p.dt_stride, p.dtype);
-    dtv = tid < rows ? d : 0.f;
-    if (p.cum == nullptr) {
-      v = tid < rows ? d * p.A[h] : 0.f;
-    } else {
-      v = load_elem(p.cum, tok * p.ldcum + (int64_t)h * p.dt_stride, p.dtype);
-    }
-  }
+  // Every load is issued on both sides of the cum test (without cum they all
+  // read dt's first element, unused): a register left unloaded on one side
+  // makes the compiler wait for the other side's load there.
+  const bool cm = p.cum != nullptr;
+  const void* cs = cm ? p.cum : p.dt;
+  RunSumIn r{0u, 0u, 0u, cm ? 0.f : p.A[h]};
+  const int l = min(min(tid, p.Q - 1), rows - 1);
+  const int64_t tok = (int64_t)b * p.S + t0 + l;
+  r.dt = load_raw(p.dt, tok * p.lddt + (int64_t)h * p.dt_stride, p.dtype);
+  r.cum = load_raw(cs, cm ? tok * p.ldcum + (int64_t)h * p.dt_stride : 0, p.dtype);
+  // re-base on the running sum just before the chunk (its first row for chunk 0,
+  // where no earlier state exists and only differences are used)
+  const int64_t row = (int64_t)b * p.S + (c == 0 ? 0 : t0 - 1);
+  r.base = load_raw(cs, cm ? row * p.ldcum + (int64_t)h * p.dt_stride : 0, p.dtype);
+  return r;
+}
+
+// Needs 4 floats of scratch in ``tmp``.
+__device__ __forceinline__ void chunk_running_sum_finish(const SsdK& p, int h, int c, const RunSumIn& r, float* cl,
+                                                         float* dts, float* tmp) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int rows = min(p.Q, p.S - c * p.Q);
+  const bool in = tid < p.Q && tid < rows;
+  const float d = raw_f32(r.dt, p.dtype);
   if (p.cum == nullptr) {
-    // inclusive Hillis-Steele scan over Q <= 256 values
-    float* a = tmp;
-    float* bb = tmp + 256;
-    a[tid] = v;
+    // inclusive scan: within each wave by shuffles, then the earlier waves' totals
+    float x = in ? d * r.a : 0.f;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const float y = __shfl_up(x, off, 64);
+      if (lane >= off) x += y;
+    }
+    if (lane == 63) tmp[wave] = x;
     __syncthreads();
-    for (int off = 1; off < p.Q; off <<= 1) {
-      float s = a[tid];
-      if (tid >= off && tid < p.Q) s += a[tid - off];
-      bb[tid] = s;
-      __syncthreads();
-      float* t = a; a = bb; bb = t;
-    }
-    if (tid < p.Q) cl[tid] = a[tid];
+    float pre = 0.f;
+    for (int w = 0; w < wave; ++w) pre += tmp[w];
+    if (tid < p.Q) cl[tid] = x + pre;
   } else {
-    // re-base on the running sum just before the chunk (its first row for chunk 0,
-    // where no earlier state exists and only differences are used)
-    float base;
-    if (c == 0) {
-      base = load_elem(p.cum, ((int64_t)b * p.S) * p.ldcum + (int64_t)h * p.dt_stride, p.dtype);
-    } else {
-      base = load_elem(p.cum, ((int64_t)b * p.S + t0 - 1) * p.ldcum + (int64_t)h * p.dt_stride, p.dtype);
-    }
-    if (tid < p.Q) cl[tid] = v - base;
+    if (tid < p.Q) cl[tid] = raw_f32(r.cum, p.dtype) - raw_f32(r.base, p.dtype);
   }
-  if (tid < p.Q) dts[tid] = dtv;
+  if (tid < p.Q) dts[tid] = in ? d : 0.f;
   __syncthreads();
+}
+
+__device__ void chunk_running_sum(const SsdK& p, int b, int h, int c, float* cl, float* dts, float* tmp) {
+  chunk_running_sum_finish(p, h, c, chunk_running_sum_load(p, b, h, c), cl, dts, tmp);
 }
 
 __global__ void __launch_bounds__(256) ssd_state_kernel(SsdK p) {
@@ -488,33 +511,44 @@ __global__ void __launch_bounds__(256) ssd_carry2_kernel(SsdK p, uint4* hf) {
 // x of the chunk is staged once in LDS as B fragments (relayout()). A unit is
 // a 32-row t-block with NPT p-tiles; for each s-block s <= t the wave forms
 // G^T = B_s C_t^T on the MFMA (lane = t, registers = s in C order), weighs it
-// element-wise with the decay (every exponent a difference cl_t - cl_s <= 0,
-// in base 2, on the raw v_exp_f32: results below 2^-126 flush to zero) and
-// uses it directly as the A operand of the product with x.
-// Full chunks load without guards; only the diagonal s-block is masked. The
-// result goes out through a per-wave LDS tile as 16-byte rows (gate in, y out).
-constexpr int kEpiStride = 36;  // floats per row of the per-wave 32 x 32 output tile
+// element-wise with the decay and uses it directly as the A operand of the
+// product with x. Exponents are in base 2 on the raw v_exp_f32 (results below
+// 2^-126 flush to zero). For an s-block before the t-block (first token t0)
+// the decay factors as exp2(cl_t - cl_t0) exp2(cl_t0 - cl_s): the second
+// factor, times dt_s, comes from a per-chunk table in LDS, and the first
+// scales the finished rows of acc once per unit (together with the state
+// term). Both factors are <= 1 because the running sum of dt A does not
+// increase along the chunk (A < 0, dt > 0), so neither overflows where the
+// direct exponent would not. Only the diagonal s-block takes the exponent
+// per element, and is masked. The result goes out through a per-wave LDS
+// tile as 16-byte rows (gate in, y out), 16 rows at a time.
+// The carried state's hi/lo fragments (P N 4 bytes, the same for every unit
+// of the block) are copied into LDS once, by direct-to-LDS loads issued at the
+// start, instead of being re-read from L2 by each unit.
+constexpr int kEpiStride = 36;  // floats per row of the per-wave 16 x 32 output tile
 
 template <int KS, int NPT>  // KS = state_dim / 16, NPT = p-tiles per unit
 __global__ void __launch_bounds__(256, 2) ssd_out2_kernel(SsdK p, const uint4* hf) {
   extern __shared__ float sm[];
   float* cl = sm;          // running sum of dA, in log2 units after set-up
   float* dts = cl + 256;
-  float* tmp = dts + 256;
-  float* epi = tmp + 512;  // [4 waves][32][kEpiStride]
-  uint4* xs = (uint4*)(epi + 4 * 32 * kEpiStride);  // [Q/32][2][PT][64] B fragments of x
+  float* epi = dts + 256;  // [4 waves][16][kEpiStride]; the running sum's scratch before that
+  uint4* xs = (uint4*)(epi + 4 * 16 * kEpiStride);  // [Q/32][2][PT][64] B fragments of x
+  uint4* hs = xs + (p.Q >> 5) * 2 * (p.P >> 5) * 64;  // [PT][KS][64][2] carried-state fragments
+  float* wt = (float*)(hs + p.P * p.N / 4);           // decay weights, row tb at 16 tb (tb - 1)
   const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z, tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = h / p.hpg, gl = lane >> 5, r32 = lane & 31;
-  chunk_running_sum(p, b, h, c, cl, dts, tmp);
   const int Q = p.Q, t0 = c * Q, rows = min(Q, p.S - t0);
-  if (tid < Q) cl[tid] *= 1.4426950408889634f;
   const int PT = p.P >> 5;
   const int64_t tok0 = (int64_t)b * p.S + t0;
   const int ntb = (rows + 31) >> 5;
-  const bool full = rows == Q;
   {
-    // this wave's x tiles (at most 8): every load issued before the first relayout
+    // Set-up loads, all in flight together: dt for the running sum, this
+    // wave's x tiles (at most 8), then the carried state into LDS (1 KiB per
+    // wave-instruction, waited for with wait_vmcnt before the barrier that
+    // precedes the first unit). The scan's barriers overlap their latency.
+    const RunSumIn rin = chunk_running_sum_load(p, b, h, c);
     const bf16x8_t e0 = eye_frag(lane, 0), e1 = eye_frag(lane, 1);
     bf16x8_t xa[8][2];
 #pragma unroll
@@ -527,6 +561,19 @@ __global__ void __launch_bounds__(256, 2) ssd_out2_kernel(SsdK p, const uint4* h
       xa[k2][0] = ldg_bf16x8(p.x, at, ok);
       xa[k2][1] = ldg_bf16x8(p.x, at + 16, ok);
     }
+    if (c > 0) {
+      // (uniform addresses; the read-first-lanes keep them in scalar registers,
+      // which the load's address and M0 operands require; the builtin returns
+      // int, so each half goes through uint32_t before widening)
+      const uint64_t sa = (uint64_t)(uintptr_t)(hf + (((int64_t)b * p.H + h) * p.nc + c) * (int64_t)(p.P * p.N / 4));
+      const uint32_t shi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(sa >> 32));
+      const uint32_t slo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)sa);
+      const char* src = (const char*)(uintptr_t)(((uint64_t)shi << 32) | (uint64_t)slo);
+      const uint32_t dst = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)hs);
+      for (int k = wave; k < p.P * p.N / 256; k += 4) dma_load16(src + 1024 * k, 16 * lane, dst + 1024 * k);
+    }
+    chunk_running_sum_finish(p, h, c, rin, cl, dts, epi);
+    if (tid < Q) cl[tid] *= 1.4426950408889634f;
 #pragma unroll
     for (int k2 = 0; k2 < 8; ++k2) {
       const int u = wave + 4 * k2;
@@ -541,11 +588,19 @@ __global__ void __launch_bounds__(256, 2) ssd_out2_kernel(SsdK p, const uint4* h
     }
   }
   __syncthreads();
+  // wt[16 tb (tb - 1) + s] = exp2(cl_t0 - cl_s) dt_s for the s before t0 = 32 tb
+  for (int tb = 1; tb < ntb; ++tb)
+    for (int s = tid; s < 32 * tb; s += 256)
+      wt[16 * tb * (tb - 1) + s] = __builtin_amdgcn_exp2f(cl[tb * 32] - cl[s]) * dts[s];
+  wait_vmcnt<0>();  // this wave's share of the carried state has landed
+  __syncthreads();
   const int PG = PT / NPT, U = ntb * PG;
-  const uint4* hfc = hf + (((int64_t)b * p.H + h) * p.nc + c) * (int64_t)(p.P * p.N / 4);
   const int64_t ccol = (int64_t)g * p.N + 8 * gl;
+  // B rows: a uniform base and 32-bit lane offsets (row stride below 2^22 elements)
+  const char* bbase = (const char*)p.b + (tok0 * p.ldb + (int64_t)g * p.N) * 2;
+  const uint32_t ldb2 = (uint32_t)p.ldb * 2, ccol2 = 16 * gl;
   const float dh = p.D ? p.D[h] : 0.f;
-  float* ep = epi + wave * 32 * kEpiStride;
+  float* ep = epi + wave * 16 * kEpiStride;
   for (int i = 0; i < U; ++i) {
     // units by decreasing work, dealt to the waves in snake order
     int w = i & 3;
@@ -561,6 +616,9 @@ __global__ void __launch_bounds__(256, 2) ssd_out2_kernel(SsdK p, const uint4* h
     for (int j = 0; j < NPT; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[j][r] = 0.f;
+    // cl at the t-block's first token: the decay exp2(cl_t - cl_s) of every
+    // earlier s factors as exp2(cl_t - cl_t0) exp2(cl_t0 - cl_s), both <= 1
+    const float clt0 = cl[tb * 32];
     if (c > 0) {
 #pragma unroll
       for (int j = 0; j < NPT; ++j) {
@@ -568,7 +626,7 @@ __global__ void __launch_bounds__(256, 2) ssd_out2_kernel(SsdK p, const uint4* h
         uint4 hfr[KS][2];
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
-          const uint4* f = hfc + 2 * ((pt * KS + ks) * 64 + lane);
+          const uint4* f = hs + 2 * ((pt * KS + ks) * 64 + lane);
           hfr[ks][0] = f[0];
           hfr[ks][1] = f[1];
         }
@@ -578,40 +636,34 @@ __global__ void __launch_bounds__(256, 2) ssd_out2_kernel(SsdK p, const uint4* h
           acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(cf[ks], __builtin_bit_cast(bf16x8_t, hfr[ks][1]), acc[j], 0, 0, 0);
         }
       }
+      // state term exp2(cl_t) C_t H = exp2(cl_t - cl_t0) (exp2(cl_t0) C_t H): the
+      // per-row factor is applied with the earlier s-blocks' terms below
+      const float e0 = __builtin_amdgcn_exp2f(clt0);
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const float4 c4 = *(const float4*)&cl[tb * 32 + 8 * q + 4 * gl];
-        const float ex[4] = {__builtin_amdgcn_exp2f(c4.x), __builtin_amdgcn_exp2f(c4.y),
-                             __builtin_amdgcn_exp2f(c4.z), __builtin_amdgcn_exp2f(c4.w)};
+      for (int j = 0; j < NPT; ++j)
 #pragma unroll
-        for (int j = 0; j < NPT; ++j)
-#pragma unroll
-          for (int i2 = 0; i2 < 4; ++i2) acc[j][4 * q + i2] *= ex[i2];
-      }
+        for (int r = 0; r < 16; ++r) acc[j][r] *= e0;
     }
     const float clt = cl[t];
-    // one s-block: G^T = B_s C_t^T, decay-weighted and (diagonal block) masked, times x_s
-    auto sblock = [&](const bf16x8_t* bfr, int sb) {
+    // B rows of s-block sb; rows past the chunk's end repeat its last row (their
+    // products only reach masked or discarded outputs, and x there is zero)
+    auto load_b = [&](bf16x8_t* bfr, int sb) {
+      const uint32_t sr = (uint32_t)min(sb * 32 + r32, rows - 1);
+      const char* bp = bbase + (sr * ldb2 + ccol2);
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) bfr[ks] = *(const bf16x8_t*)(bp + 32 * ks);
+    };
+    // G^T = B_s C_t^T (lane = t, registers = s in C order)
+    auto chain = [&](const bf16x8_t* bfr) {
       f32x16_t gt;
 #pragma unroll
       for (int r = 0; r < 16; ++r) gt[r] = 0.f;
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) gt = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[ks], cf[ks], gt, 0, 0, 0);
-      float m[16];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int s0 = sb * 32 + 8 * q + 4 * gl;
-        const float4 c4 = *(const float4*)&cl[s0];
-        const float4 d4 = *(const float4*)&dts[s0];
-        const float cs[4] = {c4.x, c4.y, c4.z, c4.w}, ds[4] = {d4.x, d4.y, d4.z, d4.w};
-#pragma unroll
-        for (int i2 = 0; i2 < 4; ++i2)
-          m[4 * q + i2] = gt[4 * q + i2] * __builtin_amdgcn_exp2f(clt - cs[i2]) * ds[i2];
-      }
-      if (sb == tb) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) m[r] = tb * 32 + crow_of(r, lane) <= t ? m[r] : 0.f;
-      }
+      return gt;
+    };
+    // acc += M x_s, M (registers = s) split into bf16 hi + lo
+    auto xprod = [&](const float* m, int sb) {
       bf16x8_t mh0, ml0, mh1, ml1;
       pk8_split(m, mh0, ml0);
       pk8_split(m + 8, mh1, ml1);
@@ -626,27 +678,95 @@ __global__ void __launch_bounds__(256, 2) ssd_out2_kernel(SsdK p, const uint4* h
         acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ml1, x1, acc[j], 0, 0, 0);
       }
     };
-    auto load_b = [&](bf16x8_t* bfr, int sb) {
-      const int sr = sb * 32 + r32;
-      const int64_t at = (tok0 + sr) * p.ldb + ccol;
-      if (full) {
+    // an earlier s-block: M = G^T exp2(cl_t0 - cl_s) dt_s from the per-t-block table
+    auto offdiag = [&](const f32x16_t& gt, int sb) {
+      float m[16];
+      const float* wr = wt + 16 * tb * (tb - 1) + sb * 32 + 4 * gl;
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) bfr[ks] = *(const bf16x8_t*)((const uint16_t*)p.b + at + ks * 16);
-      } else {
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) bfr[ks] = ldg_bf16x8(p.b, at + ks * 16, sr < rows);
+      for (int q = 0; q < 4; ++q) {
+        const float4 w4 = *(const float4*)(wr + 8 * q);
+        m[4 * q] = gt[4 * q] * w4.x;
+        m[4 * q + 1] = gt[4 * q + 1] * w4.y;
+        m[4 * q + 2] = gt[4 * q + 2] * w4.z;
+        m[4 * q + 3] = gt[4 * q + 3] * w4.w;
       }
+      xprod(m, sb);
     };
-    // two buffers: the next s-block's B rows are in flight while this one computes
+    // the diagonal s-block: full decay exp2(cl_t - cl_s) dt_s, masked to s <= t
+    auto diag = [&](const f32x16_t& gt) {
+      float m[16];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int s0 = tb * 32 + 8 * q + 4 * gl;
+        const float4 c4 = *(const float4*)&cl[s0];
+        const float4 d4 = *(const float4*)&dts[s0];
+        const float cs[4] = {c4.x, c4.y, c4.z, c4.w}, ds[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+        for (int i2 = 0; i2 < 4; ++i2) {
+          const float v = gt[4 * q + i2] * __builtin_amdgcn_exp2f(clt - cs[i2]) * ds[i2];
+          m[4 * q + i2] = 8 * q + 4 * gl + i2 <= r32 ? v : 0.f;
+        }
+      }
+      xprod(m, tb);
+    };
+    // Earlier s-blocks, each G^T chain issued one step ahead of the weighting
+    // and product that consume it (the MFMA chain runs under the VALU work),
+    // and the B rows two steps ahead: a buffer is refilled as soon as its
+    // chain has read it, a full step before the next chain waits for it. The
+    // refills are unconditional (the last two re-read clamped rows) so that
+    // every chain waits only for its own loads; a scheduling barrier keeps the
+    // compiler from sinking them to their uses.
     bf16x8_t b0[KS], b1[KS];
+    f32x16_t g0, g1;
     load_b(b0, 0);
-    for (int sb = 0; sb <= tb; sb += 2) {
-      if (sb + 1 <= tb) load_b(b1, sb + 1);
-      sblock(b0, sb);
-      if (sb + 1 > tb) break;
-      if (sb + 2 <= tb) load_b(b0, sb + 2);
-      sblock(b1, sb + 1);
+    if (tb > 0) load_b(b1, 1);
+    g0 = chain(b0);
+    int sb = 0;
+    while (sb < tb) {
+      load_b(b0, sb + 2);
+      __builtin_amdgcn_sched_barrier(0);
+      g1 = chain(b1);  // s-block sb + 1
+      offdiag(g0, sb);
+      if (++sb == tb) break;
+      load_b(b1, sb + 2);
+      __builtin_amdgcn_sched_barrier(0);
+      g0 = chain(b0);
+      offdiag(g1, sb);
+      ++sb;
     }
+    // rows t of acc: the factor exp2(cl_t - cl_t0) of the state and earlier terms
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float4 c4 = *(const float4*)&cl[tb * 32 + 8 * q + 4 * gl];
+      const float ex[4] = {__builtin_amdgcn_exp2f(c4.x - clt0), __builtin_amdgcn_exp2f(c4.y - clt0),
+                           __builtin_amdgcn_exp2f(c4.z - clt0), __builtin_amdgcn_exp2f(c4.w - clt0)};
+#pragma unroll
+      for (int j = 0; j < NPT; ++j)
+#pragma unroll
+        for (int i2 = 0; i2 < 4; ++i2) acc[j][4 * q + i2] *= ex[i2];
+    }
+    // the vector epilogue's gate rows, fetched under the diagonal block: lane
+    // (row, c0) holds 8 columns of rows 16 hh + row of the t-block
+    const int erow = lane >> 2, ec0 = 8 * (lane & 3);
+    bool eok[2];
+    int64_t etok[2];
+    uint4 gw[NPT][2];
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      const int tr = tb * 32 + 16 * hh + erow;
+      eok[hh] = tr < rows;
+      etok[hh] = tok0 + (eok[hh] ? tr : 0);
+    }
+    if (p.vec_epi && p.gate) {
+#pragma unroll
+      for (int j = 0; j < NPT; ++j)
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh)
+          gw[j][hh] = *(const uint4*)((const uint16_t*)p.gate + etok[hh] * p.ldgate + (int64_t)h * p.P +
+                                      (pg * NPT + j) * 32 + ec0);
+    }
+    if (tb & 1) diag(g1);
+    else diag(g0);
 #pragma unroll
     for (int j = 0; j < NPT; ++j) {
       const int pt = pg * NPT + j;
@@ -655,42 +775,42 @@ __global__ void __launch_bounds__(256, 2) ssd_out2_kernel(SsdK p, const uint4* h
       unpk8(xs[((tb * 2 + 1) * PT + pt) * 64 + lane], xv + 8);
       const int64_t col = (int64_t)h * p.P + pt * 32 + r32;
       if (p.vec_epi) {
-        // C layout -> row-major tile in LDS -> 16 columns of one row per lane
-#pragma unroll
-        for (int r = 0; r < 16; ++r) ep[crow_of(r, lane) * kEpiStride + r32] = acc[j][r] + xv[r] * dh;
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        const int row = lane >> 1, c0 = 16 * (lane & 1);
-        float v[16];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const float4 f = *(const float4*)&ep[row * kEpiStride + c0 + 4 * q];
-          v[4 * q] = f.x; v[4 * q + 1] = f.y; v[4 * q + 2] = f.z; v[4 * q + 3] = f.w;
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        const int tr = tb * 32 + row;
-        const bool ok = tr < rows;
-        const int64_t tok = tok0 + (ok ? tr : 0);
+        // C layout -> row-major 16-row tile in LDS -> 8 columns of one row per
+        // lane; registers 8 hh .. 8 hh + 7 hold rows 16 hh .. 16 hh + 15
+        const int row = erow, c0 = ec0;
         const int64_t oc = (int64_t)h * p.P + pt * 32 + c0;
-        if (p.gate) {
-          const uint4* gp = (const uint4*)((const uint16_t*)p.gate + tok * p.ldgate + oc);
-          float gv[16];
-          unpk8(gp[0], gv);
-          unpk8(gp[1], gv + 8);
+        const bool* ok = eok;
+        const int64_t* tok = etok;
 #pragma unroll
-          for (int k2 = 0; k2 < 16; ++k2) v[k2] *= gv[k2];
-        }
-        if (ok) {
-          uint4* yp = (uint4*)((uint16_t*)p.y + tok * p.ldy + oc);
-          yp[0] = __builtin_bit_cast(uint4, pk8(v));
-          yp[1] = __builtin_bit_cast(uint4, pk8(v + 8));
-          if (p.y32) {
-            float4* y4 = (float4*)(p.y32 + tok * p.ldy32 + oc);
+        for (int hh = 0; hh < 2; ++hh) {
 #pragma unroll
-            for (int q = 0; q < 4; ++q) y4[q] = make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
+          for (int r = 0; r < 8; ++r)
+            ep[(crow_of(8 * hh + r, lane) - 16 * hh) * kEpiStride + r32] = acc[j][8 * hh + r] + xv[8 * hh + r] * dh;
+          __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+          __builtin_amdgcn_wave_barrier();
+          __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+          float v[8];
+#pragma unroll
+          for (int q = 0; q < 2; ++q) {
+            const float4 f = *(const float4*)&ep[row * kEpiStride + c0 + 4 * q];
+            v[4 * q] = f.x; v[4 * q + 1] = f.y; v[4 * q + 2] = f.z; v[4 * q + 3] = f.w;
+          }
+          __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+          __builtin_amdgcn_wave_barrier();
+          __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+          if (p.gate) {
+            float gv[8];
+            unpk8(gw[j][hh], gv);
+#pragma unroll
+            for (int k2 = 0; k2 < 8; ++k2) v[k2] *= gv[k2];
+          }
+          if (ok[hh]) {
+            *(uint4*)((uint16_t*)p.y + tok[hh] * p.ldy + oc) = __builtin_bit_cast(uint4, pk8(v));
+            if (p.y32) {
+              float4* y4 = (float4*)(p.y32 + tok[hh] * p.ldy32 + oc);
+              y4[0] = make_float4(v[0], v[1], v[2], v[3]);
+              y4[1] = make_float4(v[4], v[5], v[6], v[7]);
+            }
           }
         }
       } else {
@@ -818,7 +938,12 @@ __global__ void __launch_bounds__(256) conv1d_vec_kernel(ConvK p, int cg, int ru
 }
 
 static size_t state_lds(int P, int N) { return (size_t)(256 * 4 + 32 * P + 32 * N) * 4; }
-static size_t out2_lds(int Q, int P) { return 1024 * 4 + 4 * 32 * kEpiStride * 4 + (size_t)Q * P * 2; }
+// cl, dts | epilogue tiles (and the running sum's scratch) | x fragments |
+// carried state | triangular decay-weight table
+static size_t out2_lds(int Q, int P, int N) {
+  const size_t nt = Q / 32;
+  return 512 * 4 + 4 * 16 * kEpiStride * 4 + (size_t)Q * P * 2 + (size_t)P * N * 4 + 16 * nt * (nt - 1) * 4;
+}
 static size_t out_lds(int RB, int P, int N) {
   const size_t intra = (size_t)RB * (N + 1) + (size_t)RB * (P + 1) + (size_t)RB * (RB + 1);
   const size_t inter = (size_t)P * (N + 1);
@@ -901,8 +1026,8 @@ extern "C" int th_ssd_chunked(const th_ssd_desc* d, void* stream) {
   auto al16 = [](const void* q) { return ((uintptr_t)q & 15) == 0; };
   const bool mfma = d->dtype == TH_BF16 && (k.P == 32 || k.P == 64 || k.P == 128) &&
                     (k.N == 32 || k.N == 64 || k.N == 128) && k.Q % 32 == 0 && d->ld_x % 8 == 0 &&
-                    d->ld_b % 8 == 0 && d->ld_c % 8 == 0 && al16(d->x) && al16(d->b) && al16(d->c) &&
-                    out2_lds(k.Q, k.P) <= kMaxLds;
+                    d->ld_b % 8 == 0 && d->ld_c % 8 == 0 && d->ld_b < (1 << 22) && al16(d->x) && al16(d->b) && al16(d->c) &&
+                    out2_lds(k.Q, k.P, k.N) <= kMaxLds;
   if (mfma) {
     const int64_t bhc = (int64_t)k.B * k.H * k.nc;
     uint4* hf = (uint4*)(d->workspace + bhc * k.P * k.N + ssd_tot_floats(bhc));
@@ -917,7 +1042,7 @@ extern "C" int th_ssd_chunked(const th_ssd_desc* d, void* stream) {
       hipLaunchKernelGGL(ssd_carry2_kernel, dim3((unsigned)cdiv(k.P * k.N / 8, 256), k.H, k.B), dim3(256), 0, s, k, hf);
       TH_CHECK_LAUNCH();
     }
-    const size_t l3 = out2_lds(k.Q, k.P);
+    const size_t l3 = out2_lds(k.Q, k.P, k.N);
     // a full 8-block chunk gives every wave two t-blocks: share each G^T tile over
     // two p-tiles (more accumulators would not fit two waves per SIMD)
     const int npt = k.Q / 32 >= 8 ? std::min(PT, 2) : 1;
