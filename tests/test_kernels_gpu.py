@@ -226,25 +226,27 @@ def _quant_e4m3(w: torch.Tensor):
 @pytest.mark.parametrize("M,N,K,case", [(64, 4096, 4096, "add"), (64, 1024, 4096, "rope_kv"),
                                         (37, 2048, 1024, "swiglu"), (100, 512, 512, "acc"),
                                         (16, 1024, 2048, "add"), (20, 256, 992, "acc"),
-                                        (64, 14336, 512, "swiglu"), (32, 24576, 256, "rope_q")])
+                                        (64, 14336, 512, "swiglu"), (32, 24576, 256, "rope_q"),
+                                        (64, 1024, 4096, "rope_qk")])
 def test_gemm_fp8_weights(gpu, M, N, K, case):
     """bf16 activations x e4m3 weights with per-column scales (the decode projections), split-K,
     against fp32 math on the dequantised weights. K a multiple of 128 takes the shared-activation
     kernel (32-, 64- and 128-row variants here); K = 992 the per-wave split-K kernel. The two
     widest cases run as one split whose workgroups finish their tiles themselves (SwiGLU pairs
-    and RoPE partners inside a tile); the others go through the reduce pass."""
+    and RoPE partners inside a tile); the others go through the reduce pass. rope_qk rotates
+    both accumulators over the same columns: each output takes its own accumulator's partner."""
     from torch_helion.hip import abi, ops
 
     announce(f"gemm fp8 weights M={M} N={N} K={K} {case}")
     g = torch.Generator().manual_seed(M + N + K)
-    n_acc = {"add": 1, "rope_kv": 2, "swiglu": 2, "acc": 1, "rope_q": 1}[case]
+    n_acc = {"add": 1, "rope_kv": 2, "swiglu": 2, "acc": 1, "rope_q": 1, "rope_qk": 2}[case]
     x = torch.randn(M, K, generator=g).bfloat16()
     qs = [_quant_e4m3(torch.randn(K, N, generator=g) * 0.02) for _ in range(n_acc)]
     wdq = [q.float() * s[None, :] for q, s in qs]
     xf = x.float()
     accs = [xf @ w for w in wdq]
     kw = {}
-    if case in ("rope_kv", "swiglu", "rope_q"):
+    if case in ("rope_kv", "swiglu", "rope_q", "rope_qk"):
         r = ((xf * xf).sum(-1, keepdim=True) / K + 1e-5).pow(-0.5)
         accs = [a * r for a in accs]
         kw = dict(sumsq=True, rscale_mask=(1 << n_acc) - 1, inv_k=1.0 / K, eps=1e-5)
@@ -261,6 +263,13 @@ def test_gemm_fp8_weights(gpu, M, N, K, case):
         refs = [accs[0] * c1.repeat(M, N // hd) + _rot_heads(accs[0], hd) * s1.repeat(M, N // hd), accs[1]]
         kw.update(rope_cos=c1.to(gpu), rope_sin=s1.to(gpu), rope_head_dim=hd, rope_period=1)
         ops_ = [(abi.EPI_ROPE, 0, -1, -1), (abi.EPI_ACC, 1, -1, -1)]
+    elif case == "rope_qk":
+        hd, pos = 128, 300
+        cos, sin = _rope_tables(pos + 1, hd, theta=500000.0)
+        c1, s1 = cos[pos:pos + 1].contiguous(), sin[pos:pos + 1].contiguous()
+        refs = [a * c1.repeat(M, N // hd) + _rot_heads(a, hd) * s1.repeat(M, N // hd) for a in accs]
+        kw.update(rope_cos=c1.to(gpu), rope_sin=s1.to(gpu), rope_head_dim=hd, rope_period=1)
+        ops_ = [(abi.EPI_ROPE, 0, -1, -1), (abi.EPI_ROPE, 1, -1, -1)]
     elif case == "rope_q":
         hd, pos = 128, 77
         cos, sin = _rope_tables(pos + 1, hd, theta=10000.0)

@@ -1511,18 +1511,6 @@ extern "C" int th_gemm(const th_gemm_desc* d, void* stream) {
     }
   }
   k.n_out = d->n_out;
-  if (fp8) {
-    // the e4m3 epilogues gather one rotation partner per column group: every
-    // fused-RoPE output must rotate the same accumulator
-    int rope_acc = -1;
-    for (int o = 0; o < d->n_out; ++o) {
-      if (d->out[o].op != TH_EPI_ROPE) continue;
-      TH_CHECK_ARG(rope_acc < 0 || rope_acc == d->out[o].a,
-                   "th_gemm: fp8 weights: TH_EPI_ROPE outputs on different accumulators (%d, %d)", rope_acc,
-                   d->out[o].a);
-      rope_acc = d->out[o].a;
-    }
-  }
   if (need_rope) {
     TH_CHECK_ARG(d->rope_cos && d->rope_sin, "th_gemm: RoPE output without cos/sin tables");
     TH_CHECK_ARG(d->rope_head_dim >= 4 && d->rope_head_dim % 8 == 0 && d->N % d->rope_head_dim == 0,

@@ -280,19 +280,22 @@ __device__ __forceinline__ void fp8_emit4(const Fp8K& p, int64_t m, int64_t n4, 
   // gather (the shared-activation kernel's packings have one or two accumulators)
   const float4 c0 = sum4(0, n4);
   const float4 c1 = g.n_acc > 1 ? sum4(1, n4) : c0;
-  int rope_a = -1;
+  // the rotation partner of each accumulator some ROPE output here reads
+  bool rope_acc[2] = {false, false};
   bool tab = false;
   for (int o = 0; o < g.n_out; ++o) {
     const EpiOutK& eo = g.out[o];
     if (n4 < eo.cb || n4 >= eo.ce) continue;
-    if (eo.op == TH_EPI_ROPE) rope_a = eo.a;
+    if (eo.op == TH_EPI_ROPE) rope_acc[eo.a & 1] = true;
     if (eo.op == TH_EPI_ROPE || eo.op == TH_EPI_ROPE_PAIR) tab = true;
   }
   const int within = g.hd > 0 ? (int)n4 % g.hd : 0;
   const int half = g.hd >> 1;
-  float4 rot = make_float4(0.f, 0.f, 0.f, 0.f);
-  if (rope_a >= 0) rot = sum4(rope_a, within < half ? n4 + half : n4 - half);
-  float4 cs = rot, sn = rot;
+  const int64_t pn = within < half ? n4 + half : n4 - half;
+  const float4 zero4 = make_float4(0.f, 0.f, 0.f, 0.f);
+  const float4 rot0 = rope_acc[0] ? sum4(0, pn) : zero4;
+  const float4 rot1 = rope_acc[1] ? sum4(1, pn) : zero4;
+  float4 cs = zero4, sn = zero4;
   if (tab) {
     const int toff = ((int)m % g.period) * g.hd + within;
     cs = make_float4(g.rcos[toff], g.rcos[toff + 1], g.rcos[toff + 2], g.rcos[toff + 3]);
@@ -328,7 +331,7 @@ __device__ __forceinline__ void fp8_emit4(const Fp8K& p, int64_t m, int64_t n4, 
         float4 r;
         if (eo.op == TH_EPI_ROPE) {
           const float sg = within < half ? -1.f : 1.f;
-          r = scl(rot, ((g.rscale_mask >> eo.a) & 1u) ? sg * rr : sg);
+          r = scl(eo.a == 1 ? rot1 : rot0, ((g.rscale_mask >> eo.a) & 1u) ? sg * rr : sg);
         } else {
           r = ((g.rscale_mask >> eo.b) & 1u) ? scl(sel(eo.b), rr) : sel(eo.b);
         }
