@@ -283,8 +283,8 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_bf16_kernel(AttnK p) {
     if (qr >= p.Sq) continue;
     const float4 x = *(const float4*)(ostage + r * OROW + c4);
     uint2 w;
-    w.x = (uint32_t)f32_to_bf16(x.x) | ((uint32_t)f32_to_bf16(x.y) << 16);
-    w.y = (uint32_t)f32_to_bf16(x.z) | ((uint32_t)f32_to_bf16(x.w) << 16);
+    w.x = pk_bf16x2(x.x, x.y);
+    w.y = pk_bf16x2(x.z, x.w);
     *(uint2*)(obase + (int64_t)qr * p.ldo + c4) = w;
   }
 }

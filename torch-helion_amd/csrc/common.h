@@ -76,11 +76,20 @@ __device__ __forceinline__ float bf16_to_f32(uint16_t h) {
 }
 
 // Round-to-nearest-even fp32 -> bf16 (what torch's .to(bfloat16) does; NaN
-// stays a quiet NaN). The cast compiles to gfx950's v_cvt_pk_bf16_f32, one
-// instruction per pair of values: epilogues are VALU-bound, and the bit
-// arithmetic this replaces took about six instructions per value.
+// stays a quiet NaN). The cast compiles to gfx950's v_cvt_pk_bf16_f32 (see
+// pk_bf16x2 for a pair in one instruction): epilogues are VALU-bound, and the
+// bit arithmetic this replaces took about six instructions per value.
 __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
   return __builtin_bit_cast(uint16_t, (__bf16)f);
+}
+
+// Two fp32 -> one packed bf16 pair (a in the low half), round to nearest even,
+// in one v_cvt_pk_bf16_f32 (two single casts cost a shift and an OR besides).
+__device__ __forceinline__ uint32_t pk_bf16x2(float a, float b) {
+  typedef float f2_t __attribute__((ext_vector_type(2)));
+  typedef __bf16 b2_t __attribute__((ext_vector_type(2)));
+  const f2_t v = {a, b};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, b2_t));
 }
 
 __device__ __forceinline__ float load_elem(const void* p, int64_t i, int dtype) {

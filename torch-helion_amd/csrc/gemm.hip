@@ -86,10 +86,10 @@ __device__ __forceinline__ void store8(void* p, int64_t off, int dtype, bool vec
   if (vec8 && valid >= 8) {
     if (dtype == TH_BF16) {
       uint4 w;
-      w.x = (uint32_t)f32_to_bf16(v[0]) | ((uint32_t)f32_to_bf16(v[1]) << 16);
-      w.y = (uint32_t)f32_to_bf16(v[2]) | ((uint32_t)f32_to_bf16(v[3]) << 16);
-      w.z = (uint32_t)f32_to_bf16(v[4]) | ((uint32_t)f32_to_bf16(v[5]) << 16);
-      w.w = (uint32_t)f32_to_bf16(v[6]) | ((uint32_t)f32_to_bf16(v[7]) << 16);
+      w.x = pk_bf16x2(v[0], v[1]);
+      w.y = pk_bf16x2(v[2], v[3]);
+      w.z = pk_bf16x2(v[4], v[5]);
+      w.w = pk_bf16x2(v[6], v[7]);
       *(uint4*)((uint16_t*)p + off) = w;
     } else {
       *(float4*)((float*)p + off) = make_float4(v[0], v[1], v[2], v[3]);

@@ -82,8 +82,8 @@ __device__ __forceinline__ void store4(void* p, int64_t off, int dtype, bool vec
   if (vec && valid >= 4) {
     if (dtype == TH_BF16) {
       uint2 w;
-      w.x = (uint32_t)f32_to_bf16(v.x) | ((uint32_t)f32_to_bf16(v.y) << 16);
-      w.y = (uint32_t)f32_to_bf16(v.z) | ((uint32_t)f32_to_bf16(v.w) << 16);
+      w.x = pk_bf16x2(v.x, v.y);
+      w.y = pk_bf16x2(v.z, v.w);
       *(uint2*)((uint16_t*)p + off) = w;
     } else {
       *(float4*)((float*)p + off) = v;

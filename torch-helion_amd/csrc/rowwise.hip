@@ -97,10 +97,10 @@ __global__ void __launch_bounds__(256) rmsnorm_kernel(NormK p) {
       uint16_t* orow = (uint16_t*)p.out + row * p.ldo + base;
       if constexpr (XB) {
         uint4 o;
-        o.x = (uint32_t)f32_to_bf16(v[0]) | ((uint32_t)f32_to_bf16(v[1]) << 16);
-        o.y = (uint32_t)f32_to_bf16(v[2]) | ((uint32_t)f32_to_bf16(v[3]) << 16);
-        o.z = (uint32_t)f32_to_bf16(v[4]) | ((uint32_t)f32_to_bf16(v[5]) << 16);
-        o.w = (uint32_t)f32_to_bf16(v[6]) | ((uint32_t)f32_to_bf16(v[7]) << 16);
+        o.x = pk_bf16x2(v[0], v[1]);
+        o.y = pk_bf16x2(v[2], v[3]);
+        o.z = pk_bf16x2(v[4], v[5]);
+        o.w = pk_bf16x2(v[6], v[7]);
         *(uint4*)orow = o;
       } else {
 #pragma unroll

@@ -919,10 +919,10 @@ __global__ void __launch_bounds__(256) conv1d_vec_kernel(ConvK p, int cg, int ru
     const int64_t tok = base + t;
     if (p.ydt == TH_BF16) {
       uint4 o;
-      o.x = (uint32_t)f32_to_bf16(acc[0]) | ((uint32_t)f32_to_bf16(acc[1]) << 16);
-      o.y = (uint32_t)f32_to_bf16(acc[2]) | ((uint32_t)f32_to_bf16(acc[3]) << 16);
-      o.z = (uint32_t)f32_to_bf16(acc[4]) | ((uint32_t)f32_to_bf16(acc[5]) << 16);
-      o.w = (uint32_t)f32_to_bf16(acc[6]) | ((uint32_t)f32_to_bf16(acc[7]) << 16);
+      o.x = pk_bf16x2(acc[0], acc[1]);
+      o.y = pk_bf16x2(acc[2], acc[3]);
+      o.z = pk_bf16x2(acc[4], acc[5]);
+      o.w = pk_bf16x2(acc[6], acc[7]);
       *(uint4*)((uint16_t*)p.y + tok * p.ldy + ch) = o;
     } else {
       float* yo = (float*)p.y + tok * p.ldy + ch;
