@@ -427,6 +427,29 @@ def test_mamba_lm_c4_shapes_two_layers(gpu, tmp_path):
     assert rel < 2e-2, (rel, mx)
 
 
+def test_mamba_lm_merged_in_projection_activation_gain(gpu, tmp_path):
+    """norm_gain='activation' with merge_siblings=True: the in-projection GEMMs unfold the same
+    norm gain, so they merge into one launch over the unfolded weights behind one shared
+    normalised-lhs launch; the logits match the separate launches (each output column is the
+    same dot product in the same K order)."""
+    from targets.mamba import build_mamba_model, config_c4
+
+    announce("e2e mamba lm merged in-projection, activation-side gain")
+    cfg = config_c4()
+    cfg.n_layers, cfg.batch, cfg.seq, cfg.vocab = 2, 1, 512, 4096
+    m = build_mamba_model(cfg, seed=0)
+    ids = m.example_inputs(seed=0)
+    kw = dict(device_check=False, fp32_outputs=False, norm_gain="activation")
+    sep = _compile(m, ids, tmp_path, "lm_sep", merge_siblings=False, **kw)
+    mer = _compile(m, ids, tmp_path, "lm_mer", merge_siblings=True, **kw)
+    merged = [l for l in mer.device_program.launches if "+" in l.kernel and l.entry == "th_gemm"]
+    assert len(merged) == 2 and all(l.info["gain_on_activation"] for l in merged), \
+        [l.kernel for l in mer.device_program.launches]
+    a = sep.run(*ids)[0].float().cpu()
+    b = mer.run(*ids)[0].float().cpu()
+    assert (a - b).abs().max().item() / a.abs().max().item() < 1e-3
+
+
 def test_llama_block_c3_full(gpu, tmp_path):
     """BASELINE config 2 (C3) at its full size: Llama-3-8B-shaped block, bf16, B=8, S=2048,
     32/8 heads x 128, FFN 14336, causal, through compile_model. Sequence 0 of the output (its

@@ -648,7 +648,8 @@ class DeviceProgram:
         lhs is bf16. None otherwise (the kernel then runs as folded)."""
         if not self.fold_sources or plan.rscale is None or not used:
             return None
-        if self.buffers[spec.arg("lhs").tensor].dtype != torch.bfloat16:
+        # (the declared dtype: the merge planner asks before buffers are bound)
+        if self.program.tensors[spec.arg("lhs").tensor].dtype != "bfloat16":
             return None
         tens = [spec.arg(spec.gemms[i].rhs).tensor for i in used]
         if any(t not in self.fold_sources for t in tens) or not all(plan.scaled.get(i, False) for i in used):
@@ -701,14 +702,19 @@ class DeviceProgram:
         used = sorted({o.a for o in plan.outs})
         if any(k.arg(k.gemms[a].rhs).tensor not in self.program.params for a in used):
             return None
-        # a weight with its norm gain folded in runs on the normalised activations
-        # and the unfolded weight (_lower_gemm_fused); the merged launch would not
+        # A weight with its norm gain folded in runs on the normalised activations
+        # and the unfolded weight (_lower_gemm_fused): such kernels merge only with
+        # kernels that unfold the same gain, and the merged launch does the same.
+        unfold = None
         if any(k.arg(k.gemms[a].rhs).tensor in self.fold_sources for a in used):
-            return None
+            g = self._unfold_gain(k, plan, used)
+            if g is None:
+                return None
+            unfold = g.data_ptr()
         flags = {bool(plan.scaled.get(a, False)) for a in used}
         if len(flags) != 1:
             return None
-        return (lhs_t, k.k_extent, plan.rscale, flags.pop()), plan, used
+        return (lhs_t, k.k_extent, plan.rscale, flags.pop(), unfold), plan, used
 
     def _plan_sibling_merges(self, program: Program):
         """Leader kernel name -> [(spec, plan, used accumulators)] in launch
@@ -743,16 +749,23 @@ class DeviceProgram:
 
     def _lower_gemm_merged(self, members) -> list[Launch]:
         lead = members[0][0]
-        lhs = self.buffers[lead.arg("lhs").tensor]
+        lhs_t = lead.arg("lhs").tensor
+        lhs = self.buffers[lhs_t]
         T, K = lead.grid["rows"], lead.k_extent
         plan0 = members[0][1]
+        # (every member unfolds the same gain, or none does: it is part of the merge key)
+        gain = self._unfold_gain(lead, plan0, members[0][2])
+        norm_launch = None
+        if gain is not None:
+            norm_launch, lhs = self._normed_lhs(lead, lhs_t, gain, plan0.rscale)
         cols: dict[tuple[str, int], tuple[int, int]] = {}
         weights: list[torch.Tensor] = []
         n_tot = 0
         for spec, plan, used in members:
             n = spec.grid["cols"]
             for a in used:
-                w = self.buffers[spec.arg(spec.gemms[a].rhs).tensor]
+                t = spec.arg(spec.gemms[a].rhs).tensor
+                w = self.fold_sources[t][1].to(self.device) if gain is not None else self.buffers[t]
                 weights.append(w if w.dtype in (torch.float32, torch.bfloat16) else w.float())
                 cols[(spec.name, a)] = (n_tot, n_tot + n)
                 n_tot += n
@@ -772,18 +785,22 @@ class DeviceProgram:
         extra_bufs = [self.operand(t) for t in extras]
         scaled = bool(plan0.scaled.get(members[0][2][0], False))
         inv_k, eps = plan0.rscale if plan0.rscale else (0.0, 0.0)
+        sumsq = plan0.rscale is not None
+        if gain is not None:  # the row scale is inside the normalised lhs
+            scaled, sumsq = False, False
         names = [m[0].name for m in members]
         info = {"n_acc": 1, "merged": names, "cols": n_tot, "ops": [x.op for x in epi], "rscale": plan0.rscale is not None,
-                "rope_fused": False}
+                "rope_fused": False, "gain_on_activation": gain is not None}
 
         def run() -> None:
-            ops.gemm(ops.GemmCall(T, n_tot, K, 1, lhs, packed, epi, sumsq=plan0.rscale is not None,
+            ops.gemm(ops.GemmCall(T, n_tot, K, 1, lhs, packed, epi, sumsq=sumsq,
                                   rscale_mask=1 if scaled else 0, inv_k=inv_k, eps=eps, extras=extra_bufs),
                      kernel="+".join(names))
 
         for n in names:
             self.plans[n] = info
-        return [Launch("+".join(names), "gemm", run, "th_gemm", info)]
+        launch = Launch("+".join(names), "gemm", run, "th_gemm", info)
+        return [norm_launch, launch] if norm_launch is not None else [launch]
 
     # generic path ---------------------------------------------------------
     def _lower_gemm_vm(self, spec: KernelSpec) -> list[Launch]:
