@@ -245,7 +245,10 @@ int th_attention_decode(const th_decode_desc* desc, void* stream);
  *   y_t = sum_{s<=t} (C_t . B_s) exp(cum_t - cum_s) dt_s x_s + D_h x_t  [* gate_t]
  * evaluated chunk by chunk (states of each chunk, an inter-chunk carry, then
  * the outputs) with every exponent a difference of running sums inside one
- * chunk or between chunk ends, so nothing overflows at any length.
+ * chunk or between chunk ends, so nothing overflows at any length. (The
+ * bf16 path splits some of these differences in two at a block boundary,
+ * which keeps both parts <= 0 when dt*A <= 0 everywhere, as Mamba's
+ * A = -exp(A_log) and dt = softplus(.) guarantee.)
  * Two operand forms:
  *   ssd_chunked kind (new): cum = running sum of dt*A, with dt [T, H] and A [H];
  *   ssd kind (reference: optimizer/evaluate.py:123-138, codegen/emit.py:254-324):
