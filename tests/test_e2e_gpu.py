@@ -350,6 +350,9 @@ def test_compile_model_decode_fp8_vs_oracle(gpu, tmp_path, which):
     assert all(prog.tensors[k.arg(g.rhs).tensor].dtype == "float8_e4m3fn" for k in prog.kernels
                if k.kind == "gemm" for g in k.gemms)
     dp = res.device_program
+    # q and k|v read the same input: one e4m3 launch over both, on column windows
+    assert any(l.info.get("weights") == "float8_e4m3fn" and len(l.info.get("merged", [])) == 2
+               for l in dp.launches), [l.kernel for l in dp.launches]
     dp.run([x, kc, vc])
     torch.cuda.synchronize()
     out, k_dev, v_dev = (t.double().cpu() for t in dp.outputs(fp32=True))

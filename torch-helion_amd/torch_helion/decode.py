@@ -171,7 +171,8 @@ def compile_decode(model, example_args, config):
         from .hip.runtime import DeviceProgram
 
         device_program = DeviceProgram(prog, params, config.device, fp32_outputs=config.fp32_outputs,
-                                       residual_fp32=config.residual_fp32, reuse_buffers=config.reuse_buffers)
+                                       residual_fp32=config.residual_fp32, reuse_buffers=config.reuse_buffers,
+                                       merge_siblings=config.merge_siblings)
         rw.write_json("kernels/launches.json", [{"kernel": l.kernel, "entry": l.entry, "info": l.info}
                                                 for l in device_program.launches])
     validation: dict[str, Any] = {}

@@ -174,12 +174,13 @@ class DeviceProgram:
         if merge_siblings is None:  # small row counts: launches, not tiles, set the time
             merge_siblings = all(k.grid.get("rows", 0) <= 4096 for k in program.kernels if k.kind == "gemm")
         self._merge_groups, self._merged_away = self._plan_sibling_merges(program) if merge_siblings else ({}, set())
+        self._fp8_groups = self._plan_fp8_merges(program, self._merged_away) if merge_siblings else {}
         for i, k in enumerate(program.kernels):
             self._cur = i
             if self.reuse:
                 self._pool.release_before(i)
                 self._bind_outputs(k)
-                for m in self._merge_groups.get(k.name, [])[1:]:
+                for m in (self._merge_groups.get(k.name) or self._fp8_groups.get(k.name) or [])[1:]:
                     self._bind_outputs(m[0])
             if k.name in self._merged_away:
                 continue
@@ -190,6 +191,12 @@ class DeviceProgram:
                 continue  # runs with its group, at the group's last member
             if k.name in self._merge_groups:
                 self.launches.extend(self._lower_gemm_merged(self._merge_groups[k.name]))
+            elif k.name in self._fp8_groups:
+                members = [m[0] for m in self._fp8_groups[k.name]]
+                merged = self._lower_fp8_merged(members)
+                if merged is None:  # the parts disagree: each member at the leader's position
+                    merged = [x for m in members for x in self._lower(m)]
+                self.launches.extend(merged)
             else:
                 self.launches.extend(self._lower(k))
 
@@ -514,7 +521,9 @@ class DeviceProgram:
                 return Launch(spec.name, "rmsnorm", run, "th_rmsnorm", {"inv_k": inv_k, "eps": eps})
         return None
 
-    def _lower_gemm_fused(self, spec: KernelSpec, plan: EpiloguePlan) -> list[Launch] | None:
+    def _lower_gemm_fused(self, spec: KernelSpec, plan: EpiloguePlan, collect: list | None = None) -> list[Launch] | None:
+        """The fused th_gemm launch of this kernel (None: the epilogue needs the VM).
+        ``collect``: append the call's parts there instead (for a merged launch)."""
         T, N, K = spec.grid["rows"], spec.grid["cols"], spec.k_extent
         lhs_t = spec.arg("lhs").tensor
         lhs = self.buffers[lhs_t]
@@ -630,6 +639,13 @@ class DeviceProgram:
                 # activation-side norm gain: the products see lhs * g, the sum of squares lhs
                 fp8_kw["lhs_gain"] = self.buffers[spec.arg("gain").tensor].float().reshape(-1).contiguous()
             info.update({"weights": "float8_e4m3fn", "lhs_gain": "gain" in names})
+
+        if collect is not None:
+            collect.append(dict(T=T, N=N, K=K, lhs=lhs, fp8=fp8, rhs=[spec.arg(rhs_of[i]).tensor for i in used],
+                                scales=[spec.arg(rhs_of[i] + "_scale").tensor for i in used] if fp8 else [],
+                                epi=epi, mask=mask, n_used=len(used), sumsq=sumsq, inv_k=inv_k, eps=eps, rope=rope,
+                                extras=extra_bufs, lhs_gain=fp8_kw.get("lhs_gain"), norm=norm_launch, info=info))
+            return []
 
         def run() -> None:
             call = ops.GemmCall(T, N, K, len(used), lhs, get_packed(), epi, sumsq=sumsq,
@@ -801,6 +817,108 @@ class DeviceProgram:
             self.plans[n] = info
         launch = Launch("+".join(names), "gemm", run, "th_gemm", info)
         return [norm_launch, launch] if norm_launch is not None else [launch]
+
+    # e4m3 sibling merge (decode programs): GEMM kernels with e4m3 weights that
+    # read the same lhs (q and k|v of the decode step) run as ONE th_gemm over
+    # the concatenated weights and scales, each output on its own column window
+    # (fused RoPE included: a head never straddles two windows), with one
+    # activation-gain pre-pass and one reduce pass instead of one per kernel.
+    def _plan_fp8_merges(self, program: Program, away: set[str]):
+        produced_at = {o.tensor: i for i, k in enumerate(program.kernels) for o in k.outputs}
+
+        def key(k: KernelSpec):
+            if k.kind != "gemm" or not k.gemms:
+                return None
+            if any(self.program.tensors[k.arg(g.rhs).tensor].dtype != "float8_e4m3fn" for g in k.gemms):
+                return None
+            return (k.arg("lhs").tensor, k.k_extent, k.grid["rows"])
+
+        groups: dict[str, list] = {}
+        for i, k in enumerate(program.kernels):
+            ki = key(k)
+            if ki is None or k.name in away:
+                continue
+            members = [k]
+            for j in range(i + 1, len(program.kernels)):
+                k2 = program.kernels[j]
+                if k2.name in away or key(k2) != ki:
+                    continue
+                # every other operand exists before the leader runs (params, program
+                # inputs and constants, or an earlier kernel's output)
+                ins = {a.tensor for a in k2.args if a.name != "lhs"}
+                if all(produced_at.get(t, -1) < i for t in ins):
+                    members.append(k2)
+            if len(members) > 1:
+                groups[k.name] = [(m, None, None) for m in members]
+                away.update(m.name for m in members[1:])
+        return groups
+
+    def _lower_fp8_merged(self, members: list[KernelSpec]) -> list[Launch] | None:
+        """One th_gemm for these e4m3 kernels, or None when their parts disagree
+        (lhs, row scale, gain, RoPE tables) or an output needs a second accumulator
+        or an extra operand."""
+        parts = []
+        for spec in members:
+            plan = match_epilogue(spec)
+            col: list = []
+            if not plan.fused or self._lower_gemm_fused(spec, plan, collect=col) is None or not col:
+                return None
+            parts.append((spec, col[0]))
+        p0 = parts[0][1]
+        for spec, pt in parts:
+            if not pt["fp8"] or pt["lhs"] is not p0["lhs"] or pt["extras"] or pt["norm"] is not None:
+                return None
+            if (pt["T"], pt["K"], pt["sumsq"], pt["inv_k"], pt["eps"]) != (p0["T"], p0["K"], p0["sumsq"], p0["inv_k"], p0["eps"]):
+                return None
+            if pt["mask"] not in (0, (1 << pt["n_used"]) - 1) or bool(pt["mask"]) != bool(p0["mask"]):
+                return None
+            if (pt["lhs_gain"] is None) != (p0["lhs_gain"] is None) or \
+                    (pt["lhs_gain"] is not None and not torch.equal(pt["lhs_gain"], p0["lhs_gain"])):
+                return None
+            r, r0 = pt["rope"], p0["rope"]
+            if r is not None and r0 is not None:
+                if r[2:] != r0[2:] or not torch.equal(r[0], r0[0]) or not torch.equal(r[1], r0[1]):
+                    return None
+            if any(e.b >= 0 or e.e >= 0 or e.cols is not None for e in pt["epi"]):
+                return None
+        rope = next((pt["rope"] for _, pt in parts if pt["rope"] is not None), None)
+        T, K = p0["T"], p0["K"]
+        ws_: list[torch.Tensor] = []
+        scales: list[torch.Tensor] = []
+        epi = []
+        n_tot = 0
+        for spec, pt in parts:
+            win = {}
+            for slot, (t, st) in enumerate(zip(pt["rhs"], pt["scales"])):
+                ws_.append(self.buffers[t].view(torch.uint8))
+                scales.append(self.buffers[st].float().reshape(-1))
+                win[slot] = (n_tot, n_tot + pt["N"])
+                n_tot += pt["N"]
+            for e in pt["epi"]:
+                epi.append(ops.EpiSpec(e.op, e.out, a=0, cols=win[e.a]))
+        if len(epi) > abi.MAX_OUT:
+            return None
+        packed = ops.pack_rhs([torch.cat(ws_, dim=1).view(_FP8).contiguous()], _FP8)
+        scale = torch.cat(scales).reshape(1, -1).contiguous()
+        ws = self._workspace(max(ops.gemm_workspace_bytes(T, n_tot, K, 1, _FP8), 16), torch.uint8)
+        names = [spec.name for spec, _ in parts]
+        info = {"n_acc": 1, "merged": names, "cols": n_tot, "ops": [x.op for x in epi], "rscale": p0["sumsq"],
+                "rope_fused": rope is not None, "weights": "float8_e4m3fn", "lhs_gain": p0["lhs_gain"] is not None}
+        lhs, gain = p0["lhs"], p0["lhs_gain"]
+        kw = dict(sumsq=p0["sumsq"], rscale_mask=1 if p0["mask"] else 0, inv_k=p0["inv_k"], eps=p0["eps"],
+                  in_dtype=_FP8, rhs_scale=scale, workspace=ws)
+        if gain is not None:
+            kw["lhs_gain"] = gain
+
+        def run() -> None:
+            call = ops.GemmCall(T, n_tot, K, 1, lhs, packed, epi, **kw)
+            if rope is not None:
+                call.rope_cos, call.rope_sin, call.rope_period, call.rope_head_dim = rope[0], rope[1], rope[2], rope[3]
+            ops.gemm(call, kernel="+".join(names))
+
+        for n in names:
+            self.plans[n] = info
+        return [Launch("+".join(names), "gemm", run, "th_gemm", info)]
 
     # generic path ---------------------------------------------------------
     def _lower_gemm_vm(self, spec: KernelSpec) -> list[Launch]:
