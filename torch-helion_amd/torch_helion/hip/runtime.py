@@ -605,7 +605,9 @@ class DeviceProgram:
         if gain is not None:
             norm_launch, normed = self._normed_lhs(spec, lhs_t, gain, plan.rscale)
             lhs = normed
-        get_packed = self._pack(spec, [rhs_of[i] for i in used], in_dtype, unfold=gain is not None)
+        # (a merged launch packs its own concatenated weights)
+        get_packed = self._pack(spec, [rhs_of[i] for i in used], in_dtype, unfold=gain is not None) \
+            if collect is None else None
         extra_bufs = [self.operand(spec.arg(x).tensor) for x in extras]
         epi = []
         for o, op, a, b, key in outs:
@@ -633,7 +635,8 @@ class DeviceProgram:
             if any(x not in names for x in scale_t):
                 raise _err(spec.name, "e4m3 weights without their <rhs>_scale arguments")
             scale = torch.stack([self.buffers[spec.arg(x).tensor].float().reshape(-1) for x in scale_t]).contiguous()
-            ws = self._workspace(max(ops.gemm_workspace_bytes(T, N, K, len(used), _FP8), 16), torch.uint8)
+            ws = self._workspace(max(ops.gemm_workspace_bytes(T, N, K, len(used), _FP8), 16), torch.uint8) \
+                if collect is None else None
             fp8_kw = dict(in_dtype=_FP8, rhs_scale=scale, workspace=ws)
             if "gain" in names:
                 # activation-side norm gain: the products see lhs * g, the sum of squares lhs
