@@ -53,7 +53,8 @@ def attention(q, k, v, causal: bool) -> torch.Tensor:
 
 def block_forward(x: torch.Tensor, w: dict[str, torch.Tensor], *, heads: int, kv_heads: int, eps: float,
                   theta: float, causal: bool, rope: tuple[torch.Tensor, torch.Tensor] | None = None,
-                  dtype=torch.float64, storage: torch.dtype | None = None) -> torch.Tensor:
+                  dtype=torch.float64, storage: torch.dtype | None = None,
+                  round_residual: bool = False) -> torch.Tensor:
     """x [b, s, D] -> [b, s, D], computed in ``dtype``.
 
     ``rope`` overrides the cos/sin tables (e.g. with the model's own buffers,
@@ -64,7 +65,10 @@ def block_forward(x: torch.Tensor, w: dict[str, torch.Tensor], *, heads: int, kv
     the residual stream where the MLP reads it as a GEMM operand and the
     SwiGLU product -- while the residual additions and the output stay in
     ``dtype``. This is the arithmetic of a bf16 block whose kernels
-    accumulate in fp32, the bar a device result is compared against."""
+    accumulate in fp32, the bar a device result is compared against.
+    ``round_residual`` (with ``storage``) also rounds the residual stream after
+    the attention's residual addition and the block output: a program that
+    keeps no fp32 copy of the residual stream and returns the model dtype."""
     w = {k: v.to(dtype) for k, v in w.items()}
     x = x.to(dtype)
     b, s, dm = x.shape
@@ -81,11 +85,13 @@ def block_forward(x: torch.Tensor, w: dict[str, torch.Tensor], *, heads: int, kv
     v = rnd(v)
     a = rnd(attention(q, k, v, causal).transpose(1, 2).reshape(b, s, heads * hd))
     x = x + a @ w["attn.o_proj.weight"].T
+    if round_residual:
+        x = rnd(x)
     h2 = rms_norm(rnd(x), w["post_norm.weight"], eps)
     gate = h2 @ w["mlp.gate_proj.weight"].T
     up = h2 @ w["mlp.up_proj.weight"].T
     mlp = rnd(gate * torch.sigmoid(gate) * up) @ w["mlp.down_proj.weight"].T
-    return x + mlp
+    return rnd(x + mlp) if round_residual else x + mlp
 
 
 def decode_step(x: torch.Tensor, w: dict[str, torch.Tensor], k_cache: torch.Tensor, v_cache: torch.Tensor, pos: int,

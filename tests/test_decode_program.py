@@ -119,3 +119,31 @@ def test_decode_kernel_files(case):
     cfg, m, inputs, res = case
     plans = {p.name for p in res.kernel_files.values()}
     assert any("attention_decode" in p for p in plans)
+
+
+@pytest.mark.parametrize("mistake", ["one_unfolded", "different_gain"])
+def test_decode_program_refuses_inconsistent_gains(case, monkeypatch, tmp_path, mistake):
+    """A kernel whose GEMM weights do not all carry the same folded norm gain is refused: one
+    gain argument multiplies the kernel's shared lhs, so a weight folded without it (or with
+    another gain) would be computed wrongly without any error."""
+    import torch_helion.decode as dec
+
+    cfg, m, inputs, res = case
+    pair = next(k for k in res.program.kernels if len(k.gemms) == 2 and any(a.role == "gain" for a in k.args))
+    t2 = pair.arg(pair.gemms[1].rhs).tensor
+    real = dec._prefill_form
+
+    def mutated(model, batch, config, run_dir):
+        pre = real(model, batch, config, run_dir)
+        folds = pre.graph.fold_sources
+        assert t2 in folds
+        if mistake == "one_unfolded":
+            pre.graph.params[t2] = folds.pop(t2)[1]   # the model's own weight, no gain folded in
+        else:
+            g, w = folds[t2]
+            folds[t2] = (g * 2, w)
+        return pre
+
+    monkeypatch.setattr(dec, "_prefill_form", mutated)
+    with pytest.raises(ValueError, match="gain"):
+        dec.decode_program(m, cfg.batch, res.config, tmp_path)

@@ -7,6 +7,8 @@ float32 on the same (bf16) weights and inputs.
 
 from __future__ import annotations
 
+import functools
+
 import pytest
 import torch
 
@@ -15,13 +17,13 @@ from conftest import announce
 pytestmark = pytest.mark.gpu
 
 
-def _oracle(model, cfg, x, dtype, storage=None):
+def _oracle(model, cfg, x, dtype, storage=None, round_residual=False):
     from oracle.llama import block_forward
 
     w = {k: v.detach().to(dtype) for k, v in model.state_dict().items() if not k.startswith(("rope", "attn_bias"))}
     return block_forward(x.to(dtype), w, heads=cfg.heads, kv_heads=cfg.n_kv, eps=cfg.eps, theta=cfg.rope_theta,
                          causal=cfg.causal, rope=(model.rope_cos.to(dtype), model.rope_sin.to(dtype)), dtype=dtype,
-                         storage=storage)
+                         storage=storage, round_residual=round_residual)
 
 
 def _compile(model, x, tmp_path, name, **cfg):
@@ -453,80 +455,109 @@ def test_mamba_lm_merged_in_projection_activation_gain(gpu, tmp_path):
     assert (a - b).abs().max().item() / a.abs().max().item() < 1e-3
 
 
-def test_llama_block_c3_full(gpu, tmp_path):
+@pytest.mark.parametrize("fp32_copies", [True, False])
+def test_llama_block_c3_full(gpu, tmp_path, fp32_copies):
     """BASELINE config 2 (C3) at its full size: Llama-3-8B-shaped block, bf16, B=8, S=2048,
-    32/8 heads x 128, FFN 14336, causal, through compile_model. Sequence 0 of the output (its
-    fp32 copy) against the oracle in float64: normalised error <= 2e-2, and max-abs at most
-    twice the bf16 floor (the same block storing q, k, v, the attention output, the MLP's
-    residual operand and the SwiGLU product in bf16, against the unrounded block)."""
+    32/8 heads x 128, FFN 14336, causal, through compile_model. Sequence 0 of the output
+    against the oracle in float64: normalised error <= 2e-2, and max-abs at most twice the bf16
+    floor (the same block storing q, k, v, the attention output, the MLP's residual operand and
+    the SwiGLU product in bf16, against the unrounded block).
+    Both storage variants: fp32 copies of the residual stream and the output (the compiled
+    default; the output's fp32 copy is compared), and none (residual_fp32=False,
+    fp32_outputs=False: the program bench.py times), whose bf16 output is compared against a
+    floor that also rounds the residual stream and the output to bf16."""
     from targets.llama_block import build_llama_block, config_c3
 
-    announce("e2e llama C3 full size (B=8, S=2048)")
+    announce(f"e2e llama C3 full size (B=8, S=2048), fp32 copies {fp32_copies}")
     cfg = config_c3()
     model = build_llama_block(cfg, seed=0)
     x = model.example_inputs(seed=0)
-    res = _compile(model, x, tmp_path, "c3_full", device_check=False, reference_check=False, verify_passes=False)
+    res = _compile(model, x, tmp_path, "c3_full", device_check=False, reference_check=False, verify_passes=False,
+                   residual_fp32=fp32_copies, fp32_outputs=fp32_copies)
     res.device_program.run(list(x))
     torch.cuda.synchronize()
-    out = res.device_program.outputs(fp32=True)[0].reshape(cfg.batch, cfg.seq, cfg.hidden)[0].double().cpu()
+    out = res.device_program.outputs(fp32=fp32_copies)[0].reshape(cfg.batch, cfg.seq, cfg.hidden)[0].double().cpu()
     x0 = x[0][:1]
     ref = _oracle(model, cfg, x0, torch.float64)[0]
-    floor = (_oracle(model, cfg, x0, torch.float64, storage=torch.bfloat16)[0] - ref).abs().max().item()
+    emu = _oracle(model, cfg, x0, torch.float64, storage=torch.bfloat16, round_residual=not fp32_copies)[0]
+    floor = (emu - ref).abs().max().item()
     rel = ((out - ref).abs().max() / ref.abs().max()).item()
     mx = (out - ref).abs().max().item()
-    print(f"C3 full: normalised {rel:.3e}, max-abs {mx:.4f}, bf16 floor {floor:.4f}", flush=True)
+    print(f"C3 full (fp32 copies {fp32_copies}): normalised {rel:.3e}, max-abs {mx:.4f}, bf16 floor {floor:.4f}",
+          flush=True)
     assert torch.isfinite(out).all()
     assert rel < 2e-2, rel
     assert mx <= 2 * floor, (mx, floor)
 
 
-def test_mamba_lm_c4_full(gpu, tmp_path):
-    """BASELINE config 3 (C4) at its full size: token ids -> embedding -> 24 Mamba-2 layers
-    (d=1024, 32 heads x 64, N=128, chunk 256) -> final norm -> tied head (vocab 50280), bf16,
-    B=8, L=2048, with the norm gains on the activation side (norm_gain="activation").
-    The logits (fp32 copy) of sequence 0's first 256 tokens against the oracle's
-    model_forward in float64 on those tokens. The bf16 floor is the compiled program evaluated
-    in float64 with exact weights and every kernel output rounded to its declared dtype: max-abs
-    must stay within twice the floor's, and the normalised error within 2e-2 or, where the floor
-    itself is above that, within 1.25 times the floor's normalised error (24 layers of bf16
-    activations: the floor is 2.4% here, the eager bf16 model 3.8%; the rounding of the MFMA
-    operands alone, with every other intermediate exact, already costs 1.3%)."""
+@functools.lru_cache(maxsize=1)
+def _c4_reference(prefix: int):
+    """Sequence 0's first ``prefix`` tokens of the C4 model in float64: the oracle's logits and
+    the bf16 floor (the compiled program evaluated in float64 with exact weights and every
+    kernel output rounded to its declared dtype), computed once for both storage variants."""
+    import tempfile
+
     from oracle import interpret as oi
     from oracle.mamba import model_forward
     from targets.mamba import build_mamba_model, config_c4
     from torch_helion import CompileConfig, compile_model
 
-    announce("e2e mamba lm C4 full size (24 layers, B=8, L=2048)")
+    cfg = config_c4()
+    m = build_mamba_model(cfg, seed=0)
+    ids = m.example_inputs(seed=0)[0]
+    w = {k: v.detach() for k, v in m.state_dict().items()}
+    ids0 = ids[:1, :prefix]
+    ref = model_forward(ids0, w, cfg)[0]
+    small = type(cfg)(**{**cfg.__dict__, "batch": 1, "seq": prefix})
+    ms = build_mamba_model(small, seed=0)
+    rs = compile_model(ms, (ids0,), CompileConfig(run_name="c4_floor", results_dir=tempfile.mkdtemp(), backend="none",
+                                                  planner_mode="greedy", reference_check=False, verify_passes=False))
+    fs = rs.graph.fold_sources
+    params = {n: fs[n][0].double().reshape(-1, 1) * fs[n][1].double() if n in fs else v
+              for n, v in rs.graph.params.items()}
+    emu = oi.program_outputs(rs.program, params, [ids0], storage="declared")[0].reshape(ref.shape)
+    return ref, (emu - ref).abs().max().item()
+
+
+@pytest.mark.parametrize("fp32_outputs", [True, False])
+def test_mamba_lm_c4_full(gpu, tmp_path, fp32_outputs):
+    """BASELINE config 3 (C4) at its full size: token ids -> embedding -> 24 Mamba-2 layers
+    (d=1024, 32 heads x 64, N=128, chunk 256) -> final norm -> tied head (vocab 50280), bf16,
+    B=8, L=2048, with the norm gains on the activation side (norm_gain="activation").
+    The logits of sequence 0's first 256 tokens (their fp32 copy, or with fp32_outputs=False,
+    the program bench.py times, the bf16 logits themselves) against the oracle's model_forward
+    in float64 on those tokens. The bf16 floor is the compiled program evaluated in float64
+    with exact weights and every kernel output rounded to its declared dtype (bf16 logits
+    included): max-abs must stay within twice the floor's, and the normalised error within
+    2e-2 or, where the floor itself is above that, within 1.25 times the floor's normalised
+    error. This bar was set after the plain 2e-2 gate failed at 2.5%: 24 layers of bf16
+    activations put the floor at 2.4% here and the eager bf16 model at 3.8%; the rounding of
+    the MFMA operands alone, with every other intermediate exact, already costs 1.3%."""
+    from targets.mamba import build_mamba_model, config_c4
+    from torch_helion import CompileConfig, compile_model
+
+    announce(f"e2e mamba lm C4 full size (24 layers, B=8, L=2048), fp32 outputs {fp32_outputs}")
     cfg = config_c4()
     m = build_mamba_model(cfg, seed=0)
     ids = m.example_inputs(seed=0)[0]
     res = compile_model(m, (ids,), CompileConfig(run_name="c4_full", results_dir=tmp_path, backend="hip",
                                                  planner_mode="greedy", device_check=False, reference_check=False,
-                                                 verify_passes=False, norm_gain="activation"))
+                                                 verify_passes=False, norm_gain="activation",
+                                                 fp32_outputs=fp32_outputs))
     assert [k.kind for k in res.program.kernels].count("ssd_chunked") == 24
     assert any(p.get("gain_on_activation") for p in res.device_program.plans.values())
     prefix = 256
     dp = res.device_program
     dp.run([ids])
     torch.cuda.synchronize()
-    out = dp.outputs(fp32=True)[0].reshape(cfg.batch, cfg.seq, cfg.vocab)[0, :prefix].double().cpu()
-    w = {k: v.detach() for k, v in m.state_dict().items()}
-    ids0 = ids[:1, :prefix]
-    ref = model_forward(ids0, w, cfg)[0]
-    # the floor: the same program at the prefix's shape, exact weights, declared-dtype storage
-    small = type(cfg)(**{**cfg.__dict__, "batch": 1, "seq": prefix})
-    ms = build_mamba_model(small, seed=0)
-    rs = compile_model(ms, (ids0,), CompileConfig(run_name="c4_floor", results_dir=tmp_path, backend="none",
-                                                  planner_mode="greedy", reference_check=False, verify_passes=False))
-    fs = rs.graph.fold_sources
-    params = {n: fs[n][0].double().reshape(-1, 1) * fs[n][1].double() if n in fs else v
-              for n, v in rs.graph.params.items()}
-    emu = oi.program_outputs(rs.program, params, [ids0], storage="declared")[0].reshape(ref.shape)
-    floor = (emu - ref).abs().max().item()
+    out = dp.outputs(fp32=fp32_outputs)[0].reshape(cfg.batch, cfg.seq, cfg.vocab)[0, :prefix].double().cpu()
+    del res, dp
+    ref, floor = _c4_reference(prefix)
     floor_rel = floor / ref.abs().max().item()
     rel = ((out - ref).abs().max() / ref.abs().max()).item()
     mx = (out - ref).abs().max().item()
-    print(f"C4 full: normalised {rel:.3e} (floor {floor_rel:.3e}), max-abs {mx:.4f} (floor {floor:.4f})", flush=True)
+    print(f"C4 full (fp32 outputs {fp32_outputs}): normalised {rel:.3e} (floor {floor_rel:.3e}), "
+          f"max-abs {mx:.4f} (floor {floor:.4f})", flush=True)
     assert torch.isfinite(out).all()
     assert rel <= max(2e-2, 1.25 * floor_rel), (rel, floor_rel)
     assert mx <= 2 * floor, (mx, floor)

@@ -111,6 +111,38 @@ def test_gemm_bf16_rms_swiglu(gpu):
     assert _rel(ss, (xf * xf).sum(-1)) < 1e-5
 
 
+@pytest.mark.parametrize("a,b,mask", [(0, 1, 0b11), (1, 0, 0b01), (0, 1, 0b00)])
+def test_gemm_swiglu_register_epilogue(gpu, a, b, mask):
+    """The persistent 256-row kernel forms a lone bf16 SWIGLU output from the accumulator
+    registers (full tiles) and through the LDS slices otherwise (the ragged last row tile,
+    or a second output). Both routes give the same bits, and both match fp32."""
+    from torch_helion.hip import abi, ops
+
+    announce(f"gemm swiglu register epilogue a={a} b={b} mask={mask:02b}")
+    M, N, K, eps = 2000, 8192, 256, 1e-5     # 8 x 64 tiles of 256 x (2 x 128): persistent, last row tile ragged
+    g = torch.Generator().manual_seed(7)
+    x = torch.randn(M, K, generator=g).bfloat16()
+    w = [(torch.randn(K, N, generator=g) * 0.05).bfloat16() for _ in range(2)]
+    xf = x.float()
+    r = ((xf * xf).sum(-1, keepdim=True) / K + eps).pow(-0.5)
+    h = [(xf @ wi.float()) * (r if (mask >> i) & 1 else 1.0) for i, wi in enumerate(w)]
+    ref = h[a] * torch.sigmoid(h[a]) * h[b]
+    xd = x.to(gpu)
+    packed = ops.pack_rhs([wi.to(gpu) for wi in w], torch.bfloat16)
+    lone = torch.empty(M, N, dtype=torch.bfloat16, device=gpu)
+    pair = torch.empty(M, N, dtype=torch.bfloat16, device=gpu)
+    copy32 = torch.empty(M, N, dtype=torch.float32, device=gpu)
+    kw = dict(sumsq=mask != 0, rscale_mask=mask, inv_k=1.0 / K, eps=eps)
+    ops.gemm(ops.GemmCall(M, N, K, 2, xd, packed, [ops.EpiSpec(abi.EPI_SWIGLU, lone, a=a, b=b)], **kw))
+    ops.gemm(ops.GemmCall(M, N, K, 2, xd, packed, [ops.EpiSpec(abi.EPI_SWIGLU, pair, a=a, b=b),
+                                                   ops.EpiSpec(abi.EPI_SWIGLU, copy32, a=a, b=b)], **kw))
+    torch.cuda.synchronize()
+    assert torch.equal(lone, pair)
+    assert torch.equal(pair, copy32.bfloat16())
+    # (outputs up to ~16 here: one bf16 rounding is up to 2^-9 of the value, so the bar is relative)
+    assert _rel(lone, ref) < 1e-2
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_gemm_qkv_rope(gpu, dtype):
     """QKV with the RMS fold and RoPE: fused rotation vs the pre-rotated accumulator."""

@@ -40,11 +40,13 @@ __device__ __forceinline__ void wait_lgkmcnt0() {
 // wait for all of them (lgkmcnt(0)), exposing the latency of fragment reads
 // issued a step ahead of their MFMAs. The compiler does not track this load:
 // the caller waits for it (wait_vmcnt) before anything reads its destination
-// and before the workgroup ends.
+// and before the workgroup ends. The LDS address goes in through an "{m0}"
+// operand, so the compiler itself writes M0 (and knows it is in use) rather
+// than relying on a clobber of a reserved register.
 __device__ __forceinline__ void dma_load16(const void* base, uint32_t voff, uint32_t lds) {
-  // (one wait state between the M0 write and the load that reads it)
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "s"(lds)
-               : "memory", "m0");
+  // s_nop: one wait state between the compiler's M0 write, which it cannot
+  // see is read by the load inside the statement, and the load.
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "{m0}"(lds) : "memory");
 }
 
 // Workgroup barrier that leaves global loads in flight (__syncthreads, and

@@ -16,7 +16,7 @@
 //            x half of every accumulator's columns (or, with ASPLIT, one whole
 //            accumulator), so SwiGLU pairs and whole RoPE heads meet inside the
 //            wave. Operand tiles go HBM -> LDS by direct loads
-//            (global_load_lds_dwordx4) three stages deep, into an XOR-swizzled
+//            (global_load_lds_dwordx4) two stages deep, into an XOR-swizzled
 //            layout (conflict-free ds_read_b128 of MFMA operands); the epilogue
 //            of tile t overlaps the first loads of tile t+1;
 //          * direct (gemm_bf16_dl_kernel, small grids): one block per output
@@ -510,7 +510,8 @@ __global__ void __launch_bounds__(256, 1) gemm_bf16_kernel(GemmK p) {
   }
 
   float* slab = (float*)smem;
-#pragma unroll
+  // (not unrolled: the accumulator indices inside are constant either way, and the
+  // epilogue calls in the body are too large for the unroller)
   for (int s = 0; s < 2; ++s) {
     if (wm == s) {
 #pragma unroll
@@ -712,7 +713,8 @@ __global__ void __launch_bounds__(256, 1) gemm_bf16_dl_kernel(GemmK p) {
   lds_barrier();
 
   float* slab = (float*)smem;
-#pragma unroll
+  // (not unrolled: the accumulator indices inside are constant either way, and the
+  // epilogue calls in the body are too large for the unroller)
   for (int s = 0; s < 2; ++s) {
     if (wm == s) {
 #pragma unroll
@@ -998,6 +1000,53 @@ __global__ void __launch_bounds__(64 * NW, 1) gemm_bf16_pk_kernel(GemmK p) {
 
     // ---- epilogue of tile (tmi, tni), wave-private
     const int64_t row_w = (int64_t)tmi * BM + wm * WM;  // first row of this wave
+    // Register epilogue: one bf16 SWIGLU output over a tile inside M and the
+    // output's column window (the gate/up projection). The gate and up values of
+    // an output element sit in the same lane and register of two subtiles, so
+    // the product needs no transpose: it is formed from the accumulators and
+    // stored in the MFMA C layout, where for a fixed register lanes 0..31 hold
+    // 32 consecutive columns of one row (64 contiguous bytes) and lanes 32..63
+    // the row 4 below. Same arithmetic, in the same order, as epi_pair.
+    bool reg_epi = false;
+    if constexpr (NACC == 2 && !ASPLIT) {
+      const EpiOutK& e0 = p.out[0];
+      const int64_t c0 = (int64_t)tni * bn;
+      reg_epi = p.n_out == 1 && e0.op == TH_EPI_SWIGLU && e0.dtype == TH_BF16 && row_w - wm * WM + BM <= p.M &&
+                e0.cb <= c0 && e0.ce >= c0 + bn;
+      if (reg_epi) {
+        const bool swap = e0.a != 0;  // the gate is accumulator slot 1
+        const bool sa = SUMSQ && ((p.rscale_mask >> e0.a) & 1u);
+        const bool sb = SUMSQ && ((p.rscale_mask >> e0.b) & 1u);
+        // uniform base (row_w, the wave's first output column) + one 32-bit per-lane offset
+        char* obase = (char*)e0.ptr + (row_w * e0.ld + (c0 + wn * hbn - e0.cb)) * 2;
+        const uint32_t lofs = (uint32_t)(((lane >> 5) * 4 * e0.ld + (lane & 31)) * 2);
+#pragma unroll
+        for (int t = 0; t < TM; ++t) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            // row scales of rows 8q + 4 (lane / 32) + 0..3 of group t
+            float4 rr = make_float4(1.f, 1.f, 1.f, 1.f);
+            if constexpr (SUMSQ) rr = *(const float4*)(rsx + wm * WM + t * 32 + 8 * q + 4 * (lane >> 5));
+            const float rrv[4] = {rr.x, rr.y, rr.z, rr.w};
+#pragma unroll
+            for (int c32 = 0; c32 < TN / 2; ++c32) {
+#pragma unroll
+              for (int j = 0; j < 4; ++j) {
+                const int r = 4 * q + j;
+                const float x0 = acc[t][2 * c32][r], x1 = acc[t][2 * c32 + 1][r];
+                float g = swap ? x1 : x0, u = swap ? x0 : x1;
+                if (sa) g *= rrv[j];
+                const float ub = sb ? u * rrv[j] : u;
+                const float v = g * sigmoidf_(g) * ub;
+                const int64_t rofs = ((int64_t)(t * 32 + 8 * q + j) * e0.ld + c32 * 32) * 2;
+                *(uint16_t*)(obase + rofs + lofs) = f32_to_bf16(v);
+              }
+            }
+          }
+        }
+      }
+    }
+    if (!reg_epi) {
     // first column of this wave (in every accumulator it holds)
     const int64_t col_w = (int64_t)tni * bn + (ASPLIT ? 0 : wn * hbn);
     const int qlog = __builtin_ctz((unsigned)(wcols >> 2));  // quads per row = wcols / 4
@@ -1068,6 +1117,10 @@ __global__ void __launch_bounds__(64 * NW, 1) gemm_bf16_pk_kernel(GemmK p) {
     }
 
     lds_barrier();  // every wave is done with its stage-1 slice (its stores drain meanwhile)
+    } else {
+      // the register epilogue used no slice; rsx is rewritten only after the next
+      // tile's K loop, past its barriers
+    }
     if (!more) break;
     if (nk > 1) issue_half(rsan, rsbn, 1, 1);
     L = Ln;

@@ -15,6 +15,8 @@ key and value rows (the caller stores them at ``pos``).
 
 from __future__ import annotations
 
+import dataclasses
+
 import torch
 from torch import nn
 
@@ -64,6 +66,17 @@ class LlamaDecodeBlock(nn.Module):
         out = {name: self.weight(short) for short, name in PROJECTIONS.items()}
         out["input_norm.weight"], out["post_norm.weight"] = self.g1.clone(), self.g2.clone()
         return out
+
+    def prefill_block(self, batch: int) -> LlamaBlock:
+        """The block at S = 1 (non-causal) computing with this step's dequantised
+        weights, the model's gains and the RoPE rows of ``pos``: the module whose
+        capture compile_model turns into the decode program."""
+        cfg1 = dataclasses.replace(self.cfg, seq=1, batch=batch, causal=False)
+        blk = LlamaBlock(cfg1)
+        sd = self.dense_state_dict()
+        sd["rope_cos"], sd["rope_sin"] = self.rope_cos, self.rope_sin
+        blk.load_state_dict(sd, strict=False)
+        return blk.eval()
 
     def _norm(self, x: torch.Tensor, g: torch.Tensor) -> torch.Tensor:
         xf = x.float()

@@ -42,17 +42,15 @@ FP8 = "float8_e4m3fn"
 
 
 def _prefill_form(model, batch: int, config, run_dir):
-    """Compile the block at S = 1 with the step's dequantised weights and pos-row RoPE tables."""
-    from targets.llama_block import LlamaBlock
+    """Compile the block at S = 1 with the step's dequantised weights and pos-row RoPE tables.
 
+    The decode module supplies that block itself (``model.prefill_block(batch)``,
+    an nn.Module taking ``[batch, 1, hidden]``), so this module depends on no
+    particular model class."""
     from .pipeline import compile_model
 
-    cfg1 = dataclasses.replace(model.cfg, seq=1, batch=batch, causal=False)
-    blk = LlamaBlock(cfg1)
-    sd = model.dense_state_dict()
-    sd["rope_cos"], sd["rope_sin"] = model.rope_cos, model.rope_sin
-    blk.load_state_dict(sd, strict=False)
-    x = torch.zeros(batch, 1, cfg1.hidden, dtype=cfg1.dtype)
+    blk = model.prefill_block(batch)
+    x = torch.zeros(batch, 1, model.cfg.hidden, dtype=model.cfg.dtype)
     sub = dataclasses.replace(config, run_name="prefill_form", results_dir=run_dir, backend="none", bench=False,
                               reference_check=False, verify_passes=False, device_check=False)
     return compile_model(blk.eval(), (x,), sub)
@@ -84,7 +82,7 @@ def decode_program(model, batch: int, config, run_dir) -> tuple[Program, dict[st
     for k in P.kernels:
         k = KernelSpec.from_dict(k.to_dict())
         if k.kind == "gemm" and k.gemms:
-            gains = set()
+            gains: list[torch.Tensor] = []
             for g in k.gemms:
                 t = k.arg(g.rhs).tensor
                 folded = t in folds
@@ -104,9 +102,15 @@ def decode_program(model, batch: int, config, run_dir) -> tuple[Program, dict[st
                 param_names.append(sname)
                 k.args.append(KernelArg(g.rhs + "_scale", sname, "scale"))
                 if folded:
-                    gains.add(folds[t][0].float())
+                    gains.append(folds[t][0].float())
             if gains:
-                gain = next(iter(gains))
+                # one gain multiplies the kernel's shared lhs, so it must hold for every product
+                if len(gains) != len(k.gemms):
+                    raise ValueError(f"{k.name}: {len(gains)} of {len(k.gemms)} GEMM weights carry a folded "
+                                     "norm gain; a kernel's products must all carry it or none")
+                gain = gains[0]
+                if not all(g.shape == gain.shape and torch.equal(g, gain) for g in gains[1:]):
+                    raise ValueError(f"{k.name}: the GEMM weights were folded with different norm gains")
                 gname = f"{k.name}_gain"
                 params[gname] = gain.reshape(-1).contiguous()
                 tensors[gname] = TensorType((gain.numel(),), "float32")

@@ -603,7 +603,8 @@ class DeviceProgram:
         norm_launch, normed = None, None
         gain = self._unfold_gain(spec, plan, used)
         if gain is not None:
-            norm_launch, normed = self._normed_lhs(spec, lhs_t, gain, plan.rscale)
+            # (collect mode only asks: the shared buffer is registered when a launch is made)
+            norm_launch, normed = self._normed_lhs(spec, lhs_t, gain, plan.rscale, register=collect is None)
             lhs = normed
         # (a merged launch packs its own concatenated weights)
         get_packed = self._pack(spec, [rhs_of[i] for i in used], in_dtype, unfold=gain is not None) \
@@ -671,6 +672,10 @@ class DeviceProgram:
         if self.program.tensors[spec.arg("lhs").tensor].dtype != "bfloat16":
             return None
         tens = [spec.arg(spec.gemms[i].rhs).tensor for i in used]
+        # e4m3 weights are quantised from the model's own weights and carry their gain
+        # as a ``gain`` argument: there is nothing to take back out of them
+        if any(self.program.tensors[t].dtype == "float8_e4m3fn" for t in tens):
+            return None
         if any(t not in self.fold_sources for t in tens) or not all(plan.scaled.get(i, False) for i in used):
             return None
         g0 = self.fold_sources[tens[0]][0]
@@ -678,10 +683,13 @@ class DeviceProgram:
             return None
         return g0
 
-    def _normed_lhs(self, spec: KernelSpec, lhs_t: str, gain: torch.Tensor, rscale) -> tuple[Launch | None, torch.Tensor]:
+    def _normed_lhs(self, spec: KernelSpec, lhs_t: str, gain: torch.Tensor, rscale,
+                    register: bool = True) -> tuple[Launch | None, torch.Tensor]:
         """bf16 ``x * r * g`` of this lhs (x read from its fp32 shadow when it has one),
         made by one th_rmsnorm launch before the first kernel that needs it and shared
-        by the later ones (sibling projections of the same normalised input)."""
+        by the later ones (sibling projections of the same normalised input).
+        ``register=False``: a probe (collect mode) whose launch may never be emitted,
+        so later kernels must not take the buffer as already written."""
         inv_k, eps = rscale
         key = (lhs_t, gain.data_ptr(), float(inv_k), float(eps))
         if key in self._normed:
@@ -690,7 +698,8 @@ class DeviceProgram:
         # read only by kernels that read the lhs: the lhs's lifetime bounds it
         out = self._device_buffer(x.shape, torch.bfloat16, self._last.get(lhs_t, self._cur))
         gvec = gain.float().reshape(-1).to(self.device).contiguous()
-        self._normed[key] = out
+        if register:
+            self._normed[key] = out
 
         def run() -> None:
             ops.rmsnorm(x, gvec, eps, out, inv_k=inv_k, kernel=f"{spec.name} (normalised lhs)")
@@ -868,6 +877,7 @@ class DeviceProgram:
                 return None
             parts.append((spec, col[0]))
         p0 = parts[0][1]
+        rope = next((pt["rope"] for _, pt in parts if pt["rope"] is not None), None)
         for spec, pt in parts:
             if not pt["fp8"] or pt["lhs"] is not p0["lhs"] or pt["extras"] or pt["norm"] is not None:
                 return None
@@ -878,13 +888,12 @@ class DeviceProgram:
             if (pt["lhs_gain"] is None) != (p0["lhs_gain"] is None) or \
                     (pt["lhs_gain"] is not None and not torch.equal(pt["lhs_gain"], p0["lhs_gain"])):
                 return None
-            r, r0 = pt["rope"], p0["rope"]
-            if r is not None and r0 is not None:
-                if r[2:] != r0[2:] or not torch.equal(r[0], r0[0]) or not torch.equal(r[1], r0[1]):
-                    return None
+            # every member's RoPE tables must equal the first ones met (one pair per launch)
+            r = pt["rope"]
+            if r is not None and (r[2:] != rope[2:] or not torch.equal(r[0], rope[0]) or not torch.equal(r[1], rope[1])):
+                return None
             if any(e.b >= 0 or e.e >= 0 or e.cols is not None for e in pt["epi"]):
                 return None
-        rope = next((pt["rope"] for _, pt in parts if pt["rope"] is not None), None)
         T, K = p0["T"], p0["K"]
         ws_: list[torch.Tensor] = []
         scales: list[torch.Tensor] = []
@@ -898,8 +907,15 @@ class DeviceProgram:
                 win[slot] = (n_tot, n_tot + pt["N"])
                 n_tot += pt["N"]
             for e in pt["epi"]:
+                if e.op in (abi.EPI_ROPE, abi.EPI_ROPE_PAIR) and rope is not None:
+                    # a rotated window must hold whole heads (th_gemm would refuse it at run time)
+                    hd = rope[3]
+                    if win[e.a][0] % hd or (win[e.a][1] - win[e.a][0]) % hd:
+                        return None
                 epi.append(ops.EpiSpec(e.op, e.out, a=0, cols=win[e.a]))
         if len(epi) > abi.MAX_OUT:
+            return None
+        if rope is not None and n_tot % rope[3]:
             return None
         packed = ops.pack_rhs([torch.cat(ws_, dim=1).view(_FP8).contiguous()], _FP8)
         scale = torch.cat(scales).reshape(1, -1).contiguous()

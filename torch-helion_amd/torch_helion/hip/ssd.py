@@ -40,12 +40,30 @@ def lower_ssd(dp, spec: KernelSpec):
     x, bm, cm, dt = buf("x"), buf("b"), buf("c"), buf("dt")
     kw: dict = dict(batch=bs, seq=s, heads=h, head_dim=p, state_dim=n)
     if spec.kind == "ssd_chunked":
+        A = buf("A").float().contiguous()
+        # The scan splits decay exponents at block boundaries and needs each part <= 0,
+        # which holds when the running sum of dt*A never increases: A <= 0 with dt >= 0
+        # (Mamba's A = -exp(A_log), dt = softplus(.)). A is a parameter: check it here.
+        if not bool((A <= 0).all()):
+            raise abi.HipBackendError("lower", abi.TH_ERR_UNSUPPORTED,
+                                      "ssd_chunked needs A <= 0 for every head (the running sum of dt*A "
+                                      "must not increase)", spec.name)
         kw.update(ngroups=a.get("ngroups", h), chunk=int(a.get("chunk", 64)), dt_stride=1,
-                  A=buf("A").float().contiguous(), D=buf("D").float().contiguous())
+                  A=A, D=buf("D").float().contiguous())
     else:
         mask = dp._host(spec.arg("mask").tensor)
         if mask is None or not torch.equal(mask.float(), torch.ones(s, s).tril()):
             raise abi.HipBackendError("lower", abi.TH_ERR_UNSUPPORTED, "ssd mask is not the causal lower triangle", spec.name)
+        # The ssd kind takes cum as an operand: it must be non-increasing along each
+        # sequence (a running sum of dt*A with dt*A <= 0), which the scan's split decay
+        # exponents rely on. Known at lowering only when cum is a parameter.
+        cum_host = dp._host(spec.arg("cum").tensor)
+        if cum_host is not None:
+            c = cum_host.float().reshape(bs, s, -1)
+            if s > 1 and not bool((c[:, 1:] <= c[:, :-1]).all()):
+                raise abi.HipBackendError("lower", abi.TH_ERR_UNSUPPORTED,
+                                          "ssd needs cum non-increasing along the sequence (a running sum of "
+                                          "dt*A with dt*A <= 0)", spec.name)
         kw.update(ngroups=h, chunk=64 if s % 64 == 0 or s > 64 else s, dt_stride=int(a["pad"]), cum=buf("cum"),
                   dskip=buf("dskip"))
     gate_arg, fused = _gate_of(spec)
