@@ -467,19 +467,36 @@ def test_gemm_extra_ops(gpu):
     assert _rel(o[3], acc * torch.sigmoid(acc)) < 1e-5
 
 
-def test_gemm_f32_small(gpu):
+@pytest.mark.parametrize("M,N,K,case", [(128, 1376, 512, "add"), (128, 1376, 512, "rms_swiglu"),
+                                         (100, 200, 136, "acc"), (77, 96, 1380, "add"), (4096, 512, 256, "add")])
+def test_gemm_f32_small(gpu, M, N, K, case):
+    """fp32 GEMMs: small grids (the C1 shapes, ragged rows, K not a multiple of 8, a long K) on
+    the 32-row split-K kernel, and a grid that fills the GPU on the 64-row kernel."""
     from torch_helion.hip import abi, ops
 
-    announce("gemm f32 M=128 N=1376 K=512 + residual")
-    M, N, K = 128, 1376, 512
+    announce(f"gemm f32 M={M} N={N} K={K} {case}")
     g = torch.Generator().manual_seed(4)
     a = torch.randn(M, K, generator=g)
-    w = torch.randn(K, N, generator=g) * 0.02
+    n_acc = 2 if case == "rms_swiglu" else 1
+    w = [torch.randn(K, N, generator=g) * 0.02 for _ in range(n_acc)]
     res = torch.randn(M, N, generator=g)
-    ref = res + a @ w
-    packed = ops.pack_rhs([w.to(gpu)], torch.float32)
+    packed = ops.pack_rhs([wi.to(gpu) for wi in w], torch.float32)
     out = torch.empty(M, N, device=gpu)
-    ops.gemm(ops.GemmCall(M, N, K, 1, a.to(gpu), packed, [ops.EpiSpec(abi.EPI_ADD, out, e=0)], extras=[res.to(gpu)]))
+    kw = {}
+    if case == "add":
+        ref = res + a @ w[0]
+        epi = [ops.EpiSpec(abi.EPI_ADD, out, e=0)]
+        kw["extras"] = [res.to(gpu)]
+    elif case == "acc":
+        ref = a @ w[0]
+        epi = [ops.EpiSpec(abi.EPI_ACC, out)]
+    else:
+        r = ((a * a).sum(-1, keepdim=True) / K + 1e-5).pow(-0.5)
+        hg, hu = (a @ w[0]) * r, (a @ w[1]) * r
+        ref = hg * torch.sigmoid(hg) * hu
+        epi = [ops.EpiSpec(abi.EPI_SWIGLU, out, a=0, b=1)]
+        kw.update(sumsq=True, rscale_mask=0b11, inv_k=1.0 / K, eps=1e-5)
+    ops.gemm(ops.GemmCall(M, N, K, n_acc, a.to(gpu), packed, epi, **kw))
     torch.cuda.synchronize()
     assert _rel(out, ref) < F32_REL
 
@@ -515,17 +532,21 @@ def test_attention_bf16(gpu, B, S, Hq, Hkv, hd, causal):
     assert _maxabs(out, ref) < BF16_TOL
 
 
-def test_attention_f32(gpu):
+@pytest.mark.parametrize("B,S,Hq,Hkv,hd,causal", [(1, 128, 8, 8, 64, True), (2, 200, 4, 2, 128, True),
+                                                  (1, 77, 4, 1, 64, False), (2, 33, 2, 2, 32, True)])
+def test_attention_f32(gpu, B, S, Hq, Hkv, hd, causal):
+    """fp32 prefill attention: the matrix-core kernel (head_dim 64/128; C1 is the first case),
+    ragged query and key blocks, grouped KV heads, and the scalar kernel (head_dim 32)."""
     from torch_helion.hip import ops
 
-    announce("attention f32 B=1 S=128 H=8 hd=64 causal")
-    B, S, H, hd = 1, 128, 8, 64
+    announce(f"attention f32 B={B} S={S} Hq={Hq} Hkv={Hkv} hd={hd} causal={causal}")
     g = torch.Generator().manual_seed(9)
-    q, k, v = [torch.randn(B * S, H * hd, generator=g) for _ in range(3)]
-    ref = _attn_ref(q, k, v, B, S, H, H, hd, hd ** -0.5, True)
-    out = torch.empty(B * S, H * hd, device=gpu)
-    ops.attention_prefill(q.to(gpu), k.to(gpu), v.to(gpu), out, batch=B, seq_q=S, seq_kv=S, heads_q=H, heads_kv=H,
-                          head_dim=hd, scale=hd ** -0.5, causal=True)
+    q = torch.randn(B * S, Hq * hd, generator=g)
+    k, v = [torch.randn(B * S, Hkv * hd, generator=g) for _ in range(2)]
+    ref = _attn_ref(q, k, v, B, S, Hq, Hkv, hd, hd ** -0.5, causal)
+    out = torch.empty(B * S, Hq * hd, device=gpu)
+    ops.attention_prefill(q.to(gpu), k.to(gpu), v.to(gpu), out, batch=B, seq_q=S, seq_kv=S, heads_q=Hq,
+                          heads_kv=Hkv, head_dim=hd, scale=hd ** -0.5, causal=causal)
     torch.cuda.synchronize()
     assert _rel(out, ref) < F32_REL
 

@@ -299,6 +299,7 @@ struct AttnF32K {
   int64_t ldq, ldk, ldv, ldo;
   int B, Sq, Skv, Hq, Hkv, group, D, causal, off;
   float scale;
+  float scale_log2;  // scale * log2(e) (matrix-core kernel)
 };
 
 template <int D>
@@ -333,6 +334,119 @@ __global__ void __launch_bounds__(64) attn_fwd_f32_kernel(AttnF32K p) {
   const float inv = l > 0.f ? 1.f / l : 0.f;
 #pragma unroll
   for (int d = 0; d < D; ++d) orow[d] = acc[d] * inv;
+}
+
+// fp32 attention on the matrix cores (head_dim 64 or 128): one wave per 32
+// queries of one (batch, q head), keys in blocks of 32 with an online softmax.
+// S^T = K Q^T and O^T += V^T P^T run on v_mfma_f32_32x32x2f32, so a lane owns
+// one query column (l % 32) and the softmax statistics need one lane^32
+// exchange, as in the bf16 kernel. Operands come straight from memory in the
+// MFMA layouts (the fp32 configurations are small and L2-resident):
+//   S^T step (chunk i, component c): lane l supplies K[key l%32][8i + 4(l/32) + c]
+//     and Q[query l%32][the same d]: one float4 per chunk and lane, the
+//     contraction index permuted identically on both sides;
+//   O^T step (register r of S^T): lane l supplies P for key
+//     8(r/4) + 4(l/32) + r%4 (its own S^T register) and V[that key][32t + l%32].
+// The result goes out through LDS as whole rows.
+template <int D>
+__global__ void __launch_bounds__(64, 1) attn_fwd_f32_mfma_kernel(AttnF32K p) {
+  constexpr int NCH = D / 8;   // float4 chunks per lane of a Q or K row
+  constexpr int NDT = D / 32;  // 32-row tiles of O^T
+  constexpr int OROW = D + 4;  // LDS row stride (floats) of the output staging
+  __shared__ __attribute__((aligned(16))) float so[32 * OROW];
+  const int bh = blockIdx.y;
+  const int b = bh / p.Hq, hq = bh - b * p.Hq, hk = hq / p.group;
+  const int q0 = blockIdx.x * 32;
+  const int lane = threadIdx.x, qc = lane & 31, half = lane >> 5;
+  const float* qb = p.q + (int64_t)b * p.Sq * p.ldq + (int64_t)hq * D;
+  const float* kbase = p.k + (int64_t)b * p.Skv * p.ldk + (int64_t)hk * D;
+  const float* vbase = p.v + (int64_t)b * p.Skv * p.ldv + (int64_t)hk * D;
+  const int qrow = min(q0 + qc, p.Sq - 1);  // rows past Sq re-read the last one (never stored)
+  float4 qf[NCH];
+#pragma unroll
+  for (int i = 0; i < NCH; ++i) qf[i] = *(const float4*)(qb + (int64_t)qrow * p.ldq + 8 * i + 4 * half);
+  f32x16_t o[NDT];
+#pragma unroll
+  for (int t = 0; t < NDT; ++t)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[t][r] = 0.f;
+  float m = -INFINITY, l = 0.f;
+  // keys visible to the block's last query
+  int kend = p.Skv;
+  if (p.causal) kend = min(kend, q0 + 31 + p.off + 1);
+  const int myq = q0 + qc;
+  for (int kb = 0; kb < kend; kb += 32) {
+    // K rows of this block (rows past Skv re-read the last key; masked below)
+    float4 kf[NCH];
+    const int krow = min(kb + qc, p.Skv - 1);
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) kf[i] = *(const float4*)(kbase + (int64_t)krow * p.ldk + 8 * i + 4 * half);
+    // V operands: register r's key, columns 32t + l%32
+    float vf[NDT][16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int key = min(kb + 8 * (r >> 2) + 4 * half + (r & 3), p.Skv - 1);
+#pragma unroll
+      for (int t = 0; t < NDT; ++t) vf[t][r] = vbase[(int64_t)key * p.ldv + 32 * t + qc];
+    }
+    f32x16_t st;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) st[r] = 0.f;
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) {
+      st = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[i].x, qf[i].x, st, 0, 0, 0);
+      st = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[i].y, qf[i].y, st, 0, 0, 0);
+      st = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[i].z, qf[i].z, st, 0, 0, 0);
+      st = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[i].w, qf[i].w, st, 0, 0, 0);
+    }
+    // scores in log2 units, masked past the sequence and above the diagonal
+    float mb = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int key = kb + 8 * (r >> 2) + 4 * half + (r & 3);
+      const bool vis = key < p.Skv && (!p.causal || key <= myq + p.off);
+      st[r] = vis ? st[r] * p.scale_log2 : -INFINITY;
+      mb = fmaxf(mb, st[r]);
+    }
+    mb = fmaxf(mb, __shfl_xor(mb, 32));
+    const float mn = fmaxf(m, mb);
+    // (a column with no visible key yet keeps m = -inf: nothing to rescale, P = 0)
+    const float alpha = mn == -INFINITY ? 1.f : exp2f(m - mn);
+    float ps = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      st[r] = mn == -INFINITY ? 0.f : exp2f(st[r] - mn);
+      ps += st[r];
+    }
+    ps += __shfl_xor(ps, 32);
+    l = l * alpha + ps;
+    m = mn;
+#pragma unroll
+    for (int t = 0; t < NDT; ++t) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[t][r] *= alpha;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(vf[t][r], st[r], o[t], 0, 0, 0);
+    }
+  }
+  // O = O^T / l, transposed through LDS: lane l holds column (query) l%32, rows
+  // d = 32t + 8(r/4) + 4(l/32) + r%4
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+#pragma unroll
+  for (int t = 0; t < NDT; ++t)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) so[qc * OROW + 32 * t + 8 * (r >> 2) + 4 * half + (r & 3)] = o[t][r] * inv;
+  __syncthreads();
+  // each pass: 64 lanes write D/4 float4 of 256 / D rows
+  constexpr int F4 = D / 4, RPP = 64 / F4;
+  float* ob = p.o + (int64_t)b * p.Sq * p.ldo + (int64_t)hq * D;
+  for (int rr = lane / F4; rr < 32; rr += RPP) {
+    const int qi = q0 + rr;
+    if (qi < p.Sq) {
+      const int c4 = lane % F4;
+      *(float4*)(ob + (int64_t)qi * p.ldo + 4 * c4) = *(const float4*)(so + rr * OROW + 4 * c4);
+    }
+  }
 }
 
 }  // namespace th
@@ -395,12 +509,25 @@ extern "C" int th_attention_prefill(const th_attn_desc* d, void* stream) {
     k.B = d->batch; k.Sq = d->seq_q; k.Skv = d->seq_kv; k.Hq = d->heads_q; k.Hkv = d->heads_kv;
     k.group = d->heads_q / d->heads_kv; k.D = hd; k.causal = d->causal ? 1 : 0; k.off = d->seq_kv - d->seq_q;
     k.scale = d->scale;
-    const dim3 grid((unsigned)cdiv(d->seq_q, 64), (unsigned)(d->batch * d->heads_q));
-    switch (hd) {
-      case 16: hipLaunchKernelGGL(attn_fwd_f32_kernel<16>, grid, dim3(64), 0, s, k); break;
-      case 32: hipLaunchKernelGGL(attn_fwd_f32_kernel<32>, grid, dim3(64), 0, s, k); break;
-      case 64: hipLaunchKernelGGL(attn_fwd_f32_kernel<64>, grid, dim3(64), 0, s, k); break;
-      default: hipLaunchKernelGGL(attn_fwd_f32_kernel<128>, grid, dim3(64), 0, s, k); break;
+    k.scale_log2 = d->scale * log2e;
+    // head_dim 64 / 128 (16-byte aligned rows): the matrix-core kernel, 32 queries per wave;
+    // 16 / 32: the scalar kernel, one query per lane
+    const bool mfma = (hd == 64 || hd == 128) && d->ld_q % 4 == 0 && d->ld_k % 4 == 0 && d->ld_o % 4 == 0 &&
+                      ((uintptr_t)d->q | (uintptr_t)d->k | (uintptr_t)d->o) % 16 == 0;
+    if (mfma) {
+      const dim3 grid((unsigned)cdiv(d->seq_q, 32), (unsigned)(d->batch * d->heads_q));
+      if (hd == 64)
+        hipLaunchKernelGGL(attn_fwd_f32_mfma_kernel<64>, grid, dim3(64), 0, s, k);
+      else
+        hipLaunchKernelGGL(attn_fwd_f32_mfma_kernel<128>, grid, dim3(64), 0, s, k);
+    } else {
+      const dim3 grid((unsigned)cdiv(d->seq_q, 64), (unsigned)(d->batch * d->heads_q));
+      switch (hd) {
+        case 16: hipLaunchKernelGGL(attn_fwd_f32_kernel<16>, grid, dim3(64), 0, s, k); break;
+        case 32: hipLaunchKernelGGL(attn_fwd_f32_kernel<32>, grid, dim3(64), 0, s, k); break;
+        case 64: hipLaunchKernelGGL(attn_fwd_f32_kernel<64>, grid, dim3(64), 0, s, k); break;
+        default: hipLaunchKernelGGL(attn_fwd_f32_kernel<128>, grid, dim3(64), 0, s, k); break;
+      }
     }
   }
   TH_CHECK_LAUNCH();

@@ -1238,6 +1238,93 @@ __global__ void __launch_bounds__(256, 1) gemm_f32_kernel(GemmK p) {
   }
 }
 
+// ------------------------------------- fp32 MFMA, small grids (split-K in a workgroup)
+// A workgroup computes 32 rows x BNC packed columns with NSUB = BNC / 32
+// column slices times KS K slices of one wave each (NSUB * KS <= 16 waves), so
+// a GEMM of a few hundred rows (the fp32 Llama block: 128 tokens) still runs
+// on every SIMD. Each wave multiplies its 32 x 32 subtile over its K slice
+// with operands read straight from memory in the MFMA layout (lane l: row
+// l % 32, one float4 at k + 4 (l / 32); its four components are four k = 2
+// steps, the contraction index permuted the same way on both sides). The KS
+// partial tiles are summed through LDS in slice order, then the ordinary
+// slab epilogue runs on the first 256 threads.
+template <int BNC>
+__global__ void __launch_bounds__(1024, 1) gemm_f32_sk_kernel(GemmK p) {
+  constexpr int NSUB = BNC / 32;
+  constexpr int KS = 16 / NSUB > 0 ? 16 / NSUB : 1;
+  constexpr int NT = 64 * NSUB * KS;
+  constexpr int SROW = BNC + 8;
+  __shared__ __attribute__((aligned(16))) float part[KS * 32 * BNC];
+  __shared__ __attribute__((aligned(16))) float slab[32 * SROW];
+  __shared__ float ssp[KS * 32];
+  __shared__ float rs[32];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int ns = wave % NSUB, ks = wave / NSUB;
+  int tmi, tni;
+  map_tile(p.tiles_m, p.tiles_n, tmi, tni);
+  const int64_t m0 = (int64_t)tmi * 32;
+  const int row = (int)min(m0 + (lane & 31), p.M - 1);  // rows past M re-read row M-1 (never stored)
+  const float* A = (const float*)p.A + (int64_t)row * p.lda;
+  const float* B = (const float*)p.B + ((int64_t)tni * BNC + ns * 32 + (lane & 31)) * p.ldb;
+  // K slice of this wave: whole 8-wide steps
+  const int64_t kq = (p.K + 8 * KS - 1) / (8 * KS) * 8;
+  const int64_t k0 = ks * kq, k1 = min(p.K, k0 + kq);
+  const int h4 = 4 * (lane >> 5);
+  f32x16_t acc;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+  float ss = 0.f;
+  // (K is a multiple of 4: a float4 at k + h4 lies wholly inside K or wholly past it)
+  auto ld = [&](int64_t k, float4& a, float4& b) {
+    const bool in = k + h4 < k1;
+    a = in ? *(const float4*)(A + k + h4) : make_float4(0.f, 0.f, 0.f, 0.f);
+    b = in ? *(const float4*)(B + k + h4) : make_float4(0.f, 0.f, 0.f, 0.f);
+  };
+  float4 a0, b0, a1, b1;
+  ld(k0, a0, b0);
+  for (int64_t k = k0; k < k1; k += 16) {
+    ld(k + 8, a1, b1);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a0.x, b0.x, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a0.y, b0.y, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a0.z, b0.z, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a0.w, b0.w, acc, 0, 0, 0);
+    if (p.sumsq && ns == 0) ss += a0.x * a0.x + a0.y * a0.y + a0.z * a0.z + a0.w * a0.w;
+    if (k + 8 >= k1) break;
+    ld(k + 16, a0, b0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a1.x, b1.x, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a1.y, b1.y, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a1.z, b1.z, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a1.w, b1.w, acc, 0, 0, 0);
+    if (p.sumsq && ns == 0) ss += a1.x * a1.x + a1.y * a1.y + a1.z * a1.z + a1.w * a1.w;
+  }
+  // partial tile of slice ks: part[ks][row][col], rows 8(r/4) + 4(l/32) + r%4, column l%32
+#pragma unroll
+  for (int r = 0; r < 16; ++r)
+    part[(ks * 32 + 8 * (r >> 2) + h4 + (r & 3)) * BNC + ns * 32 + (lane & 31)] = acc[r];
+  if (p.sumsq && ns == 0) {
+    const float v = ss + __shfl_xor(ss, 32);
+    if (lane < 32) ssp[ks * 32 + lane] = v;
+  }
+  __syncthreads();
+  for (int e = tid; e < 32 * BNC; e += NT) {
+    const int r = e / BNC, c = e - r * BNC;
+    float v = part[e];
+#pragma unroll
+    for (int q = 1; q < KS; ++q) v += part[q * 32 * BNC + e];
+    slab[r * SROW + c] = v;
+  }
+  if (p.sumsq && tid < 32) {
+    float v = 0.f;
+#pragma unroll
+    for (int q = 0; q < KS; ++q) v += ssp[q * 32 + tid];
+    rs[tid] = rsqrtf(v * p.inv_k + p.eps);
+    const int64_t gr = m0 + tid;
+    if (p.sumsq_out && tni == 0 && gr < p.M) p.sumsq_out[gr] = v;
+  }
+  __syncthreads();
+  if (tid < 256) epilogue_slab(p, slab, SROW, 32, rs, m0, tni, tid);
+}
+
 // ------------------------------------------------------------------ packing
 struct PackK {
   const void* src[TH_MAX_ACC];
@@ -1473,6 +1560,13 @@ static void launch_f32(const GemmK& k, hipStream_t s) {
   hipLaunchKernelGGL((gemm_f32_kernel<BNC>), dim3(k.tiles_m * k.tiles_n), dim3(256), 0, s, k);
 }
 
+// 32-row tiles, K split over the waves of a workgroup (tiles_m counts 32-row tiles)
+template <int BNC>
+static void launch_f32_sk(const GemmK& k, hipStream_t s) {
+  constexpr int NSUB = BNC / 32, KS = 16 / NSUB > 0 ? 16 / NSUB : 1;
+  hipLaunchKernelGGL((gemm_f32_sk_kernel<BNC>), dim3(k.tiles_m * k.tiles_n), dim3(64 * NSUB * KS), 0, s, k);
+}
+
 extern "C" int th_gemm(const th_gemm_desc* d, void* stream) {
   TH_CHECK_ARG(d != nullptr, "th_gemm: null descriptor");
   TH_CHECK_ARG(d->M > 0 && d->N > 0 && d->K > 0, "th_gemm: M=%lld N=%lld K=%lld must be positive",
@@ -1590,6 +1684,20 @@ extern "C" int th_gemm(const th_gemm_desc* d, void* stream) {
     return launch_gemm_fp8(k, cdiv(d->N, bn) * bnc, d->rhs_scale, d->workspace, d->workspace_bytes, s);
   }
   if (d->in_dtype == TH_F32) {
+    const int64_t cus = device_cus() > 0 ? device_cus() : 256;
+    if (cdiv(d->M, 64) * k.tiles_n < cus) {
+      // too few 64-row tiles to occupy the GPU: 32-row tiles with the K loop split over 16 waves
+      k.tiles_m = (int)cdiv(d->M, 32);
+      switch (bnc) {
+        case 64: launch_f32_sk<64>(k, s); break;
+        case 128: launch_f32_sk<128>(k, s); break;
+        case 192: launch_f32_sk<192>(k, s); break;
+        case 256: launch_f32_sk<256>(k, s); break;
+        default: set_error("th_gemm: no fp32 kernel for tile %d", bnc); return TH_ERR_UNSUPPORTED;
+      }
+      TH_CHECK_LAUNCH();
+      return TH_OK;
+    }
     k.tiles_m = (int)cdiv(d->M, 64);
     switch (bnc) {
       case 64: launch_f32<64>(k, s); break;
