@@ -126,7 +126,8 @@ typedef struct th_gemm_desc {
   th_epi_out out[TH_MAX_OUT];
   float* sumsq_out;       /* optional [M] fp32: raw sum_k lhs^2 */
   const float* rhs_scale; /* TH_F8E4M3: [n_acc][N] fp32, acc_i[:, n] *= rhs_scale[i*N + n] */
-  float* workspace;       /* TH_F8E4M3: th_gemm_workspace_bytes(...) bytes */
+  float* workspace;       /* th_gemm_workspace_bytes(...) bytes, 16-byte aligned: required for TH_F8E4M3;
+                             optional for TH_F32 (small grids then split K over workgroups through it) */
   int64_t workspace_bytes;
   const float* lhs_gain;  /* optional [K] fp32 per-column gain of lhs (TH_F8E4M3 only; 16-byte aligned) */
 } th_gemm_desc;
@@ -149,8 +150,10 @@ int th_gemm_pack_rhs(const void* const* src, const int64_t* ld_src, int32_t src_
                      int64_t N, int64_t K, int32_t n_acc, int32_t in_dtype,
                      void* packed, void* stream);
 
-/* Workspace th_gemm needs for these sizes (0 for TH_BF16 / TH_F32; the
- * split-K partial sums for TH_F8E4M3). -1 for invalid arguments. */
+/* Workspace th_gemm uses for these sizes: 0 for TH_BF16; for TH_F8E4M3 the
+ * split-K partial sums it needs; for TH_F32 grids too small to occupy the GPU,
+ * the partial sums of the split over workgroups (optional: without it the K
+ * loop is split inside each workgroup), else 0. -1 for invalid arguments. */
 int64_t th_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t n_acc, int32_t in_dtype);
 
 /* One OpIR gemm KernelSpec. */

@@ -499,6 +499,16 @@ def test_gemm_f32_small(gpu, M, N, K, case):
     ops.gemm(ops.GemmCall(M, N, K, n_acc, a.to(gpu), packed, epi, **kw))
     torch.cuda.synchronize()
     assert _rel(out, ref) < F32_REL
+    # with a workspace, small grids split K over workgroups (a second pass sums the slices)
+    nb = ops.gemm_workspace_bytes(M, N, K, n_acc, torch.float32)
+    assert (nb > 0) == (M < 1024), nb
+    if nb:
+        ws = torch.full((nb,), 255, dtype=torch.uint8, device=gpu)   # stale contents must not matter
+        out2 = torch.empty_like(out)
+        epi2 = [ops.EpiSpec(e.op, out2, a=e.a, b=e.b, e=e.e) for e in epi]
+        ops.gemm(ops.GemmCall(M, N, K, n_acc, a.to(gpu), packed, epi2, workspace=ws, **kw))
+        torch.cuda.synchronize()
+        assert _rel(out2, ref) < F32_REL
 
 
 def _attn_ref(q, k, v, B, S, Hq, Hkv, hd, scale, causal):
@@ -513,7 +523,8 @@ def _attn_ref(q, k, v, B, S, Hq, Hkv, hd, scale, causal):
 
 @pytest.mark.parametrize("B,S,Hq,Hkv,hd,causal", [(2, 200, 4, 2, 128, True), (1, 256, 8, 8, 64, False),
                                                   (2, 384, 8, 2, 128, False), (1, 130, 4, 1, 64, True),
-                                                  (8, 320, 8, 2, 128, True)])
+                                                  (8, 320, 8, 2, 128, True), (1, 1100, 4, 1, 128, True),
+                                                  (2, 700, 4, 4, 64, False)])
 def test_attention_bf16(gpu, B, S, Hq, Hkv, hd, causal):
     from torch_helion.hip import ops
 

@@ -375,20 +375,31 @@ __global__ void __launch_bounds__(64, 1) attn_fwd_f32_mfma_kernel(AttnF32K p) {
   int kend = p.Skv;
   if (p.causal) kend = min(kend, q0 + 31 + p.off + 1);
   const int myq = q0 + qc;
-  for (int kb = 0; kb < kend; kb += 32) {
-    // K rows of this block (rows past Skv re-read the last key; masked below)
-    float4 kf[NCH];
+  // K rows of a block (rows past Skv re-read the last key; masked below) and its
+  // V operands (register r's key, columns 32t + l%32); the next block's are
+  // loaded while this one computes
+  float4 kf[NCH], kn[NCH];
+  float vf[NDT][16], vn[NDT][16];
+  auto load_block = [&](int kb, float4 (&kx)[NCH], float (&vx)[NDT][16]) {
     const int krow = min(kb + qc, p.Skv - 1);
 #pragma unroll
-    for (int i = 0; i < NCH; ++i) kf[i] = *(const float4*)(kbase + (int64_t)krow * p.ldk + 8 * i + 4 * half);
-    // V operands: register r's key, columns 32t + l%32
-    float vf[NDT][16];
+    for (int i = 0; i < NCH; ++i) kx[i] = *(const float4*)(kbase + (int64_t)krow * p.ldk + 8 * i + 4 * half);
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int key = min(kb + 8 * (r >> 2) + 4 * half + (r & 3), p.Skv - 1);
 #pragma unroll
-      for (int t = 0; t < NDT; ++t) vf[t][r] = vbase[(int64_t)key * p.ldv + 32 * t + qc];
+      for (int t = 0; t < NDT; ++t) vx[t][r] = vbase[(int64_t)key * p.ldv + 32 * t + qc];
     }
+  };
+  if (kend > 0) load_block(0, kn, vn);
+  for (int kb = 0; kb < kend; kb += 32) {
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) kf[i] = kn[i];
+#pragma unroll
+    for (int t = 0; t < NDT; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) vf[t][r] = vn[t][r];
+    if (kb + 32 < kend) load_block(kb + 32, kn, vn);
     f32x16_t st;
 #pragma unroll
     for (int r = 0; r < 16; ++r) st[r] = 0.f;

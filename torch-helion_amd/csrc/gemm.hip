@@ -1242,61 +1242,87 @@ __global__ void __launch_bounds__(256, 1) gemm_f32_kernel(GemmK p) {
 // A workgroup computes 32 rows x BNC packed columns with NSUB = BNC / 32
 // column slices times KS K slices of one wave each (NSUB * KS <= 16 waves), so
 // a GEMM of a few hundred rows (the fp32 Llama block: 128 tokens) still runs
-// on every SIMD. Each wave multiplies its 32 x 32 subtile over its K slice
-// with operands read straight from memory in the MFMA layout (lane l: row
-// l % 32, one float4 at k + 4 (l / 32); its four components are four k = 2
-// steps, the contraction index permuted the same way on both sides). The KS
-// partial tiles are summed through LDS in slice order, then the ordinary
+// on every SIMD. Each wave multiplies its 32 x 32 subtile over its K slice.
+// Operands: per 8-wide K step, lane l takes row l % 32 and the float4 at
+// k + 4 (l / 32) (its four components are four k = 2 steps of
+// v_mfma_f32_32x32x2f32, the contraction index permuted the same way on both
+// sides). They come through a wave-private LDS ring of PD steps filled by
+// direct-to-LDS loads (lane l's 16 bytes land at slot + 16 l, which is also
+// where it reads them back), so PD steps of loads are in flight with no
+// workgroup barrier; explicit vmcnt waits cover the untracked loads. The KS
+// partial tiles are then summed through LDS in slice order, and the ordinary
 // slab epilogue runs on the first 256 threads.
 template <int BNC>
 __global__ void __launch_bounds__(1024, 1) gemm_f32_sk_kernel(GemmK p) {
+#if defined(__HIP_DEVICE_COMPILE__)  // gfx950 LDS-load instructions exist only in the device pass
   constexpr int NSUB = BNC / 32;
   constexpr int KS = 16 / NSUB > 0 ? 16 / NSUB : 1;
-  constexpr int NT = 64 * NSUB * KS;
+  constexpr int NWV = NSUB * KS, NT = 64 * NWV;
   constexpr int SROW = BNC + 8;
-  __shared__ __attribute__((aligned(16))) float part[KS * 32 * BNC];
-  __shared__ __attribute__((aligned(16))) float slab[32 * SROW];
+  constexpr int SLAB = 32 * SROW * 4;            // epilogue slab bytes
+  constexpr int PART = KS * 32 * BNC * 4;        // partial tiles (after the K loop)
+  constexpr int STEP = 2048;                     // one K step of a wave: A then B, 1 KB each
+  constexpr int PD = (160 * 1024 - SLAB - 2048) / (NWV * STEP) >= 4 ? 4 : 3;
+  constexpr int RING = NWV * PD * STEP;
+  constexpr int BODY = RING > PART ? RING : PART;
+  __shared__ __attribute__((aligned(16))) char smem[BODY + SLAB];
   __shared__ float ssp[KS * 32];
   __shared__ float rs[32];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  float* part = (float*)smem;
+  float* slab = (float*)(smem + BODY);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int ns = wave % NSUB, ks = wave / NSUB;
   int tmi, tni;
   map_tile(p.tiles_m, p.tiles_n, tmi, tni);
   const int64_t m0 = (int64_t)tmi * 32;
   const int row = (int)min(m0 + (lane & 31), p.M - 1);  // rows past M re-read row M-1 (never stored)
-  const float* A = (const float*)p.A + (int64_t)row * p.lda;
-  const float* B = (const float*)p.B + ((int64_t)tni * BNC + ns * 32 + (lane & 31)) * p.ldb;
+  const int h4 = 4 * (lane >> 5);
   // K slice of this wave: whole 8-wide steps
   const int64_t kq = (p.K + 8 * KS - 1) / (8 * KS) * 8;
   const int64_t k0 = ks * kq, k1 = min(p.K, k0 + kq);
-  const int h4 = 4 * (lane >> 5);
+  const int nsteps = k1 > k0 ? (int)((k1 - k0 + 7) / 8) : 0;
+  // per-lane byte offsets from uniform bases (the host keeps both operands under 2^31 bytes);
+  // a float4 past the slice re-reads the slice's last one (K % 4 == 0), zeroed where used
+  const char* Ab = (const char*)p.A;
+  const char* Bb = (const char*)p.B;
+  const uint32_t arow = (uint32_t)((int64_t)row * p.lda * 4);
+  const uint32_t brow = (uint32_t)(((int64_t)tni * BNC + ns * 32 + (lane & 31)) * p.ldb * 4);
+  const int64_t klast = k1 > k0 ? k1 - 4 : 0;
+  const uint32_t ring = (uint32_t)(uintptr_t)smem + (uint32_t)(wave * PD * STEP);
+  auto issue = [&](int st) {  // step st into ring slot st % PD
+    const int64_t k = k0 + 8 * (int64_t)st + h4;
+    const uint32_t kb = (uint32_t)(min(k, klast) * 4);
+    const uint32_t dst = ring + (uint32_t)((st % PD) * STEP);
+    dma_load16(Ab, arow + kb, dst);
+    dma_load16(Bb, brow + kb, dst + 1024);
+  };
   f32x16_t acc;
 #pragma unroll
   for (int r = 0; r < 16; ++r) acc[r] = 0.f;
   float ss = 0.f;
-  // (K is a multiple of 4: a float4 at k + h4 lies wholly inside K or wholly past it)
-  auto ld = [&](int64_t k, float4& a, float4& b) {
-    const bool in = k + h4 < k1;
-    a = in ? *(const float4*)(A + k + h4) : make_float4(0.f, 0.f, 0.f, 0.f);
-    b = in ? *(const float4*)(B + k + h4) : make_float4(0.f, 0.f, 0.f, 0.f);
-  };
-  float4 a0, b0, a1, b1;
-  ld(k0, a0, b0);
-  for (int64_t k = k0; k < k1; k += 16) {
-    ld(k + 8, a1, b1);
-    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a0.x, b0.x, acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a0.y, b0.y, acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a0.z, b0.z, acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a0.w, b0.w, acc, 0, 0, 0);
-    if (p.sumsq && ns == 0) ss += a0.x * a0.x + a0.y * a0.y + a0.z * a0.z + a0.w * a0.w;
-    if (k + 8 >= k1) break;
-    ld(k + 16, a0, b0);
-    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a1.x, b1.x, acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a1.y, b1.y, acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a1.z, b1.z, acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a1.w, b1.w, acc, 0, 0, 0);
-    if (p.sumsq && ns == 0) ss += a1.x * a1.x + a1.y * a1.y + a1.z * a1.z + a1.w * a1.w;
+#pragma unroll
+  for (int j = 0; j < PD; ++j) issue(j);
+  for (int st = 0; st < nsteps; ++st) {
+    // step st has landed when at most the PD - 1 later steps' loads are in flight
+    wait_vmcnt<2 * (PD - 1)>();
+    asm volatile("" ::: "memory");
+    const char* slotp = smem + wave * PD * STEP + (st % PD) * STEP;
+    float4 a = *(const float4*)(slotp + 16 * lane);
+    float4 b = *(const float4*)(slotp + 1024 + 16 * lane);
+    if (!(k0 + 8 * (int64_t)st + h4 < k1)) a = b = make_float4(0.f, 0.f, 0.f, 0.f);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.x, b.x, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.y, b.y, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.z, b.z, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.w, b.w, acc, 0, 0, 0);
+    ss += a.x * a.x + a.y * a.y + a.z * a.z + a.w * a.w;  // (used only with sumsq)
+    // the slot's reads are consumed (the MFMAs above used them): refill it;
+    // past the last step the loads re-read the slice end, so every wait keeps its count
+    asm volatile("" ::: "memory");
+    issue(st + PD);
   }
+  wait_vmcnt<0>();   // no direct-to-LDS load lands after this point
+  __syncthreads();   // every wave is done with the rings before they hold the partial tiles
   // partial tile of slice ks: part[ks][row][col], rows 8(r/4) + 4(l/32) + r%4, column l%32
 #pragma unroll
   for (int r = 0; r < 16; ++r)
@@ -1323,6 +1349,140 @@ __global__ void __launch_bounds__(1024, 1) gemm_f32_sk_kernel(GemmK p) {
   }
   __syncthreads();
   if (tid < 256) epilogue_slab(p, slab, SROW, 32, rs, m0, tni, tid);
+#endif
+}
+
+// ------------------------- fp32 MFMA, small grids with a workspace (split-K over workgroups)
+// Pass 1 (gemm_f32_ksp_kernel): workgroup (tile, g) multiplies 32 rows x BNC
+// packed columns over K slice g, one wave per 32 x 32 subtile, with the same
+// operand layout and wave-private LDS ring as gemm_f32_sk_kernel, and stores its
+// partial tile to part[g][row][column] (rows of the padded row count Mp); the
+// column-0 workgroups also store the slice's row sums of squares ssq[g][row].
+// Pass 2 (gemm_f32_ksr_kernel): one workgroup per 8 rows x BNC columns sums the
+// KSG partials in slice order (deterministic) into an LDS slab and runs the
+// slab epilogue. Enough workgroups to cover the GPU (about two per CU) for the
+// fp32 block's GEMMs of 128 rows, which one workgroup per tile cannot.
+struct F32Ksp {
+  GemmK k;
+  float* part;  // [KSG][Mp][Npk]
+  float* ssq;   // [KSG][Mp]
+  int64_t Mp, Npk, kq;
+  int ksg;
+};
+
+template <int BNC>
+__global__ void __launch_bounds__(BNC * 2) gemm_f32_ksp_kernel(F32Ksp q) {
+#if defined(__HIP_DEVICE_COMPILE__)  // gfx950 LDS-load instructions exist only in the device pass
+  constexpr int NSUB = BNC / 32, STEP = 2048, PD = 4;
+  __shared__ __attribute__((aligned(16))) char smem[NSUB * PD * STEP];
+  const GemmK& p = q.k;
+  const int lane = threadIdx.x & 63;
+  const int ns = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  int tmi, tni;
+  map_tile(p.tiles_m, p.tiles_n, tmi, tni);
+  const int g = blockIdx.y;
+  const int64_t m0 = (int64_t)tmi * 32;
+  const int row = (int)min(m0 + (lane & 31), p.M - 1);  // rows past M re-read row M-1 (never stored)
+  const int h4 = 4 * (lane >> 5);
+  const int64_t k0 = g * q.kq, k1 = min(p.K, k0 + q.kq);
+  const int nsteps = k1 > k0 ? (int)((k1 - k0 + 7) / 8) : 0;
+  const char* Ab = (const char*)p.A;
+  const char* Bb = (const char*)p.B;
+  const uint32_t arow = (uint32_t)((int64_t)row * p.lda * 4);
+  const uint32_t brow = (uint32_t)(((int64_t)tni * BNC + ns * 32 + (lane & 31)) * p.ldb * 4);
+  const int64_t klast = k1 > k0 ? k1 - 4 : 0;
+  const uint32_t ring = (uint32_t)(uintptr_t)smem + (uint32_t)(ns * PD * STEP);
+  auto issue = [&](int st) {  // step st into ring slot st % PD (past the slice: the slice end again)
+    const int64_t k = k0 + 8 * (int64_t)st + h4;
+    const uint32_t kb = (uint32_t)(min(k, klast) * 4);
+    const uint32_t dst = ring + (uint32_t)((st % PD) * STEP);
+    dma_load16(Ab, arow + kb, dst);
+    dma_load16(Bb, brow + kb, dst + 1024);
+  };
+  f32x16_t acc;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < PD; ++j) issue(j);
+  for (int st = 0; st < nsteps; ++st) {
+    wait_vmcnt<2 * (PD - 1)>();  // step st landed; the PD - 1 later steps may be in flight
+    asm volatile("" ::: "memory");
+    const char* slotp = smem + ns * PD * STEP + (st % PD) * STEP;
+    float4 a = *(const float4*)(slotp + 16 * lane);
+    float4 b = *(const float4*)(slotp + 1024 + 16 * lane);
+    if (!(k0 + 8 * (int64_t)st + h4 < k1)) a = b = make_float4(0.f, 0.f, 0.f, 0.f);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.x, b.x, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.y, b.y, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.z, b.z, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.w, b.w, acc, 0, 0, 0);
+    ss += a.x * a.x + a.y * a.y + a.z * a.z + a.w * a.w;  // (used only with sumsq)
+    asm volatile("" ::: "memory");
+    issue(st + PD);
+  }
+  wait_vmcnt<0>();  // no direct-to-LDS load lands after the workgroup ends
+  // partial subtile: rows 8(r/4) + 4(l/32) + r%4, column l%32 (32 lanes store 128 contiguous bytes)
+  float* dst = q.part + ((int64_t)g * q.Mp + m0 + h4) * q.Npk + (int64_t)tni * BNC + ns * 32 + (lane & 31);
+#pragma unroll
+  for (int r = 0; r < 16; ++r) dst[(int64_t)(8 * (r >> 2) + (r & 3)) * q.Npk] = acc[r];
+  if (p.sumsq && ns == 0 && tni == 0) {
+    const float v = ss + __shfl_xor(ss, 32);
+    if (lane < 32) q.ssq[(int64_t)g * q.Mp + m0 + lane] = v;
+  }
+#endif
+}
+
+template <int BNC>
+__global__ void __launch_bounds__(256) gemm_f32_ksr_kernel(F32Ksp q) {
+  constexpr int RB = 8, SROW = BNC + 8, V4 = RB * BNC / 4;  // float4s of the 8-row slab
+  __shared__ __attribute__((aligned(16))) float slab[RB * SROW];
+  __shared__ float rs[RB];
+  const GemmK& p = q.k;
+  const int tid = threadIdx.x;
+  const int tn = (int)blockIdx.x % p.tiles_n, tr = (int)blockIdx.x / p.tiles_n;
+  const int64_t r0 = (int64_t)tr * RB;
+  for (int v = tid; v < V4; v += 256) {
+    const int r = v / (BNC / 4), c4 = (v - r * (BNC / 4)) * 4;
+    const float* src = q.part + (r0 + r) * q.Npk + (int64_t)tn * BNC + c4;
+    const int64_t plane = q.Mp * q.Npk;
+    float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+    // slices in order, eight loads in flight at a time
+    for (int g0 = 0; g0 < q.ksg; g0 += 8) {
+      float4 x[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (g0 + u < q.ksg) x[u] = *(const float4*)(src + (int64_t)(g0 + u) * plane);
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (g0 + u < q.ksg) {
+          a.x += x[u].x; a.y += x[u].y; a.z += x[u].z; a.w += x[u].w;
+        }
+    }
+    *(float4*)(slab + r * SROW + c4) = a;
+  }
+  if (p.sumsq && tid < RB) {
+    float v = 0.f;
+    for (int g = 0; g < q.ksg; ++g) v += q.ssq[(int64_t)g * q.Mp + r0 + tid];
+    rs[tid] = rsqrtf(v * p.inv_k + p.eps);
+    const int64_t gr = r0 + tid;
+    if (p.sumsq_out && tn == 0 && gr < p.M) p.sumsq_out[gr] = v;
+  }
+  __syncthreads();
+  epilogue_slab(p, slab, SROW, RB, rs, r0, tn, tid);
+}
+
+// K slices of the split-K fp32 path for tiles 32-row x BNC tiles: about two
+// workgroups per CU, each slice at least two 8-wide steps
+static int f32_ksp_slices(int64_t tiles, int64_t K) {
+  const int64_t cus = device_cus() > 0 ? device_cus() : 256;
+  const int64_t want = cdiv(2 * cus, tiles);
+  return (int)std::max((int64_t)1, std::min({want, cdiv(K, 16), (int64_t)64}));
+}
+
+static int64_t f32_ksp_bytes(int64_t M, int64_t Npk, int64_t K, int bnc) {
+  const int64_t Mp = cdiv(M, 32) * 32;
+  const int ksg = f32_ksp_slices(cdiv(M, 32) * (Npk / bnc), K);
+  return (int64_t)ksg * Mp * (Npk + 1) * 4;
 }
 
 // ------------------------------------------------------------------ packing
@@ -1439,8 +1599,15 @@ extern "C" int64_t th_gemm_packed_bytes(int64_t N, int64_t K, int32_t n_acc, int
 
 extern "C" int64_t th_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t n_acc, int32_t in_dtype) {
   if (M <= 0 || N <= 0 || K <= 0 || n_acc < 1 || n_acc > TH_MAX_ACC || !gemm_in_ok(in_dtype)) return -1;
-  if (in_dtype != TH_F8E4M3) return 0;
   const int bn = choose_bn(N, n_acc, in_dtype);
+  if (in_dtype == TH_F32) {
+    // the split-K pass of small grids (too few 64-row tiles to occupy the GPU); optional:
+    // without it th_gemm splits K inside each workgroup instead
+    const int64_t cus = device_cus() > 0 ? device_cus() : 256;
+    if (cdiv(M, 64) * cdiv(N, bn) >= cus) return 0;
+    return f32_ksp_bytes(M, cdiv(N, bn) * bn * n_acc, K, bn * n_acc);
+  }
+  if (in_dtype != TH_F8E4M3) return 0;
   return fp8_workspace_bytes(M, cdiv(N, bn) * bn * n_acc, K, bn, n_acc);
 }
 
@@ -1567,6 +1734,13 @@ static void launch_f32_sk(const GemmK& k, hipStream_t s) {
   hipLaunchKernelGGL((gemm_f32_sk_kernel<BNC>), dim3(k.tiles_m * k.tiles_n), dim3(64 * NSUB * KS), 0, s, k);
 }
 
+// 32-row tiles, K split over workgroups through the workspace, then the reduce / epilogue pass
+template <int BNC>
+static void launch_f32_ksp(const F32Ksp& q, hipStream_t s) {
+  hipLaunchKernelGGL((gemm_f32_ksp_kernel<BNC>), dim3(q.k.tiles_m * q.k.tiles_n, q.ksg), dim3(2 * BNC), 0, s, q);
+  hipLaunchKernelGGL((gemm_f32_ksr_kernel<BNC>), dim3((unsigned)(q.Mp / 8 * q.k.tiles_n)), dim3(256), 0, s, q);
+}
+
 extern "C" int th_gemm(const th_gemm_desc* d, void* stream) {
   TH_CHECK_ARG(d != nullptr, "th_gemm: null descriptor");
   TH_CHECK_ARG(d->M > 0 && d->N > 0 && d->K > 0, "th_gemm: M=%lld N=%lld K=%lld must be positive",
@@ -1685,9 +1859,35 @@ extern "C" int th_gemm(const th_gemm_desc* d, void* stream) {
   }
   if (d->in_dtype == TH_F32) {
     const int64_t cus = device_cus() > 0 ? device_cus() : 256;
-    if (cdiv(d->M, 64) * k.tiles_n < cus) {
-      // too few 64-row tiles to occupy the GPU: 32-row tiles with the K loop split over 16 waves
+    // (32-bit per-lane byte offsets into both operands)
+    const bool small_ok = d->M * d->ld_lhs * 4 < ((int64_t)1 << 31) && (int64_t)cdiv(d->N, bn) * bnc * k.ldb * 4 <
+                                                                             ((int64_t)1 << 31);
+    if (small_ok && cdiv(d->M, 64) * k.tiles_n < cus) {
       k.tiles_m = (int)cdiv(d->M, 32);
+      const int64_t npk = (int64_t)k.tiles_n * bnc;
+      if (d->workspace && d->workspace_bytes >= f32_ksp_bytes(d->M, npk, d->K, bnc) &&
+          ((uintptr_t)d->workspace & 15) == 0) {
+        // too few 64-row tiles to occupy the GPU: K split over workgroups through the workspace
+        F32Ksp q{};
+        q.k = k;
+        q.Mp = (int64_t)k.tiles_m * 32;
+        q.Npk = npk;
+        q.ksg = f32_ksp_slices((int64_t)k.tiles_m * k.tiles_n, d->K);
+        q.kq = cdiv(cdiv(d->K, q.ksg), 8) * 8;
+        q.ksg = (int)cdiv(d->K, q.kq);
+        q.part = d->workspace;
+        q.ssq = d->workspace + q.ksg * q.Mp * q.Npk;
+        switch (bnc) {
+          case 64: launch_f32_ksp<64>(q, s); break;
+          case 128: launch_f32_ksp<128>(q, s); break;
+          case 192: launch_f32_ksp<192>(q, s); break;
+          case 256: launch_f32_ksp<256>(q, s); break;
+          default: set_error("th_gemm: no fp32 kernel for tile %d", bnc); return TH_ERR_UNSUPPORTED;
+        }
+        TH_CHECK_LAUNCH();
+        return TH_OK;
+      }
+      // without a workspace: 32-row tiles with the K loop split over the waves of a workgroup
       switch (bnc) {
         case 64: launch_f32_sk<64>(k, s); break;
         case 128: launch_f32_sk<128>(k, s); break;

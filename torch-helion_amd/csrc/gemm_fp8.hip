@@ -897,8 +897,14 @@ using namespace th;
 
 extern "C" int th_gemm_noalloc(const th_gemm_desc* d, void* stream) {
   TH_CHECK_ARG(d != nullptr, "th_gemm_noalloc: null descriptor");
-  // bf16 / fp32 weights use no scratch memory: the call is th_gemm itself
-  if (d->in_dtype != TH_F8E4M3) return th_gemm(d, stream);
+  // bf16 / fp32 weights: th_gemm with no workspace (fp32 small grids then split K
+  // inside each workgroup instead of through a workspace)
+  if (d->in_dtype != TH_F8E4M3) {
+    th_gemm_desc c = *d;
+    c.workspace = nullptr;
+    c.workspace_bytes = 0;
+    return th_gemm(&c, stream);
+  }
   const int64_t need = th_gemm_workspace_bytes(d->M, d->N, d->K, d->n_acc, d->in_dtype);
   TH_CHECK_ARG(need <= (int64_t)TH_GEMM_NOALLOC_SCRATCH_BYTES,
                "th_gemm_noalloc: M=%lld N=%lld K=%lld n_acc=%d need %lld bytes of scratch, above the fixed %lld "

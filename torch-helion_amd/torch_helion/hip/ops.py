@@ -104,7 +104,7 @@ class GemmCall:
     sumsq_out: torch.Tensor | None = None
     in_dtype: torch.dtype | None = None        # torch.float8_e4m3fn: bf16 lhs x e4m3 packed rhs
     rhs_scale: torch.Tensor | None = None      # fp8: [n_acc, N] fp32 per-column scales
-    workspace: torch.Tensor | None = None      # fp8: gemm_workspace_bytes(...) bytes
+    workspace: torch.Tensor | None = None      # gemm_workspace_bytes(...) bytes (fp8: required; fp32: optional)
     lhs_gain: torch.Tensor | None = None       # fp8: [K] fp32, products use lhs * gain (RMSNorm gain)
 
     def descriptor(self) -> abi.GemmDesc:

@@ -630,6 +630,11 @@ class DeviceProgram:
         info = {"n_acc": len(used), "ops": [op for _, op, *_ in outs], "rscale": plan.rscale is not None,
                 "rope_fused": any(op == abi.EPI_ROPE for _, op, *_ in outs), "gain_on_activation": normed is not None}
         fp8_kw: dict[str, Any] = {}
+        if in_dtype == torch.float32 and collect is None:
+            # small fp32 grids split K over workgroups through a workspace (0 bytes otherwise)
+            nb = ops.gemm_workspace_bytes(T, N, K, len(used), torch.float32)
+            if nb > 0:
+                fp8_kw["workspace"] = self._workspace(nb, torch.uint8)
         if fp8:
             scale_t = [rhs_of[i] + "_scale" for i in used]
             names = {x.name for x in spec.args}
