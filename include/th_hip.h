@@ -132,9 +132,12 @@ typedef struct th_gemm_desc {
   const float* lhs_gain;  /* optional [K] fp32 per-column gain of lhs (TH_F8E4M3 only; 16-byte aligned) */
 } th_gemm_desc;
 
-/* Per-accumulator column tile th_gemm uses for (N, n_acc, in_dtype); a block
- * computes n_acc * tile columns. Fused RoPE (TH_EPI_ROPE) needs the tile to
- * be a multiple of the head dim. Returns 0 for invalid arguments. */
+/* Per-accumulator column tile th_gemm uses for (N, n_acc, in_dtype) when an
+ * output is fused RoPE; a block computes n_acc * tile columns, and fused RoPE
+ * (TH_EPI_ROPE) needs the tile to be a multiple of the head dim. (Without
+ * RoPE, one bf16 accumulator over a multiple of 256 columns may run on
+ * 256-column tiles instead, which the packed layout allows.) Returns 0 for
+ * invalid arguments. */
 int th_gemm_acc_tile(int64_t N, int32_t n_acc, int32_t in_dtype);
 
 /* Bytes of the packed right-hand side for th_gemm (weights are packed once

@@ -467,6 +467,33 @@ def test_gemm_extra_ops(gpu):
     assert _rel(o[3], acc * torch.sigmoid(acc)) < 1e-5
 
 
+@pytest.mark.parametrize("M", [16384, 16300])
+def test_gemm_whole_wave_wide_tiles(gpu, M):
+    """One accumulator over 1024 columns at 64 row tiles of 256: exactly one wave of
+    256 x 256 tiles on a 256-CU device, the tile th_gemm then takes instead of two
+    256 x 128 tiles per CU (the Mamba-2 out-projection with its fp32 residual; a ragged
+    last row tile in the second case)."""
+    from torch_helion.hip import abi, ops
+
+    announce(f"gemm bf16 whole-wave 256x256 tiles M={M}")
+    N, K = 1024, 2048
+    g = torch.Generator().manual_seed(M)
+    a = torch.randn(M, K, generator=g).bfloat16()
+    w = (torch.randn(K, N, generator=g) * 0.03).bfloat16()
+    res = torch.randn(M, N, generator=g)
+    ref = a.float() @ w.float() + res
+    packed = ops.pack_rhs([w.to(gpu)], torch.bfloat16)
+    o16 = torch.empty(M, N, dtype=torch.bfloat16, device=gpu)
+    o32 = torch.empty(M, N, dtype=torch.float32, device=gpu)
+    ops.gemm(ops.GemmCall(M, N, K, 1, a.to(gpu), packed,
+                          [ops.EpiSpec(abi.EPI_ADD, o16, e=0), ops.EpiSpec(abi.EPI_ADD, o32, e=0)],
+                          extras=[res.to(gpu)]))
+    torch.cuda.synchronize()
+    assert _rel(o32, ref) < 1e-5
+    assert _maxabs(o16, ref) < 4 * BF16_TOL   # |ref| up to ~8: bf16 rounding of the output itself
+    assert _rel(o16, ref) < 1e-2
+
+
 @pytest.mark.parametrize("M,N,K,case", [(128, 1376, 512, "add"), (128, 1376, 512, "rms_swiglu"),
                                          (100, 200, 136, "acc"), (77, 96, 1380, "add"), (4096, 512, 256, "add")])
 def test_gemm_f32_small(gpu, M, N, K, case):

@@ -49,9 +49,9 @@ class CompileConfig:
     fp32_outputs: bool = True                     # producers of program outputs also write an fp32 copy
     residual_fp32: bool = True                    # residual operands of GEMM epilogues travel in fp32
     merge_siblings: bool | None = None            # GEMM kernels sharing an lhs run as one launch (column windows);
-                                                  # None: when every GEMM has at most 4096 rows (C2: 109 -> 99 us,
-                                                  # where launch latency dominates; at C4's 16384 rows the
-                                                  # concatenated width adds a ragged tile column: 16.7 -> 17.0 ms)
+                                                  # None: where the planner prices one launch below the separate
+                                                  # ones (optimizer/planner.py price_launch_merges; reported in
+                                                  # 05_plan/plan.md); True / False: always / never
     cpu_flop_budget: float = 2e10                 # graphs above this skip CPU-side checks in "auto" mode
     reuse_buffers: bool = True                    # intermediates share device buffers by liveness
     merge_convs: bool = True                      # the depthwise convolutions feeding one SSD run as one launch

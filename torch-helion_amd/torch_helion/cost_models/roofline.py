@@ -65,15 +65,24 @@ def _bytes(t: TensorType) -> int:
     return t.numel * DTYPE_BYTES.get(t.dtype, 4)
 
 
-def gemm_tiles(N: int, n_acc: int, M: int, dtype: str) -> tuple[int, int]:
-    """(BM, per-accumulator column tile) the HIP GEMM picks (mirrors csrc/gemm.hip)."""
+def gemm_tiles(N: int, n_acc: int, M: int, dtype: str, cus: int = 256) -> tuple[int, int]:
+    """(BM, per-accumulator column tile) the HIP GEMM picks (mirrors th_gemm in csrc/gemm.hip:
+    256-row tiles when they still give two blocks per CU, 128 when they give one, else 64;
+    one accumulator over a multiple of 256 columns takes 256 x 256 tiles when they make
+    whole waves)."""
     if dtype == "float32":
         bn = {1: 128 if N > 64 else 64, 2: 64 if N > 32 else 32, 3: 64}.get(n_acc, 64 if N > 32 else 32)
         return 64, bn
-    bn = {1: 256 if N >= 192 else (128 if N > 64 else 64), 2: 128 if N >= 128 else (64 if N > 32 else 32),
+    bn = {1: 256 if N >= 2048 else (128 if N >= 768 else 64), 2: 128 if N >= 128 else (64 if N > 32 else 32),
           3: 64}.get(n_acc, 64 if N > 32 else 32)
-    big = math.ceil(M / 256) * math.ceil(N / bn) >= 512
-    return (256 if big else 128), bn
+    if n_acc == 1 and bn == 128 and N % 256 == 0:
+        t256 = math.ceil(M / 256) * (N // 256)
+        if t256 >= cus and t256 % cus == 0:    # whole waves of 256 x 256 tiles
+            return 256, 256
+    tn = math.ceil(N / bn)
+    if math.ceil(M / 256) * tn >= 2 * cus:
+        return 256, bn
+    return (128 if math.ceil(M / 128) * tn >= cus else 64), bn
 
 
 def category(spec: KernelSpec, tensors: dict[str, TensorType]) -> str:
@@ -93,24 +102,28 @@ def category(spec: KernelSpec, tensors: dict[str, TensorType]) -> str:
 
 
 def _compose(hw: HardwareSpec, flops: float, nbytes: float, mfma_flops: float, blocks: int, dtype: str,
-             tiles: dict[str, int], detail: dict[str, Any], cat: str) -> CostBreakdown:
+             tiles: dict[str, int], detail: dict[str, Any], cat: str, wave_scale: float = 1.0) -> CostBreakdown:
     """Time of the binding roofline. With a calibration fitted for ``cat``: ideal time at
-    100% of peak over the fitted efficiency plus the fitted launch overhead; without one,
-    the hardware spec's generic MFMA / HBM efficiencies and overhead."""
+    100% of peak over the fitted efficiency plus the fitted launch overhead, plus the fitted
+    cost per wave of tiles times ``wave_scale`` (a GEMM tile's area relative to 256 x 256:
+    its pipeline fill and epilogue); without one, the hardware spec's generic MFMA / HBM
+    efficiencies and overhead."""
     calib = hw.calibration
     fitted = calib.get("efficiency", {}).get(cat)
     eff_m = fitted if fitted else hw.efficiency.get("mfma", 0.6)
     eff_h = fitted if fitted else hw.efficiency.get("hbm", 0.7)
-    overhead = calib.get("launch_overhead_us", hw.launch_overhead_us) if fitted else hw.launch_overhead_us
+    overhead = hw.launch_overhead_us
+    if fitted:
+        overhead = calib.get("fixed_us", {}).get(cat, calib.get("launch_overhead_us", hw.launch_overhead_us))
     waves = max(1, math.ceil(blocks / hw.compute_units)) if blocks else 1
     per_block = mfma_flops / max(blocks, 1)
     t_mfma = waves * per_block / (hw.peak_flops(dtype) / hw.compute_units * eff_m) * 1e6 if mfma_flops else 0.0
     t_hbm = nbytes / (hw.hbm_bytes_per_s() * eff_h) * 1e6
     us = max(t_mfma, t_hbm) + overhead
     if fitted:
-        us += waves * calib.get("tile_us", {}).get(cat, 0.0)
+        us += waves * wave_scale * calib.get("tile_us", {}).get(cat, 0.0)
     bound = "mfma" if t_mfma >= t_hbm else "hbm"
-    detail = {**detail, "category": cat, "calibrated": bool(fitted)}
+    detail = {**detail, "category": cat, "calibrated": bool(fitted), "wave_scale": wave_scale}
     return CostBreakdown(us, flops, nbytes, bound, tiles, blocks, waves, t_mfma, t_hbm, detail)
 
 
@@ -132,15 +145,55 @@ def gemm_cost(spec: KernelSpec, tensors: dict[str, TensorType], hw: HardwareSpec
         flops = 2.0 * T * N * K * n_acc
         return _compose(hw, flops, nbytes, flops, math.ceil(N / 64), "float8_e4m3fn", {"tile_n": 64},
                         {"n_acc": n_acc, "weights": "float8_e4m3fn"}, "gemm_fp8")
+    return _gemm_compose(hw, T, N, K, n_acc, dtype, nbytes,
+                         {"n_acc": n_acc, "sumsq": spec.sumsq, "extras": len(extras), "outputs": len(spec.outputs)})
+
+
+def _gemm_compose(hw: HardwareSpec, T: int, N: int, K: int, n_acc: int, dtype: str, nbytes: float,
+                  detail: dict[str, Any]) -> CostBreakdown:
+    """bf16 / fp32 GEMM of T x (n_acc N) x K on the HIP kernel's tiles."""
     flops = 2.0 * T * N * K * n_acc
-    bm, bn = gemm_tiles(N, n_acc, T, dtype)
+    bm, bn = gemm_tiles(N, n_acc, T, dtype, hw.compute_units)
     tiles_m, tiles_n = math.ceil(T / bm), math.ceil(N / bn)
     kq = math.ceil(K / (16 if dtype == "float32" else 64)) * (16 if dtype == "float32" else 64)
+    if dtype == "float32" and tiles_m * tiles_n < hw.compute_units:
+        # fp32 grids too small for the GPU: 32-row tiles, K split over about two
+        # workgroups per CU (th_gemm's workspace path), a second pass sums the slices
+        tiles_m = math.ceil(T / 32)
+        ksg = max(1, min(math.ceil(2 * hw.compute_units / (tiles_m * tiles_n)), math.ceil(K / 16), 64))
+        mfma = 2.0 * tiles_m * 32 * tiles_n * bn * n_acc * kq
+        return _compose(hw, flops, nbytes, mfma, tiles_m * tiles_n * ksg, dtype,
+                        {"tile_t": 32, "tile_n": bn, "k_slices": ksg}, detail, "gemm_fp32",
+                        wave_scale=32 * bn * n_acc / 65536.0)
     mfma = 2.0 * tiles_m * bm * tiles_n * bn * n_acc * kq
     return _compose(hw, flops, nbytes, mfma, tiles_m * tiles_n, dtype,
-                    {"tile_t": bm, "tile_n": bn, "tile_k": 16 if dtype == "float32" else 64},
-                    {"n_acc": n_acc, "sumsq": spec.sumsq, "extras": len(extras), "outputs": len(spec.outputs)},
-                    "gemm_fp32" if dtype == "float32" else "gemm_bf16")
+                    {"tile_t": bm, "tile_n": bn, "tile_k": 16 if dtype == "float32" else 64}, detail,
+                    "gemm_fp32" if dtype == "float32" else "gemm_bf16", wave_scale=bm * bn * n_acc / 65536.0)
+
+
+def merged_gemm_cost(specs: list[KernelSpec], used: list[int], tensors: dict[str, TensorType],
+                     hw: HardwareSpec) -> CostBreakdown:
+    """Sibling GEMM kernels (one lhs, one K) run as ONE launch: the used weight
+    columns of every kernel concatenated into a single accumulator, each output
+    on its own column window (hip/runtime.py's merged launch). ``used[i]``: the
+    accumulators kernel i contributes."""
+    s0 = specs[0]
+    T, K = s0.grid["rows"], s0.k_extent
+    dtype = _dtype(s0, tensors)
+    eb = DTYPE_BYTES.get(dtype, 4)
+    n_tot = sum(sp.grid["cols"] * u for sp, u in zip(specs, used))
+    extras = {a.tensor for sp in specs for a in sp.args if a.role == "extra"}
+    outs = sum(len(sp.outputs) * T * sp.grid["cols"] for sp in specs)
+    nbytes = T * K * eb + n_tot * K * eb + sum(_bytes(tensors[t]) for t in extras) + outs * eb
+    c = _gemm_compose(hw, T, n_tot, K, 1, dtype, nbytes, {"merged": [sp.name for sp in specs], "cols": n_tot})
+    # Measured merged launches run slower than a plain GEMM of their shape (every output
+    # window through the general LDS-staged epilogue, a partial last wave of wide tiles):
+    # the calibration fits that as one factor over the merged launches it has seen.
+    f = hw.calibration.get("merged_launch_factor")
+    if f and c.detail.get("calibrated"):
+        c.us *= f
+        c.detail["merged_launch_factor"] = f
+    return c
 
 
 def attention_cost(spec: KernelSpec, tensors: dict[str, TensorType], hw: HardwareSpec) -> CostBreakdown:

@@ -21,6 +21,8 @@ CSRC = PROJECT / "csrc"
 INCLUDE = REPO / "include"
 BUILD_DIR = PROJECT / "_build"
 LIB_PATH = PKG_ROOT / "lib" / "libth_hip.so"
+PROBE_SRC = PKG_ROOT / "hwspec" / "probe.hip"
+PROBE_PATH = PKG_ROOT / "lib" / "th_probe"
 
 ARCH = "gfx950"
 HIPCC_FLAGS = [
@@ -74,5 +76,21 @@ def build(jobs: int | None = None, verbose: bool = False) -> Path:
     return LIB_PATH
 
 
+def build_probe(verbose: bool = False) -> Path:
+    """Compile the peak probe (MFMA rate, HBM stream bandwidth; hwspec/probe.hip) into an
+    executable beside the library. cost_models.measure_peaks runs it."""
+    PROBE_PATH.parent.mkdir(parents=True, exist_ok=True)
+    tmp = PROBE_PATH.with_suffix(".tmp")
+    cmd = [hipcc(), *[f for f in HIPCC_FLAGS if f != "-fPIC"], str(PROBE_SRC), "-o", str(tmp)]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {PROBE_SRC.name}:\n{r.stderr[-4000:]}")
+    os.replace(tmp, PROBE_PATH)
+    if verbose:
+        print(f"built {PROBE_PATH}")
+    return PROBE_PATH
+
+
 if __name__ == "__main__":
     build(verbose=True)
+    build_probe(verbose=True)

@@ -91,7 +91,7 @@ class DeviceProgram:
                  fuse_rope: bool = True, fp32_outputs: bool = True, residual_fp32: bool = True,
                  merge_siblings: bool | None = False,
                  fold_sources: dict[str, tuple[torch.Tensor, torch.Tensor]] | None = None,
-                 reuse_buffers: bool = True, merge_convs: bool = True) -> None:
+                 reuse_buffers: bool = True, merge_convs: bool = True, hw=None) -> None:
         self.program = program
         # RMSNorm gains folded into weights by the front end, to be taken back
         # out (weight const -> (gain, unfolded weight)): such GEMMs read the
@@ -171,10 +171,24 @@ class DeviceProgram:
             if k.kind == "embedding" and k.arg("ids").tensor in program.inputs:
                 ids = k.arg("ids").tensor
                 self._vocab[ids] = min(self._vocab.get(ids, k.attrs["vocab"]), k.attrs["vocab"])
-        if merge_siblings is None:  # small row counts: launches, not tiles, set the time
-            merge_siblings = all(k.grid.get("rows", 0) <= 4096 for k in program.kernels if k.kind == "gemm")
-        self._merge_groups, self._merged_away = self._plan_sibling_merges(program) if merge_siblings else ({}, set())
-        self._fp8_groups = self._plan_fp8_merges(program, self._merged_away) if merge_siblings else {}
+        # Sibling GEMM kernels (one lhs) as one launch: True merges every group that can
+        # merge, False none; None (the default) takes the planner's priced decision per
+        # group (optimizer/planner.py price_launch_merges: separate launches against one
+        # launch of the concatenated width, on the calibrated cost model).
+        self.launch_merges: list = []
+        groups, away = self._plan_sibling_merges(program) if merge_siblings is not False else ({}, set())
+        if merge_siblings is None and groups:
+            from ..cost_models.hw_spec import HardwareSpec
+            from ..optimizer.planner import price_launch_merges
+
+            cand = [[(m[0].name, len(m[2])) for m in members] for members in groups.values()]
+            self.launch_merges = price_launch_merges(program, cand, hw or HardwareSpec.load())
+            keep = {lm.members[0] for lm in self.launch_merges if lm.merged}
+            groups = {k: v for k, v in groups.items() if k in keep}
+            away = {m[0].name for v in groups.values() for m in v[1:]}
+        self._merge_groups, self._merged_away = groups, away
+        # (e4m3 decode GEMMs: a few rows against weight streams, one launch always pays)
+        self._fp8_groups = self._plan_fp8_merges(program, self._merged_away) if merge_siblings is not False else {}
         for i, k in enumerate(program.kernels):
             self._cur = i
             if self.reuse:

@@ -25,7 +25,7 @@ from typing import Any
 
 from ..capture.opgraph import OpGraph
 from ..cost_models.hw_spec import HardwareSpec
-from ..cost_models.roofline import CostModelError, kernel_cost
+from ..cost_models.roofline import CostModelError, kernel_cost, merged_gemm_cost
 from .legality import check_program
 from .opir import Program
 from .partition import Grouping, PartitionError, build_program, sibling_sets
@@ -192,3 +192,54 @@ def plan(g: OpGraph, hw: HardwareSpec, config, name: str = "program") -> PlanRes
                                      "total_cycles": best.total_cycles, "kernel_us": best.kernel_cycles,
                                      "launch_overhead_us": hw.launch_overhead_us}
     return PlanResult(best, candidates)
+
+
+# ---------------------------------------------------------------- launch merges
+# After the partition, a backend may still run several GEMM kernels as one
+# launch: kernels that multiply the same lhs by different weights (projections
+# the partition kept apart because their widths or epilogue ops differ) become
+# one GEMM over the concatenated weights, each output on its own column window.
+# Which groups CAN merge is structural (the HIP runtime's _plan_sibling_merges);
+# whether they SHOULD is decided here with the cost model: the group's kernels
+# as separate launches (each with its launch overhead and its own wave and tile
+# quantisation) against one launch of the concatenated width.
+
+
+@dataclass
+class LaunchMerge:
+    members: list[str]
+    split_us: float
+    merged_us: float
+
+    @property
+    def merged(self) -> bool:
+        return self.merged_us < self.split_us
+
+    def to_dict(self) -> dict[str, Any]:
+        return {"members": self.members, "split_us": self.split_us, "merged_us": self.merged_us,
+                "merged": self.merged}
+
+
+def price_launch_merges(program: Program, groups: list[list[tuple[str, int]]], hw: HardwareSpec) -> list[LaunchMerge]:
+    """Each group (kernel name, accumulators it contributes) priced split and merged."""
+    kern = {k.name: k for k in program.kernels}
+    out = []
+    for g in groups:
+        specs = [kern[n] for n, _ in g]
+        split = sum(kernel_cost(sp, program.tensors, hw).us for sp in specs)
+        merged = merged_gemm_cost(specs, [u for _, u in g], program.tensors, hw).us
+        out.append(LaunchMerge([n for n, _ in g], split, merged))
+    return out
+
+
+def launch_merge_report(merges: list[LaunchMerge]) -> str:
+    lines = ["## Launch merges (HIP backend)", "",
+             "Sibling GEMM kernels reading one lhs, priced as separate launches and as one launch over",
+             "their concatenated weights (calibrated cost model, launch overhead included).", "",
+             "| kernels | split us | merged us | decision |", "|---|---:|---:|---|"]
+    for m in merges:
+        lines.append(f"| {' + '.join(m.members)} | {m.split_us:,.1f} | {m.merged_us:,.1f} | "
+                     f"{'merged' if m.merged else 'split'} |")
+    if not merges:
+        lines.append("| (none: no two GEMM kernels share an lhs) | | | |")
+    return "\n".join(lines)

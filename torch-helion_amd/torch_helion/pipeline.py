@@ -158,9 +158,16 @@ def compile_model(model: torch.nn.Module, example_args: Sequence[Any], config: C
                                            merge_siblings=config.merge_siblings,
                                            fold_sources=graph.fold_sources if config.norm_gain == "activation"
                                            else None, reuse_buffers=config.reuse_buffers,
-                                           merge_convs=config.merge_convs)
+                                           merge_convs=config.merge_convs, hw=hw)
             rw.write_json("kernels/launches.json", [{"kernel": l.kernel, "entry": l.entry, "info": l.info}
                                                     for l in device_program.launches])
+            if device_program.launch_merges:
+                from .optimizer.planner import launch_merge_report
+
+                program.metadata["launch_merges"] = [m.to_dict() for m in device_program.launch_merges]
+                rw.write_text("05_plan/plan.md", plan_report(result, hw, config) + "\n\n" +
+                              launch_merge_report(device_program.launch_merges) + "\n")
+                program.to_json(rw.path("06_opir.json"))
 
     reference_check: dict[str, Any] = {}
     do_ref = small if config.reference_check is None else config.reference_check
