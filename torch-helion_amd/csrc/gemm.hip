@@ -1360,8 +1360,8 @@ __global__ void __launch_bounds__(1024, 1) gemm_f32_sk_kernel(GemmK p) {
 // column-0 workgroups also store the slice's row sums of squares ssq[g][row].
 // Pass 2 (gemm_f32_ksr_kernel): one workgroup per 8 rows x BNC columns sums the
 // KSG partials in slice order (deterministic) into an LDS slab and runs the
-// slab epilogue. Enough workgroups to cover the GPU (about two per CU) for the
-// fp32 block's GEMMs of 128 rows, which one workgroup per tile cannot.
+// slab epilogue. Enough pass-1 workgroups to cover the GPU (about one per CU)
+// for the fp32 block's GEMMs of 128 rows, which one workgroup per tile cannot.
 struct F32Ksp {
   GemmK k;
   float* part;  // [KSG][Mp][Npk]
@@ -1471,11 +1471,13 @@ __global__ void __launch_bounds__(256) gemm_f32_ksr_kernel(F32Ksp q) {
   epilogue_slab(p, slab, SROW, RB, rs, r0, tn, tid);
 }
 
-// K slices of the split-K fp32 path for tiles 32-row x BNC tiles: about two
-// workgroups per CU, each slice at least two 8-wide steps
+// K slices of the split-K fp32 path for tiles 32-row x BNC tiles: about one
+// workgroup per CU, each slice at least two 8-wide steps. (Two per CU measured
+// 15% slower on the fp32 block: twice the partial sums to write and re-read,
+// each workgroup's K slice little more than its load pipeline's depth.)
 static int f32_ksp_slices(int64_t tiles, int64_t K) {
   const int64_t cus = device_cus() > 0 ? device_cus() : 256;
-  const int64_t want = cdiv(2 * cus, tiles);
+  const int64_t want = cdiv(cus, tiles);
   return (int)std::max((int64_t)1, std::min({want, cdiv(K, 16), (int64_t)64}));
 }
 

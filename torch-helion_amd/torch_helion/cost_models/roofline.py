@@ -157,10 +157,10 @@ def _gemm_compose(hw: HardwareSpec, T: int, N: int, K: int, n_acc: int, dtype: s
     tiles_m, tiles_n = math.ceil(T / bm), math.ceil(N / bn)
     kq = math.ceil(K / (16 if dtype == "float32" else 64)) * (16 if dtype == "float32" else 64)
     if dtype == "float32" and tiles_m * tiles_n < hw.compute_units:
-        # fp32 grids too small for the GPU: 32-row tiles, K split over about two
-        # workgroups per CU (th_gemm's workspace path), a second pass sums the slices
+        # fp32 grids too small for the GPU: 32-row tiles, K split over about one
+        # workgroup per CU (th_gemm's workspace path), a second pass sums the slices
         tiles_m = math.ceil(T / 32)
-        ksg = max(1, min(math.ceil(2 * hw.compute_units / (tiles_m * tiles_n)), math.ceil(K / 16), 64))
+        ksg = max(1, min(math.ceil(hw.compute_units / (tiles_m * tiles_n)), math.ceil(K / 16), 64))
         mfma = 2.0 * tiles_m * 32 * tiles_n * bn * n_acc * kq
         return _compose(hw, flops, nbytes, mfma, tiles_m * tiles_n * ksg, dtype,
                         {"tile_t": 32, "tile_n": bn, "k_slices": ksg}, detail, "gemm_fp32",
