@@ -41,6 +41,8 @@ sys.path.insert(0, str(REPO))
 
 METRIC = "µs per block fwd (Llama-8B block, Mamba-2 layer); % of MFMA/HBM roofline"
 RESULTS = REPO / "gpurun_out" / "results"   # compile_model results dirs (--results-dir)
+# sibling GEMM merges: None = the planner decides (priced), True / False = forced (--merge-siblings)
+MERGE = None
 
 
 def write_device_results(*a):
@@ -130,6 +132,7 @@ def bench_llama_c3(args) -> dict:
     # One block at the eager model's precision: bf16 activations, the residual
     # stream rounded to bf16 where it is stored, the block output in bf16.
     res = compile_model(model, x, CompileConfig(run_name="bench_llama_c3", results_dir=RESULTS, backend="hip",
+                                                merge_siblings=MERGE,
                                                 device_check=False, reference_check=False, verify_passes=False,
                                                 planner_mode="exhaustive", fp32_outputs=False, residual_fp32=False))
     log(f"compiled in {time.time() - t0:.1f} s: {len(res.program.kernels)} kernels")
@@ -186,6 +189,7 @@ def bench_llama_c1(args) -> dict:
     model = build_llama_block(cfg, seed=0)
     x = model.example_inputs(seed=0)
     res = compile_model(model, x, CompileConfig(run_name="bench_llama_c1", results_dir=RESULTS, backend="hip",
+                                                merge_siblings=MERGE,
                                                 device_check=False, reference_check=True, planner_mode="exhaustive"))
     b = bench_program(res.device_program, x, res.hw, warmup=args.warmup, reps=args.steps)
     write_device_results(res.run_dir, res.program, res.hw, b)
@@ -220,6 +224,7 @@ def bench_mamba_c2(args) -> dict:
     x = model.example_inputs(seed=0)
     # one layer at the eager model's precision: bf16 activations and residual, bf16 output
     res = compile_model(model, x, CompileConfig(run_name="bench_mamba_c2", results_dir=RESULTS, backend="hip",
+                                                merge_siblings=MERGE,
                                                 device_check=False, reference_check=False, verify_passes=False,
                                                 planner_mode="exhaustive", fp32_outputs=False, residual_fp32=False))
     b = bench_program(res.device_program, x, res.hw, warmup=args.warmup, reps=args.steps)
@@ -369,6 +374,7 @@ def bench_mamba_c4(args) -> dict:
     ids = model.example_inputs(seed=0)[0]
     t0 = time.time()
     res = compile_model(model, (ids,), CompileConfig(run_name="bench_mamba_c4", results_dir=RESULTS, backend="hip",
+                                                     merge_siblings=MERGE,
                                                      device_check=False, reference_check=False, verify_passes=False,
                                                      planner_mode="greedy", fp32_outputs=False, norm_gain="activation"))
     log(f"compiled in {time.time() - t0:.1f} s: {len(res.program.kernels)} kernels")
@@ -442,9 +448,12 @@ def main() -> int:
     ap.add_argument("--only", choices=["c1", "c2", "c3", "c4", "c5"], default=None,
                     help="run one secondary workload alone and print its object (for profiling runs)")
     ap.add_argument("--results-dir", type=Path, default=None, help="where compile_model writes results/<run>/")
+    ap.add_argument("--merge-siblings", choices=["auto", "on", "off"], default="auto",
+                    help="sibling GEMM launch merges: priced by the planner (auto) or forced, for calibration runs")
     args = ap.parse_args()
+    global RESULTS, MERGE
+    MERGE = {"auto": None, "on": True, "off": False}[args.merge_siblings]
     if args.results_dir is not None:
-        global RESULTS
         RESULTS = args.results_dir
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU; --gpus must be 1 (multi-GPU sharding is not built)"}))
