@@ -45,6 +45,11 @@ RESULTS = REPO / "gpurun_out" / "results"   # compile_model results dirs (--resu
 MERGE = None
 
 
+def _merge_tag() -> str:
+    """Run-name suffix of a forced merge setting (kept apart from the priced runs)."""
+    return "" if MERGE is None else ("_merged" if MERGE else "_split")
+
+
 def write_device_results(*a):
     from torch_helion.pipeline import write_device_results as w
 
@@ -131,7 +136,8 @@ def bench_llama_c3(args) -> dict:
     t0 = time.time()
     # One block at the eager model's precision: bf16 activations, the residual
     # stream rounded to bf16 where it is stored, the block output in bf16.
-    res = compile_model(model, x, CompileConfig(run_name="bench_llama_c3", results_dir=RESULTS, backend="hip",
+    res = compile_model(model, x, CompileConfig(run_name="bench_llama_c3" + _merge_tag(),
+                                                results_dir=RESULTS, backend="hip",
                                                 merge_siblings=MERGE,
                                                 device_check=False, reference_check=False, verify_passes=False,
                                                 planner_mode="exhaustive", fp32_outputs=False, residual_fp32=False))
@@ -188,7 +194,8 @@ def bench_llama_c1(args) -> dict:
     cfg = config_c1()
     model = build_llama_block(cfg, seed=0)
     x = model.example_inputs(seed=0)
-    res = compile_model(model, x, CompileConfig(run_name="bench_llama_c1", results_dir=RESULTS, backend="hip",
+    res = compile_model(model, x, CompileConfig(run_name="bench_llama_c1" + _merge_tag(),
+                                                results_dir=RESULTS, backend="hip",
                                                 merge_siblings=MERGE,
                                                 device_check=False, reference_check=True, planner_mode="exhaustive"))
     b = bench_program(res.device_program, x, res.hw, warmup=args.warmup, reps=args.steps)
@@ -223,7 +230,8 @@ def bench_mamba_c2(args) -> dict:
     model = build_mamba_block(cfg, seed=0)
     x = model.example_inputs(seed=0)
     # one layer at the eager model's precision: bf16 activations and residual, bf16 output
-    res = compile_model(model, x, CompileConfig(run_name="bench_mamba_c2", results_dir=RESULTS, backend="hip",
+    res = compile_model(model, x, CompileConfig(run_name="bench_mamba_c2" + _merge_tag(),
+                                                results_dir=RESULTS, backend="hip",
                                                 merge_siblings=MERGE,
                                                 device_check=False, reference_check=False, verify_passes=False,
                                                 planner_mode="exhaustive", fp32_outputs=False, residual_fp32=False))
@@ -373,7 +381,8 @@ def bench_mamba_c4(args) -> dict:
     model = build_mamba_model(cfg, seed=0)
     ids = model.example_inputs(seed=0)[0]
     t0 = time.time()
-    res = compile_model(model, (ids,), CompileConfig(run_name="bench_mamba_c4", results_dir=RESULTS, backend="hip",
+    res = compile_model(model, (ids,), CompileConfig(run_name="bench_mamba_c4" + _merge_tag(),
+                                                     results_dir=RESULTS, backend="hip",
                                                      merge_siblings=MERGE,
                                                      device_check=False, reference_check=False, verify_passes=False,
                                                      planner_mode="greedy", fp32_outputs=False, norm_gain="activation"))

@@ -88,14 +88,22 @@ def samples(run_dirs: list[Path], hw: HardwareSpec) -> list[dict[str, Any]]:
 def _merged_sample(name: str, m: dict[str, Any], specs: dict[str, Any], prog: Program,
                    unit: HardwareSpec) -> dict[str, Any] | None:
     """A merged sibling launch ("k0_gemm+k2_gemm"): one th_gemm over the concatenated
-    weights of several GEMM kernels, priced as roofline.merged_gemm_cost prices it."""
+    weights of several GEMM kernels, priced as roofline.merged_gemm_cost prices it; or a
+    grouped convolution ("k1_conv1d+k4_conv1d"): one th_conv1d_causal over the members'
+    channels, whose ideal time is the sum of theirs (HBM-bound, bytes add)."""
     from ..hip.epilogue import match_epilogue
     from .roofline import merged_gemm_cost
 
     names = name.split("+")
-    if len(names) < 2 or any(n not in specs for n in names) or m.get("entries") != ["th_gemm"]:
+    if len(names) < 2 or any(n not in specs for n in names):
         return None
     members = [specs[n] for n in names]
+    if all(sp.kind == "conv1d" for sp in members) and m.get("entries") == ["th_conv1d_causal"]:
+        costs = [kernel_cost(sp, prog.tensors, unit) for sp in members]
+        return {"kernel": name, "category": "conv1d", "ideal_us": sum(max(c.t_mfma_us, c.t_hbm_us) for c in costs),
+                "waves": 0.0, "measured_us": float(m["us"]), "bound": "hbm"}
+    if m.get("entries") != ["th_gemm"]:
+        return None
     if any(sp.kind != "gemm" or category(sp, prog.tensors) != "gemm_bf16" for sp in members):
         return None
     used = [len({o.a for o in match_epilogue(sp).outs}) for sp in members]
