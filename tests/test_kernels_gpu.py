@@ -772,6 +772,7 @@ def test_conv1d_causal(gpu, dtype, bs, s, c, k, col0):
 @pytest.mark.parametrize("dtype,ids_dtype,V,D,T", [
     (torch.bfloat16, torch.int64, 50280, 1024, 16384),  # C4 lookup, 16-byte vector path
     (torch.float32, torch.int32, 1000, 64, 333),
+    (torch.bfloat16, torch.int32, 500, 256, 37),         # a ragged last workgroup (1184 chunks of 16 bytes)
     (torch.bfloat16, torch.int64, 77, 100, 129),         # 200-byte rows: element-wise path
 ])
 def test_embedding_gather_exact(gpu, dtype, ids_dtype, V, D, T):
