@@ -172,9 +172,10 @@ class DeviceProgram:
                 ids = k.arg("ids").tensor
                 self._vocab[ids] = min(self._vocab.get(ids, k.attrs["vocab"]), k.attrs["vocab"])
         # Sibling GEMM kernels (one lhs) as one launch: True merges every group that can
-        # merge, False none; None (the default) takes the planner's priced decision per
-        # group (optimizer/planner.py price_launch_merges: separate launches against one
-        # launch of the concatenated width, on the calibrated cost model).
+        # merge, False (this constructor's default) none; None (CompileConfig's default)
+        # takes the planner's priced decision per group (optimizer/planner.py
+        # price_launch_merges: separate launches against one launch of the concatenated
+        # width, on the calibrated cost model of ``hw``, else the shipped hardware spec).
         self.launch_merges: list = []
         groups, away = self._plan_sibling_merges(program) if merge_siblings is not False else ({}, set())
         if merge_siblings is None and groups:
