@@ -279,12 +279,25 @@ typedef struct th_ssd_desc {
   int32_t gate_dtype, y_dtype;
   void* y; int64_t ld_y;              /* [B*S, H*P] */
   float* y32; int64_t ld_y32;         /* optional fp32 copy of y */
-  float* workspace;                   /* th_ssd_workspace_bytes(...) bytes */
+  float* workspace;                   /* th_ssd_workspace_bytes(...) bytes, or
+                                         th_ssd_gtile_workspace_bytes(...) (16-byte aligned) */
   int64_t workspace_bytes;
 } th_ssd_desc;
 
 int64_t th_ssd_workspace_bytes(int32_t batch, int32_t seq, int32_t heads, int32_t head_dim,
                                int32_t state_dim, int32_t chunk);
+
+/* The workspace th_ssd_chunked runs fastest with: th_ssd_workspace_bytes plus,
+ * for state_dim 128 with several heads per B/C group, the chunks' G^T = C_t B_s^T
+ * tiles of every group. When the workspace holds them (and the bf16 MFMA path
+ * runs), the state pass forms each chunk's tiles once per group, its work dealt
+ * over the group's heads, and the output pass reads them instead of every head
+ * forming them again; the results are the same bits either way. For other shapes
+ * the tiles save less than they cost to store and reload, and the size is
+ * th_ssd_workspace_bytes's. No counterpart in the reference (its ssd kind is one
+ * dense expression, optimizer/evaluate.py:123-138). -1 for invalid arguments. */
+int64_t th_ssd_gtile_workspace_bytes(int32_t batch, int32_t seq, int32_t heads, int32_t head_dim,
+                                     int32_t state_dim, int32_t chunk, int32_t ngroups);
 
 /* One OpIR ssd / ssd_chunked KernelSpec. */
 int th_ssd_chunked(const th_ssd_desc* desc, void* stream);

@@ -86,6 +86,17 @@ def test_pure_queries(lib):
     # rows = ceil(N / tile) * tile * n_acc, K padded to 8 bf16 elements
     assert lib.th_gemm_packed_bytes(1000, 100, 2, abi.TH_BF16) == 8 * 128 * 2 * 104 * 2
     assert lib.th_gemm_packed_bytes(10, 10, 9, abi.TH_BF16) == -1
+    # the scan's shared G^T tiles: 4 KiB each (32 x 32 fp32), nt (nt + 1) / 2 per chunk and
+    # group, nt = chunk / 32; only state_dim 128 with several heads per group takes them
+    base = lib.th_ssd_workspace_bytes(8, 2048, 32, 64, 128, 256)
+    assert base == (2 * 8 * 32 * 8 * 64 * 128 + 8 * 32 * 8) * 4
+    assert lib.th_ssd_gtile_workspace_bytes(8, 2048, 32, 64, 128, 256, 1) == base + 8 * 1 * 8 * 36 * 4096
+    assert lib.th_ssd_gtile_workspace_bytes(2, 300, 6, 64, 128, 128, 2) == (
+        lib.th_ssd_workspace_bytes(2, 300, 6, 64, 128, 128) + 2 * 2 * 3 * 10 * 4096)
+    assert lib.th_ssd_gtile_workspace_bytes(8, 2048, 32, 64, 128, 256, 32) == base      # one head per group
+    assert lib.th_ssd_gtile_workspace_bytes(2, 1024, 16, 64, 64, 64, 1) == lib.th_ssd_workspace_bytes(
+        2, 1024, 16, 64, 64, 64)                                                           # state_dim 64
+    assert lib.th_ssd_gtile_workspace_bytes(8, 2048, 32, 64, 128, 256, 5) == -1           # 32 heads, 5 groups
 
 
 def _gemm_desc(**over):

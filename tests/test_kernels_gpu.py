@@ -741,6 +741,49 @@ def test_ssd_reference_form_padded_cum(gpu, dtype):
         assert _maxabs(out, ref) < BF16_TOL
 
 
+@pytest.mark.parametrize("bs,s,h,p,n,g,chunk", [
+    (2, 2048, 8, 64, 128, 1, 256),     # C4's head shape and length (8 of its 32 heads), 2 p-tiles per unit
+    (1, 300, 4, 128, 128, 1, 256),     # 4 p-tiles, 2 per unit, ragged last chunk
+    (1, 200, 4, 64, 128, 2, 64),       # two groups of two heads, 64-row chunks (1 p-tile per unit), ragged
+    (2, 300, 6, 64, 128, 2, 128),      # three heads per group, 128-row chunks, ragged
+])
+def test_ssd_shared_g_tiles_bit_exact(gpu, bs, s, h, p, n, g, chunk):
+    """With room for the shared G^T tiles (th_ssd_gtile_workspace_bytes, state_dim 128) the
+    state kernels of a group form each chunk's C_t B_s^T once between them and the out kernel
+    loads it; the tiles come from the same MFMA chain on the same operands as the per-head
+    chain, so y and y32 equal the minimum-workspace call's bit for bit, and the tiles' region
+    is written."""
+    from oracle.mamba import ssd_chunked_program
+    from torch_helion.hip import ops
+
+    announce(f"ssd shared G tiles bs={bs} s={s} h={h} p={p} n={n} g={g} chunk={chunk}")
+    x, bm, cm, dt, A, D, gate = _ssd_case(bs, s, h, p, n, g, torch.bfloat16, seed=3 * s + h)
+    args = dict(x=x.to(gpu), b=bm.to(gpu), c=cm.to(gpu), dt=dt.to(gpu), batch=bs, seq=s, heads=h, head_dim=p,
+                state_dim=n, ngroups=g, chunk=chunk, A=A.to(gpu), D=D.to(gpu), gate=gate.to(gpu))
+    base = ops.ssd_workspace_bytes(bs, s, h, p, n, chunk)
+    big = ops.ssd_workspace_bytes(bs, s, h, p, n, chunk, g)
+    # tiles [batch][group][chunk][pair] of 32 x 32 floats, pairs (t-block, s-block <= t-block)
+    nt = chunk // 32
+    nc, npair = -(-s // chunk), nt * (nt + 1) // 2
+    assert big - base == bs * g * nc * npair * 1024 * 4
+    outs = []
+    for nbytes in (base, big):
+        ws = torch.full((nbytes // 4,), float("nan"), device=gpu)
+        out = torch.empty(bs * s, h * p, dtype=torch.bfloat16, device=gpu)
+        out32 = torch.empty(bs * s, h * p, device=gpu)
+        ops.ssd_chunked(out=out, out32=out32, workspace=ws, **args)
+        torch.cuda.synchronize()
+        outs.append((out, out32, ws))
+    # chunk 0 of the last (batch, group) is full: its last pair is written
+    last = base // 4 + (((bs - 1) * g + g - 1) * nc * npair + npair - 1) * 1024
+    assert torch.isfinite(outs[1][2][base // 4:base // 4 + 1024]).all(), "the first G^T tile was not written"
+    assert torch.isfinite(outs[1][2][last:last + 1024]).all(), "the last pair of a full chunk was not written"
+    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
+    a = {"batch": bs, "seq": s, "heads": h, "head_dim": p, "state_dim": n, "ngroups": g}
+    ref = ssd_chunked_program(cm.double(), bm.double(), x.double(), dt.double(), A.double(), D.double(), a)
+    assert _maxabs(outs[1][1], ref * gate.double()) < BF16_TOL
+
+
 @pytest.mark.parametrize("dtype,bs,s,c,k,col0", [
     (torch.float32, 2, 300, 1152, 4, 0),
     (torch.bfloat16, 2, 300, 1152, 4, 0),     # 16-byte vector path, ragged last token run

@@ -38,6 +38,8 @@ struct SsdK {
   float* states;  // [B][H][nc][P*N]
   float* tot;     // [B][H][nc]
   int vec_epi;    // bf16 y (and gate), no dskip, 16-byte aligned rows: vector epilogue
+  float* gtile;   // optional [B][G][nc][npair][64 lanes][16]: the chunks' G^T tiles (MFMA path)
+  int npair;      // tiles per chunk: (Q/32)(Q/32 + 1)/2
 };
 
 // Running sum of dA (or the given cum re-based) for chunk ``c`` into cl[0..Q),
@@ -368,12 +370,54 @@ __device__ __forceinline__ f32x16_t relayout(bf16x8_t a0, bf16x8_t a1, bf16x8_t 
   return d;
 }
 
+// G^T tiles of chunk c, group g: tile (tb, sb), sb <= tb, at pair index
+// tb (tb + 1) / 2 + sb, is G^T = B_s C_t^T over the chunk's 32-token blocks t
+// (tb) and s (sb), in the MFMA C layout (lane = t, register r = s row
+// 8 (r / 4) + 4 (lane / 32) + r % 4), 16 floats per lane. The same loads (C
+// rows past the chunk zero, B rows clamped to its last row) and the same MFMA
+// chain as the output kernel's own, so either route gives the same bits. With
+// one B/C group per several heads every head of a chunk shares the tiles; the
+// pairs are dealt round robin over (head within the group, wave), so the
+// workgroups of a group share the work.
+template <int KS>  // state_dim / 16
+__device__ void ssd_g_tiles(const SsdK& p, int b, int g, int hg, int c, int rows) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, gl = lane >> 5, r32 = lane & 31;
+  const int64_t tok0 = (int64_t)b * p.S + (int64_t)c * p.Q;
+  const int64_t ccol = (int64_t)g * p.N + 8 * gl;
+  const char* bbase = (const char*)p.b + (tok0 * p.ldb + (int64_t)g * p.N) * 2;
+  const uint32_t ldb2 = (uint32_t)p.ldb * 2, ccol2 = 16 * gl;
+  float* gtb = p.gtile + (((int64_t)b * p.G + g) * p.nc + c) * (int64_t)p.npair * 1024;
+  const int ntb = (rows + 31) >> 5;
+  for (int pi = hg * 4 + wave; pi < ntb * (ntb + 1) / 2; pi += 4 * p.hpg) {
+    int tb = 0;
+    while ((tb + 1) * (tb + 2) / 2 <= pi) ++tb;
+    const int sb = pi - tb * (tb + 1) / 2, t = tb * 32 + r32;
+    bf16x8_t cf[KS], bfr[KS];
+    const uint32_t sr = (uint32_t)min(sb * 32 + r32, rows - 1);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      cf[ks] = ldg_bf16x8(p.c, (tok0 + t) * p.ldc + ccol + ks * 16, t < rows);
+      bfr[ks] = *(const bf16x8_t*)(bbase + (sr * ldb2 + ccol2) + 32 * ks);
+    }
+    f32x16_t gt;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) gt[r] = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) gt = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[ks], cf[ks], gt, 0, 0, 0);
+    float4* dst = (float4*)(gtb + (int64_t)pi * 1024 + lane * 16);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) dst[q] = make_float4(gt[4 * q], gt[4 * q + 1], gt[4 * q + 2], gt[4 * q + 3]);
+  }
+}
+
 // S_c[p][n] = sum_l (w_l x_l[p]) B_l[n],  w_l = dt_l exp(cl_last - cl_l)  (exponent <= 0).
 // One workgroup per (chunk, head, batch), no LDS staging: wave w owns p-tile
 // w % PT and n-tiles w / PT + j * (4 / PT), j < NTW, and walks the chunk in
 // 32-token blocks, each x / B block moved into operand order by relayout().
+// Occupancy floors: four waves per SIMD for NTW 1 (at most 128 VGPRs), three
+// for NTW 2 (168), which the G^T tile epilogue would otherwise push to two.
 template <int NTW>
-__global__ void __launch_bounds__(256) ssd_state2_kernel(SsdK p) {
+__global__ void __launch_bounds__(256, NTW == 1 ? 4 : NTW == 2 ? 3 : 1) ssd_state2_kernel(SsdK p) {
   __shared__ float cl[256], dts[256], tmp[512], wl[256];
   const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z, tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -457,6 +501,8 @@ __global__ void __launch_bounds__(256) ssd_state2_kernel(SsdK p) {
     for (int r = 0; r < 16; ++r) st[(int64_t)(pt * 32 + crow_of(r, lane)) * p.N + nt * 32 + r32] = acc[j][r];
   }
   if (tid == 0) p.tot[((int64_t)b * p.H + h) * p.nc + c] = last;
+  // this workgroup's share of the chunk's G^T tiles (set for state_dim 128 only)
+  if (p.gtile != nullptr) ssd_g_tiles<8>(p, b, g, h - g * p.hpg, c, rows);
 }
 
 // H_0 = 0, H_{c+1} = exp(tot_c) H_c + S_c, written for c >= 1 as the hi/lo bf16
@@ -527,7 +573,7 @@ __global__ void __launch_bounds__(256) ssd_carry2_kernel(SsdK p, uint4* hf) {
 // start, instead of being re-read from L2 by each unit.
 constexpr int kEpiStride = 36;  // floats per row of the per-wave 16 x 32 output tile
 
-template <int KS, int NPT>  // KS = state_dim / 16, NPT = p-tiles per unit
+template <int KS, int NPT, bool GT>  // KS = state_dim / 16, NPT = p-tiles per unit, GT: G^T tiles given
 __global__ void __launch_bounds__(256, 2) ssd_out2_kernel(SsdK p, const uint4* hf) {
   extern __shared__ float sm[];
   float* cl = sm;          // running sum of dA, in log2 units after set-up
@@ -716,23 +762,52 @@ __global__ void __launch_bounds__(256, 2) ssd_out2_kernel(SsdK p, const uint4* h
     // refills are unconditional (the last two re-read clamped rows) so that
     // every chain waits only for its own loads; a scheduling barrier keeps the
     // compiler from sinking them to their uses.
-    bf16x8_t b0[KS], b1[KS];
     f32x16_t g0, g1;
-    load_b(b0, 0);
-    if (tb > 0) load_b(b1, 1);
-    g0 = chain(b0);
-    int sb = 0;
-    while (sb < tb) {
-      load_b(b0, sb + 2);
-      __builtin_amdgcn_sched_barrier(0);
-      g1 = chain(b1);  // s-block sb + 1
-      offdiag(g0, sb);
-      if (++sb == tb) break;
-      load_b(b1, sb + 2);
-      __builtin_amdgcn_sched_barrier(0);
+    if constexpr (GT) {
+      // The chunk's G^T tiles were formed once per group by the state kernel:
+      // each is loaded two s-blocks ahead of the weighting and product that
+      // consume it (past the diagonal, the diagonal tile again).
+      const float* gtb = p.gtile + (((int64_t)b * p.G + g) * p.nc + c) * (int64_t)p.npair * 1024 +
+                         (int64_t)(tb * (tb + 1) / 2) * 1024 + lane * 16;
+      auto load_g = [&](int sb) {
+        const float4* q = (const float4*)(gtb + (int64_t)min(sb, tb) * 1024);
+        f32x16_t v;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const float4 f = q[k];
+          v[4 * k] = f.x; v[4 * k + 1] = f.y; v[4 * k + 2] = f.z; v[4 * k + 3] = f.w;
+        }
+        return v;
+      };
+      g0 = load_g(0);
+      g1 = load_g(1);
+      int sb = 0;
+      while (sb < tb) {
+        offdiag(g0, sb);
+        g0 = load_g(sb + 2);
+        if (++sb == tb) break;
+        offdiag(g1, sb);
+        g1 = load_g(sb + 2);
+        ++sb;
+      }
+    } else {
+      bf16x8_t b0[KS], b1[KS];
+      load_b(b0, 0);
+      if (tb > 0) load_b(b1, 1);
       g0 = chain(b0);
-      offdiag(g1, sb);
-      ++sb;
+      int sb = 0;
+      while (sb < tb) {
+        load_b(b0, sb + 2);
+        __builtin_amdgcn_sched_barrier(0);
+        g1 = chain(b1);  // s-block sb + 1
+        offdiag(g0, sb);
+        if (++sb == tb) break;
+        load_b(b1, sb + 2);
+        __builtin_amdgcn_sched_barrier(0);
+        g0 = chain(b0);
+        offdiag(g1, sb);
+        ++sb;
+      }
     }
     // rows t of acc: the factor exp2(cl_t - cl_t0) of the state and earlier terms
 #pragma unroll
@@ -955,10 +1030,11 @@ constexpr size_t kMaxLds = 163840;  // 160 KiB per workgroup on gfx950
 // Raise the dynamic-LDS limit of the scan kernels once per device (th_init),
 // so that launching them needs no attribute call (and can be graph-captured).
 int ssd_init_device() {
-  const void* fns[] = {(const void*)ssd_state_kernel,          (const void*)ssd_out_kernel,
-                       (const void*)ssd_out2_kernel<2, 1>,      (const void*)ssd_out2_kernel<4, 1>,
-                       (const void*)ssd_out2_kernel<8, 1>,      (const void*)ssd_out2_kernel<2, 2>,
-                       (const void*)ssd_out2_kernel<4, 2>,      (const void*)ssd_out2_kernel<8, 2>};
+  const void* fns[] = {(const void*)ssd_state_kernel,             (const void*)ssd_out_kernel,
+                       (const void*)ssd_out2_kernel<2, 1, false>, (const void*)ssd_out2_kernel<4, 1, false>,
+                       (const void*)ssd_out2_kernel<8, 1, false>, (const void*)ssd_out2_kernel<2, 2, false>,
+                       (const void*)ssd_out2_kernel<4, 2, false>, (const void*)ssd_out2_kernel<8, 2, false>,
+                       (const void*)ssd_out2_kernel<8, 1, true>,  (const void*)ssd_out2_kernel<8, 2, true>};
   for (const void* f : fns) TH_CHECK_HIP(hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxLds));
   return TH_OK;
 }
@@ -971,12 +1047,34 @@ using namespace th;
 // (padded to 4 floats), then the carried states as MFMA fragments (4 bytes
 // per element, the MFMA path only).
 static int64_t ssd_tot_floats(int64_t bhc) { return (bhc + 3) / 4 * 4; }
+// G^T tiles: [B][G][nc][npair] tiles of 32 x 32 fp32
+static int64_t ssd_gtile_bytes(int64_t batch, int64_t groups, int64_t nc, int64_t npair) {
+  return batch * groups * nc * npair * 1024 * 4;
+}
 
 extern "C" int64_t th_ssd_workspace_bytes(int32_t batch, int32_t seq, int32_t heads, int32_t head_dim,
                                           int32_t state_dim, int32_t chunk) {
   if (batch <= 0 || seq <= 0 || heads <= 0 || head_dim <= 0 || state_dim <= 0 || chunk <= 0) return -1;
   const int64_t bhc = (int64_t)batch * heads * cdiv(seq, chunk);
   return (2 * bhc * head_dim * state_dim + ssd_tot_floats(bhc)) * 4;
+}
+
+// The shared G^T tiles pay for state_dim 128 (8 MFMAs saved per tile, 4 KiB
+// reloaded in place of 8 KiB of B rows) with several heads per group. Measured
+// on MI355X: N = 128, 256-row chunks, 32 heads per group, 8 x 2048 tokens, 14%
+// faster; N = 64, 64-row chunks, 16 heads per group, 2 x 1024 tokens, 4% slower
+// (there a tile costs as many bytes as the B rows it replaces).
+static bool ssd_gtile_pays(int state_dim, int heads_per_group) { return state_dim == 128 && heads_per_group > 1; }
+
+extern "C" int64_t th_ssd_gtile_workspace_bytes(int32_t batch, int32_t seq, int32_t heads, int32_t head_dim,
+                                                int32_t state_dim, int32_t chunk, int32_t ngroups) {
+  const int64_t base = th_ssd_workspace_bytes(batch, seq, heads, head_dim, state_dim, chunk);
+  if (base < 0) return -1;
+  const int g = ngroups > 0 ? ngroups : heads;
+  if (heads % g != 0) return -1;
+  if (!ssd_gtile_pays(state_dim, heads / g)) return base;
+  const int64_t nt = cdiv(std::min(chunk, 256), 32);
+  return base + ssd_gtile_bytes(batch, g, cdiv(seq, chunk), nt * (nt + 1) / 2);
 }
 
 extern "C" int th_ssd_chunked(const th_ssd_desc* d, void* stream) {
@@ -1021,6 +1119,8 @@ extern "C" int th_ssd_chunked(const th_ssd_desc* d, void* stream) {
   }
   k.states = d->workspace;
   k.tot = d->workspace + (int64_t)k.B * k.H * k.nc * k.P * k.N;
+  k.gtile = nullptr;
+  k.npair = (k.Q / 32) * (k.Q / 32 + 1) / 2;
   hipStream_t s = (hipStream_t)stream;
   // MFMA path: bf16 operands, 32-wide p / n tiles, 16-byte aligned rows.
   auto al16 = [](const void* q) { return ((uintptr_t)q & 15) == 0; };
@@ -1031,6 +1131,10 @@ extern "C" int th_ssd_chunked(const th_ssd_desc* d, void* stream) {
   if (mfma) {
     const int64_t bhc = (int64_t)k.B * k.H * k.nc;
     uint4* hf = (uint4*)(d->workspace + bhc * k.P * k.N + ssd_tot_floats(bhc));
+    // Several heads per B/C group and room for the tiles after the base workspace
+    // (th_ssd_gtile_workspace_bytes): C_t B_s^T of a chunk is formed once per group.
+    if (ssd_gtile_pays(k.N, k.hpg) && d->workspace_bytes >= need + ssd_gtile_bytes(k.B, g, k.nc, k.npair))
+      k.gtile = (float*)((char*)d->workspace + need);
     const int PT = k.P / 32, NT = k.N / 32;
     const int ntw = (NT * PT + 3) / 4;
     const dim3 grid(k.nc, k.H, k.B);
@@ -1046,7 +1150,16 @@ extern "C" int th_ssd_chunked(const th_ssd_desc* d, void* stream) {
     // a full 8-block chunk gives every wave two t-blocks: share each G^T tile over
     // two p-tiles (more accumulators would not fit two waves per SIMD)
     const int npt = k.Q / 32 >= 8 ? std::min(PT, 2) : 1;
-#define TH_SSD_OUT2(KS_, NPT_) hipLaunchKernelGGL((ssd_out2_kernel<KS_, NPT_>), grid, dim3(256), l3, s, k, (const uint4*)hf)
+#define TH_SSD_OUT2(KS_, NPT_)                                                                       \
+  do {                                                                                               \
+    if constexpr (KS_ == 8) {                                                                        \
+      if (k.gtile) {                                                                                 \
+        hipLaunchKernelGGL((ssd_out2_kernel<KS_, NPT_, true>), grid, dim3(256), l3, s, k, (const uint4*)hf); \
+        break;                                                                                       \
+      }                                                                                              \
+    }                                                                                                \
+    hipLaunchKernelGGL((ssd_out2_kernel<KS_, NPT_, false>), grid, dim3(256), l3, s, k, (const uint4*)hf);  \
+  } while (0)
 #define TH_SSD_OUT2_KS(NPT_)                \
   do {                                      \
     if (k.N == 32) TH_SSD_OUT2(2, NPT_);    \

@@ -162,6 +162,7 @@ SIGNATURES: dict[str, tuple] = {
     "th_attention_decode": (_i32, [C.POINTER(DecodeDesc), _p]),
     "th_epilogue_vm": (_i32, [C.POINTER(VmDesc), _p]),
     "th_ssd_workspace_bytes": (_i64, [_i32, _i32, _i32, _i32, _i32, _i32]),
+    "th_ssd_gtile_workspace_bytes": (_i64, [_i32, _i32, _i32, _i32, _i32, _i32, _i32]),
     "th_ssd_chunked": (_i32, [C.POINTER(SsdDesc), _p]),
     "th_conv1d_causal": (_i32, [C.POINTER(ConvDesc), _p]),
     "th_embedding": (_i32, [C.POINTER(EmbeddingDesc), _p]),

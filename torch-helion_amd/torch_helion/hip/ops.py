@@ -274,8 +274,13 @@ def epilogue_vm(M: int, N: int, operands: list[tuple[torch.Tensor, bool]], ops: 
 
 
 # ------------------------------------------------------------------- SSD
-def ssd_workspace_bytes(batch: int, seq: int, heads: int, head_dim: int, state_dim: int, chunk: int) -> int:
-    return int(abi.load().th_ssd_workspace_bytes(batch, seq, heads, head_dim, state_dim, chunk))
+def ssd_workspace_bytes(batch: int, seq: int, heads: int, head_dim: int, state_dim: int, chunk: int,
+                        ngroups: int | None = None) -> int:
+    """Workspace of th_ssd_chunked: the minimum, or with ``ngroups`` the size that also holds
+    the chunks' shared G^T tiles (formed once per B/C group instead of once per head)."""
+    if ngroups is None:
+        return int(abi.load().th_ssd_workspace_bytes(batch, seq, heads, head_dim, state_dim, chunk))
+    return int(abi.load().th_ssd_gtile_workspace_bytes(batch, seq, heads, head_dim, state_dim, chunk, ngroups))
 
 
 def ssd_chunked(*, x, b, c, dt, out, workspace, batch, seq, heads, head_dim, state_dim, ngroups, chunk, A=None, D=None,

@@ -67,7 +67,8 @@ def lower_ssd(dp, spec: KernelSpec):
         kw.update(ngroups=h, chunk=64 if s % 64 == 0 or s > 64 else s, dt_stride=int(a["pad"]), cum=buf("cum"),
                   dskip=buf("dskip"))
     gate_arg, fused = _gate_of(spec)
-    ws = dp._workspace((ops.ssd_workspace_bytes(bs, s, h, p, n, kw["chunk"]) + 3) // 4)
+    # (with room for the chunks' G^T tiles: shared by the heads of a B/C group)
+    ws = dp._workspace((ops.ssd_workspace_bytes(bs, s, h, p, n, kw["chunk"], kw["ngroups"]) + 3) // 4)
     out_name = spec.outputs[0].tensor if spec.outputs else None
     if fused:
         out = dp.buffers[out_name]
