@@ -331,7 +331,12 @@ __device__ __forceinline__ void unpk8(const uint4& w, float* f) {
   }
 }
 
+// lo = bf16(v - hi) from the rounded v: the subtraction is kept out of FMA
+// contraction, which the compiler would otherwise decide per kernel instance
+// (fusing it with the product that formed v), so every kernel and route that
+// splits the same values gets the same bits.
 __device__ __forceinline__ void pk8_split(const float* v, bf16x8_t& hi, bf16x8_t& lo) {
+#pragma clang fp contract(off)
   const uint4 h = make_uint4(pk_bf16(v[0], v[1]), pk_bf16(v[2], v[3]), pk_bf16(v[4], v[5]), pk_bf16(v[6], v[7]));
   float f[8], r[8];
   unpk8(h, f);
@@ -411,51 +416,83 @@ __device__ void ssd_g_tiles(const SsdK& p, int b, int g, int hg, int c, int rows
 }
 
 // S_c[p][n] = sum_l (w_l x_l[p]) B_l[n],  w_l = dt_l exp(cl_last - cl_l)  (exponent <= 0).
-// One workgroup per (chunk, head, batch), no LDS staging: wave w owns p-tile
-// w % PT and n-tiles w / PT + j * (4 / PT), j < NTW, and walks the chunk in
-// 32-token blocks, each x / B block moved into operand order by relayout().
-// Occupancy floors: four waves per SIMD for NTW 1 (at most 128 VGPRs), three
-// for NTW 2 (168), which the G^T tile epilogue would otherwise push to two.
-template <int NTW>
-__global__ void __launch_bounds__(256, NTW == 1 ? 4 : NTW == 2 ? 3 : 1) ssd_state2_kernel(SsdK p) {
-  __shared__ float cl[256], dts[256], tmp[512], wl[256];
+// One workgroup per (chunk, head, batch): wave w owns p-tile w % PT and
+// n-tiles w / PT + j * (4 / PT), j < NTW, and walks the chunk in 32-token
+// blocks, each x / B block moved into operand order by relayout().
+// The blocks come through a ring of kStateRing LDS stages filled by
+// direct-to-LDS loads (no registers held for loads in flight; each byte read
+// once per workgroup, where two waves share every x and B fragment): stage =
+// x block (32 x P bf16) then B block (32 x N), as 16-byte chunks in load
+// order, load i covering columns 16 i .. 16 i + 15 of one of them, lane l at
+// row l % 32, columns 16 i + 8 (l / 32) .. + 7, so each operand fragment is
+// one lane-contiguous 16-byte LDS read. The first stages are issued before
+// the running sum. Rows past the chunk's end re-read its last row (their
+// weight w_l is zero). NL = loads per wave per stage, (P + N) / 64 rounded
+// up; a wave with fewer repeats its last (the same bytes to the same place).
+// Occupancy floor: four waves per SIMD (at most 128 VGPRs) for NTW 1 and 2;
+// with P = 64, N = 128 four workgroups then fit the LDS (4 x 39 KiB).
+constexpr int kStateRing = 3;
+template <int NTW, int NL>
+__global__ void __launch_bounds__(256, NTW <= 2 ? 4 : 1) ssd_state2_kernel(SsdK p) {
+  __shared__ float cl[256], dts[256], tmp[4], wl[256];
+  extern __shared__ __align__(16) char ring[];
   const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z, tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = h / p.hpg, gl = lane >> 5, r32 = lane & 31;
-  chunk_running_sum(p, b, h, c, cl, dts, tmp);
   const int Q = p.Q, t0 = c * Q, rows = min(Q, p.S - t0);
+  const int nsb = (rows + 31) >> 5;
+  const int64_t tok0 = (int64_t)b * p.S + t0;
+  const int XI = p.P >> 4, NI = XI + (p.N >> 4);  // loads per stage: x, then x + B
+  const uint32_t SB = (uint32_t)NI * 1024;         // stage bytes
+  const char* xbase = (const char*)p.x + (tok0 * p.ldx + (int64_t)h * p.P) * 2;
+  const char* bbase = (const char*)p.b + (tok0 * p.ldb + (int64_t)g * p.N) * 2;
+  const uint32_t lds0 = (uint32_t)(uintptr_t)ring;
+  // this wave's loads: index n, and its 16-byte column offset within x or B
+  int ln[NL];
+  uint32_t lcol[NL];
+#pragma unroll
+  for (int i = 0; i < NL; ++i) {
+    ln[i] = min(wave + 4 * i, NI - 1);
+    const int ci = ln[i] < XI ? ln[i] : ln[i] - XI;
+    lcol[i] = (uint32_t)(32 * ci + 16 * gl);
+  }
+  auto issue = [&](int sb) {
+    const uint32_t r = (uint32_t)min(sb * 32 + r32, rows - 1);
+    const uint32_t xo = r * (uint32_t)p.ldx * 2u, bo = r * (uint32_t)p.ldb * 2u;
+    const uint32_t st = lds0 + (uint32_t)(sb % kStateRing) * SB;
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+      if (ln[i] < XI) dma_load16(xbase, xo + lcol[i], st + (uint32_t)ln[i] * 1024);
+      else dma_load16(bbase, bo + lcol[i], st + (uint32_t)ln[i] * 1024);
+    }
+  };
+#pragma unroll
+  for (int sb = 0; sb < kStateRing - 1; ++sb)
+    if (sb < nsb) issue(sb);
+  chunk_running_sum(p, b, h, c, cl, dts, tmp);
   const float last = cl[Q - 1];
   if (tid < Q) wl[tid] = dts[tid] * __expf(last - cl[tid]);
   __syncthreads();
   const int PT = p.P >> 5, NT = p.N >> 5, WPP = 4 / PT;
   const int pt = wave % PT, nt0 = wave / PT;
-  const int64_t tok0 = (int64_t)b * p.S + t0;
-  const int64_t xcol = (int64_t)h * p.P + pt * 32 + 8 * gl, bcol = (int64_t)g * p.N + 8 * gl;
   const bf16x8_t e0 = eye_frag(lane, 0), e1 = eye_frag(lane, 1);
   f32x16_t acc[NTW];
 #pragma unroll
   for (int j = 0; j < NTW; ++j)
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[j][r] = 0.f;
-  const int nsb = (rows + 31) >> 5;
-  struct Blk {
-    bf16x8_t xa0, xa1, ba[NTW][2];
-  };
-  auto load_blk = [&](Blk& k2, int sb) {
-    const int l = sb * 32 + r32;
-    const bool ok = sb < nsb && l < rows;
-    const int64_t tok = tok0 + l;
-    k2.xa0 = ldg_bf16x8(p.x, tok * p.ldx + xcol, ok);
-    k2.xa1 = ldg_bf16x8(p.x, tok * p.ldx + xcol + 16, ok);
-#pragma unroll
-    for (int j = 0; j < NTW; ++j) {
-      const int nt = nt0 + j * WPP;
-      k2.ba[j][0] = ldg_bf16x8(p.b, tok * p.ldb + bcol + nt * 32, ok && nt < NT);
-      k2.ba[j][1] = ldg_bf16x8(p.b, tok * p.ldb + bcol + nt * 32 + 16, ok && nt < NT);
-    }
-  };
-  auto compute_blk = [&](const Blk& k2, int sb) {
-    const f32x16_t xr = relayout(k2.xa0, k2.xa1, e0, e1);
+  for (int sb = 0; sb < nsb; ++sb) {
+    // this wave's loads of block sb have landed (those of sb + 1 may not
+    // have); after the barrier every wave's have, and every wave is done
+    // reading block sb - 1, whose stage block sb + 2 refills
+    if (sb + 1 < nsb) wait_vmcnt<NL>();
+    else wait_vmcnt<0>();
+    barrier_keep_loads();
+    if (sb + kStateRing - 1 < nsb) issue(sb + kStateRing - 1);
+    const char* st = ring + (sb % kStateRing) * SB + lane * 16;
+    const bf16x8_t xa0 = *(const bf16x8_t*)(st + (2 * pt) * 1024);
+    const bf16x8_t xa1 = *(const bf16x8_t*)(st + (2 * pt + 1) * 1024);
+    const f32x16_t xr = relayout(xa0, xa1, e0, e1);
     float v[16];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -470,8 +507,11 @@ __global__ void __launch_bounds__(256, NTW == 1 ? 4 : NTW == 2 ? 3 : 1) ssd_stat
     pk8_split(v + 8, xh1, xl1);
 #pragma unroll
     for (int j = 0; j < NTW; ++j) {
-      if (nt0 + j * WPP >= NT) continue;
-      const f32x16_t br = relayout(k2.ba[j][0], k2.ba[j][1], e0, e1);
+      const int nt = nt0 + j * WPP;
+      if (nt >= NT) continue;
+      const bf16x8_t ba0 = *(const bf16x8_t*)(st + (XI + 2 * nt) * 1024);
+      const bf16x8_t ba1 = *(const bf16x8_t*)(st + (XI + 2 * nt + 1) * 1024);
+      const f32x16_t br = relayout(ba0, ba1, e0, e1);
       float bv[16];
 #pragma unroll
       for (int r = 0; r < 16; ++r) bv[r] = br[r];
@@ -481,24 +521,14 @@ __global__ void __launch_bounds__(256, NTW == 1 ? 4 : NTW == 2 ? 3 : 1) ssd_stat
       acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xh1, bb1, acc[j], 0, 0, 0);
       acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xl1, bb1, acc[j], 0, 0, 0);
     }
-  };
-  // two buffers: the next token block's loads are in flight while this one computes
-  Blk k0, k1;
-  load_blk(k0, 0);
-  for (int sb = 0; sb < nsb; sb += 2) {
-    load_blk(k1, sb + 1);
-    compute_blk(k0, sb);
-    if (sb + 1 >= nsb) break;
-    load_blk(k0, sb + 2);
-    compute_blk(k1, sb + 1);
   }
-  float* st = p.states + (((int64_t)b * p.H + h) * p.nc + c) * (int64_t)(p.P * p.N);
+  float* sto = p.states + (((int64_t)b * p.H + h) * p.nc + c) * (int64_t)(p.P * p.N);
 #pragma unroll
   for (int j = 0; j < NTW; ++j) {
     const int nt = nt0 + j * WPP;
     if (nt >= NT) continue;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) st[(int64_t)(pt * 32 + crow_of(r, lane)) * p.N + nt * 32 + r32] = acc[j][r];
+    for (int r = 0; r < 16; ++r) sto[(int64_t)(pt * 32 + crow_of(r, lane)) * p.N + nt * 32 + r32] = acc[j][r];
   }
   if (tid == 0) p.tot[((int64_t)b * p.H + h) * p.nc + c] = last;
   // this workgroup's share of the chunk's G^T tiles (set for state_dim 128 only)
@@ -1126,7 +1156,8 @@ extern "C" int th_ssd_chunked(const th_ssd_desc* d, void* stream) {
   auto al16 = [](const void* q) { return ((uintptr_t)q & 15) == 0; };
   const bool mfma = d->dtype == TH_BF16 && (k.P == 32 || k.P == 64 || k.P == 128) &&
                     (k.N == 32 || k.N == 64 || k.N == 128) && k.Q % 32 == 0 && d->ld_x % 8 == 0 &&
-                    d->ld_b % 8 == 0 && d->ld_c % 8 == 0 && d->ld_b < (1 << 22) && al16(d->x) && al16(d->b) && al16(d->c) &&
+                    d->ld_b % 8 == 0 && d->ld_c % 8 == 0 && d->ld_b < (1 << 22) && d->ld_x < (1 << 22) && al16(d->x) &&
+                    al16(d->b) && al16(d->c) &&
                     out2_lds(k.Q, k.P, k.N) <= kMaxLds;
   if (mfma) {
     const int64_t bhc = (int64_t)k.B * k.H * k.nc;
@@ -1138,9 +1169,15 @@ extern "C" int th_ssd_chunked(const th_ssd_desc* d, void* stream) {
     const int PT = k.P / 32, NT = k.N / 32;
     const int ntw = (NT * PT + 3) / 4;
     const dim3 grid(k.nc, k.H, k.B);
-    if (ntw == 1) hipLaunchKernelGGL(ssd_state2_kernel<1>, grid, dim3(256), 0, s, k);
-    else if (ntw == 2) hipLaunchKernelGGL(ssd_state2_kernel<2>, grid, dim3(256), 0, s, k);
-    else hipLaunchKernelGGL(ssd_state2_kernel<4>, grid, dim3(256), 0, s, k);
+    // the state kernel's ring: kStateRing stages of 32 x (P + N) bf16; loads
+    // per wave per stage (P + N) / 64 rounded up
+    const size_t lring = (size_t)kStateRing * 32 * (k.P + k.N) * 2;
+    const int nl = (k.P + k.N + 63) / 64;
+    if (ntw == 1 && nl == 1) hipLaunchKernelGGL((ssd_state2_kernel<1, 1>), grid, dim3(256), lring, s, k);
+    else if (ntw == 1 && nl == 2) hipLaunchKernelGGL((ssd_state2_kernel<1, 2>), grid, dim3(256), lring, s, k);
+    else if (ntw == 1) hipLaunchKernelGGL((ssd_state2_kernel<1, 3>), grid, dim3(256), lring, s, k);
+    else if (ntw == 2) hipLaunchKernelGGL((ssd_state2_kernel<2, 3>), grid, dim3(256), lring, s, k);
+    else hipLaunchKernelGGL((ssd_state2_kernel<4, 4>), grid, dim3(256), lring, s, k);
     TH_CHECK_LAUNCH();
     if (k.nc > 1) {
       hipLaunchKernelGGL(ssd_carry2_kernel, dim3((unsigned)cdiv(k.P * k.N / 8, 256), k.H, k.B), dim3(256), 0, s, k, hf);
