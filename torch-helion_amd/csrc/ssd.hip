@@ -603,6 +603,19 @@ __global__ void __launch_bounds__(256) ssd_carry2_kernel(SsdK p, uint4* hf) {
 // start, instead of being re-read from L2 by each unit.
 constexpr int kEpiStride = 36;  // floats per row of the per-wave 16 x 32 output tile
 
+// G^T tile min(sb, tb) of a t-block's run of tiles (gtb: its first tile plus
+// this lane's 16 floats), as the MFMA C-layout registers
+__device__ __forceinline__ f32x16_t ssd_load_gtile(const float* gtb, int sb, int tb) {
+  const float4* q = (const float4*)(gtb + (int64_t)min(sb, tb) * 1024);
+  f32x16_t v;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const float4 f = q[k];
+    v[4 * k] = f.x; v[4 * k + 1] = f.y; v[4 * k + 2] = f.z; v[4 * k + 3] = f.w;
+  }
+  return v;
+}
+
 template <int KS, int NPT, bool GT>  // KS = state_dim / 16, NPT = p-tiles per unit, GT: G^T tiles given
 __global__ void __launch_bounds__(256, 2) ssd_out2_kernel(SsdK p, const uint4* hf) {
   extern __shared__ float sm[];
@@ -677,6 +690,20 @@ __global__ void __launch_bounds__(256, 2) ssd_out2_kernel(SsdK p, const uint4* h
   const uint32_t ldb2 = (uint32_t)p.ldb * 2, ccol2 = 16 * gl;
   const float dh = p.D ? p.D[h] : 0.f;
   float* ep = epi + wave * 16 * kEpiStride;
+  // C rows of t-block tb (rows past the chunk's end read as zero)
+  auto load_cf = [&](bf16x8_t* dst, int tb) {
+    const int t = tb * 32 + r32;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) dst[ks] = ldg_bf16x8(p.c, (tok0 + t) * p.ldc + ccol + ks * 16, t < rows);
+  };
+  // With the G^T tiles given, C enters only the state term (chunks after the
+  // first): a wave's first unit's rows load here, each later unit's while the
+  // unit before it runs, once the state term has consumed the current ones.
+  // The wave's units: i = 4 k + (k odd ? 3 - wave : wave), k = 0, 1, ...
+  bf16x8_t cfn[KS];
+  if constexpr (GT) {
+    if (c > 0 && wave < U) load_cf(cfn, ntb - 1 - wave / PG);
+  }
   for (int i = 0; i < U; ++i) {
     // units by decreasing work, dealt to the waves in snake order
     int w = i & 3;
@@ -685,8 +712,22 @@ __global__ void __launch_bounds__(256, 2) ssd_out2_kernel(SsdK p, const uint4* h
     const int tb = ntb - 1 - i / PG, pg = i % PG;
     const int t = tb * 32 + r32;
     bf16x8_t cf[KS];
+    if constexpr (GT) {
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) cf[ks] = ldg_bf16x8(p.c, (tok0 + t) * p.ldc + ccol + ks * 16, t < rows);
+      for (int ks = 0; ks < KS; ++ks) cf[ks] = cfn[ks];
+    } else {
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) cf[ks] = ldg_bf16x8(p.c, (tok0 + t) * p.ldc + ccol + ks * 16, t < rows);
+    }
+    // the first two G^T tiles load under the state term
+    f32x16_t gq[GT ? 2 : 1];
+    const float* gtb = GT ? p.gtile + (((int64_t)b * p.G + g) * p.nc + c) * (int64_t)p.npair * 1024 +
+                                (int64_t)(tb * (tb + 1) / 2) * 1024 + lane * 16
+                          : nullptr;
+    if constexpr (GT) {
+      gq[0] = ssd_load_gtile(gtb, 0, tb);
+      gq[1] = ssd_load_gtile(gtb, 1, tb);
+    }
     f32x16_t acc[NPT];
 #pragma unroll
     for (int j = 0; j < NPT; ++j)
@@ -711,6 +752,10 @@ __global__ void __launch_bounds__(256, 2) ssd_out2_kernel(SsdK p, const uint4* h
           acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(cf[ks], __builtin_bit_cast(bf16x8_t, hfr[ks][0]), acc[j], 0, 0, 0);
           acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(cf[ks], __builtin_bit_cast(bf16x8_t, hfr[ks][1]), acc[j], 0, 0, 0);
         }
+      }
+      if constexpr (GT) {
+        const int k = i >> 2, inext = 4 * (k + 1) + (((k + 1) & 1) ? 3 - wave : wave);
+        if (inext < U) load_cf(cfn, ntb - 1 - inext / PG);
       }
       // state term exp2(cl_t) C_t H = exp2(cl_t - cl_t0) (exp2(cl_t0) C_t H): the
       // per-row factor is applied with the earlier s-blocks' terms below
@@ -797,27 +842,15 @@ __global__ void __launch_bounds__(256, 2) ssd_out2_kernel(SsdK p, const uint4* h
       // The chunk's G^T tiles were formed once per group by the state kernel:
       // each is loaded two s-blocks ahead of the weighting and product that
       // consume it (past the diagonal, the diagonal tile again).
-      const float* gtb = p.gtile + (((int64_t)b * p.G + g) * p.nc + c) * (int64_t)p.npair * 1024 +
-                         (int64_t)(tb * (tb + 1) / 2) * 1024 + lane * 16;
-      auto load_g = [&](int sb) {
-        const float4* q = (const float4*)(gtb + (int64_t)min(sb, tb) * 1024);
-        f32x16_t v;
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          const float4 f = q[k];
-          v[4 * k] = f.x; v[4 * k + 1] = f.y; v[4 * k + 2] = f.z; v[4 * k + 3] = f.w;
-        }
-        return v;
-      };
-      g0 = load_g(0);
-      g1 = load_g(1);
+      g0 = gq[0];
+      g1 = gq[GT ? 1 : 0];
       int sb = 0;
       while (sb < tb) {
         offdiag(g0, sb);
-        g0 = load_g(sb + 2);
+        g0 = ssd_load_gtile(gtb, sb + 2, tb);
         if (++sb == tb) break;
         offdiag(g1, sb);
-        g1 = load_g(sb + 2);
+        g1 = ssd_load_gtile(gtb, sb + 2, tb);
         ++sb;
       }
     } else {
