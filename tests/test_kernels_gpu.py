@@ -87,6 +87,39 @@ def test_gemm_bf16_deep_k_ragged_m(gpu, M, N, K, n_acc):
     assert _rel(ss, (xf * xf).sum(-1)) < 1e-5
 
 
+@pytest.mark.parametrize("M,N,K,n_acc,mask", [(2000, 2192, 512, 1, 1), (2048, 2192, 512, 1, 0), (1000, 5000, 256, 1, 1),
+                                              (2040, 1100, 512, 2, 2), (2048, 1100, 512, 1, 1), (2000, 700, 512, 1, 1)])
+def test_gemm_direct_two_blocks_per_cu(gpu, M, N, K, n_acc, mask):
+    """64-row tiles numbering between one and two per CU (288, 288, 320, 288, 288 and 352 tiles of
+    64 x 256, 64 x 256, 64 x 256, 64 x 2 x 128, 64 x 128 and 64 x 64) run the direct loop with
+    stages within 80 KiB, two workgroups per CU, the row scales kept in the stage memory:
+    RMS-scaled and plain accumulators, the sums of squares, a ragged M and N."""
+    from torch_helion.hip import abi, ops
+
+    announce(f"gemm bf16 direct two per CU M={M} N={N} K={K} n_acc={n_acc} mask={mask}")
+    g = torch.Generator().manual_seed(3 * M + N)
+    x = torch.randn(M, K, generator=g).bfloat16()
+    ws = [(torch.randn(K, N, generator=g) * 0.03).bfloat16() for _ in range(n_acc)]
+    xf = x.float()
+    r = ((xf * xf).sum(-1, keepdim=True) / K + 1e-5).pow(-0.5)
+    packed = ops.pack_rhs([w.to(gpu) for w in ws], torch.bfloat16)
+    outs = [torch.empty(M, N, dtype=torch.float32, device=gpu) for _ in range(n_acc)]
+    o16 = torch.empty(M, N, dtype=torch.bfloat16, device=gpu)
+    ss = torch.empty(M, dtype=torch.float32, device=gpu)
+    epi = [ops.EpiSpec(abi.EPI_ACC, o, a=i) for i, o in enumerate(outs)] + [ops.EpiSpec(abi.EPI_ACC, o16, a=n_acc - 1)]
+    ops.gemm(ops.GemmCall(M, N, K, n_acc, x.to(gpu), packed, epi, sumsq=True, rscale_mask=mask, inv_k=1.0 / K,
+                          eps=1e-5, sumsq_out=ss))
+    torch.cuda.synchronize()
+    for i, (o, w) in enumerate(zip(outs, ws)):
+        ref = xf @ w.float()
+        if (mask >> i) & 1:
+            ref = ref * r
+        assert _rel(o, ref) < 1e-5, i
+        if i == n_acc - 1:
+            assert _maxabs(o16, ref) < BF16_TOL
+    assert _rel(ss, (xf * xf).sum(-1)) < 1e-5
+
+
 def test_gemm_bf16_rms_swiglu(gpu):
     from torch_helion.hip import abi, ops
 

@@ -241,25 +241,31 @@ __device__ __forceinline__ bool same_values(const EpiOutK& x, const EpiOutK& y) 
 
 // Every output op over `rows` staged rows of a whole column tile
 // (slab[r * srow + i * bn + j] = acc_i(row0 + r, tile_n * bn + j)), the
-// direct-loop kernel's epilogue when 256 threads tile it evenly: each thread
-// keeps one octet of columns (8 (tid % q8), q8 = bn / 8) and walks rows
-// tid / q8 + k 256 / q8 with the per-wave epilogue's passes (one 16-byte
-// store per pass, no per-element index division). Returns false (nothing
+// direct-loop kernel's epilogue when 256 threads tile it evenly: wave w owns
+// the column strip of q8 / 4 octets (q8 = bn / 8) starting at octet w q8 / 4;
+// each lane keeps one octet of the strip and walks rows lane / (q8 / 4) +
+// k 256 / q8 with the per-wave epilogue's passes (one 16-byte store per pass,
+// no per-element index division). A wave skips every output whose column
+// window misses its strip, so a tile holding several narrow outputs (a merged
+// launch) costs each wave only the outputs it holds. Returns false (nothing
 // done) when the tile does not divide so.
 template <bool SUMSQ>
 __device__ __forceinline__ bool epilogue_octets(const GemmK& p, const float* slab, int srow, int rows, const float* rs,
                                                 int64_t row0, int tile_n, int tid) {
   const int bn = p.bn, q8 = bn >> 3;
-  if ((bn & 7) != 0 || 256 % q8 != 0 || rows % (256 / q8) != 0) return false;
-  const int rstep = 256 / q8, np = rows / rstep;
-  const int r_l = tid / q8, c8 = (tid - r_l * q8) << 3;
+  if ((bn & 7) != 0 || (q8 & 3) != 0 || 256 % q8 != 0 || rows % (256 / q8) != 0) return false;
+  const int rstep = 256 / q8, np = rows / rstep, qw = q8 >> 2;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int r_l = lane / qw, c8 = (wave * qw + lane - r_l * qw) << 3;
   const int64_t col0 = (int64_t)tile_n * bn;
+  // this wave's strip (columns fit 32 bits, N < 2^31)
+  const int s0 = (int)col0 + 8 * wave * qw, s1 = s0 + 8 * qw;
   for (int o = 0; o < p.n_out; ++o) {
     const EpiOutK& eo = p.out[o];
     // an fp32 copy right after its bf16 output is stored from the same values
     const int o2 = o + 1 < p.n_out && same_values(eo, p.out[o + 1]) ? o + 1 : -1;
     if (o2 >= 0) ++o;
-    if (eo.ce <= col0 || eo.cb >= col0 + bn) continue;  // the window misses this tile
+    if (eo.ce <= s0 || eo.cb >= s1) continue;  // the window misses this wave's strip
     const int aoff = eo.a * bn, boff = eo.b * bn;
 #define TH_EPI_CASE(OP_) \
   case OP_: epi_slice<OP_, SUMSQ>(p, eo, o2, slab, srow, aoff, boff, rs, row0, col0, r_l, c8, np, rstep); break
@@ -583,8 +589,12 @@ __global__ void __launch_bounds__(256, 1) gemm_bf16_dl_kernel(GemmK p) {
   static_assert(STAGES >= 2 && STAGES <= 8 && (STAGES - 1) * (LA + LB) < 64, "stage count");
   constexpr int BODY = MAIN_BYTES > EPI_BYTES ? MAIN_BYTES : EPI_BYTES;
   constexpr int NMF = TM * TN;
-  __shared__ __attribute__((aligned(16))) char smem[BODY + BM * 4];
-  float* rs = (float*)(smem + BODY);
+  // the row scales: at the end of the stages when that is clear of the
+  // epilogue's slab (they are stored after the main loop's last reads, past a
+  // barrier), so that a block within 80 KiB takes no extra LDS
+  constexpr int RS_OFF = BODY - BM * 4 >= EPI_BYTES ? BODY - BM * 4 : BODY;
+  __shared__ __attribute__((aligned(16))) char smem[RS_OFF + BM * 4];
+  float* rs = (float*)(smem + RS_OFF);
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -697,20 +707,25 @@ __global__ void __launch_bounds__(256, 1) gemm_bf16_dl_kernel(GemmK p) {
     }
   }
 
+  float rsv[TM];
   if constexpr (SUMSQ) {
 #pragma unroll
     for (int t = 0; t < TM; ++t) {
       const float v = ss[t] + __shfl_xor(ss[t], 32);
+      rsv[t] = rsqrtf(v * p.inv_k + p.eps);
       if ((t & 1) == wn && lane < 32) {
-        const int r = wm * WM + t * 32 + lane;
-        rs[r] = rsqrtf(v * p.inv_k + p.eps);
-        const int64_t gr = m0 + r;
+        const int64_t gr = m0 + wm * WM + t * 32 + lane;
         if (p.sumsq_out && tni == 0 && gr < p.M) p.sumsq_out[gr] = v;
       }
     }
   }
   // (barriers for LDS reuse only: the global stores drain meanwhile)
   lds_barrier();
+  if constexpr (SUMSQ) {
+#pragma unroll
+    for (int t = 0; t < TM; ++t)
+      if ((t & 1) == wn && lane < 32) rs[wm * WM + t * 32 + lane] = rsv[t];
+  }
 
   float* slab = (float*)smem;
   // (not unrolled: the accumulator indices inside are constant either way, and the
@@ -1666,13 +1681,33 @@ constexpr int dl_stages() {
   return BM > 64 ? 2 : (s > 8 ? 8 : s);
 }
 
+// Two workgroups per CU: stages within 80 KiB each (the row scales share them).
+template <int BM, int BNC>
+constexpr int dl_stages2() {
+  constexpr int s = 81920 / ((BM + BNC) * 128);
+  return s > 8 ? 8 : s;
+}
+
 template <int BM, int BNC>
 static void launch_bf16_dl(const GemmK& k, hipStream_t s) {
-  constexpr int S = dl_stages<BM, BNC>();
-  if (k.sumsq)
-    hipLaunchKernelGGL((gemm_bf16_dl_kernel<BM, BNC, true, S>), dim3(k.tiles_m * k.tiles_n), dim3(256), 0, s, k);
-  else
-    hipLaunchKernelGGL((gemm_bf16_dl_kernel<BM, BNC, false, S>), dim3(k.tiles_m * k.tiles_n), dim3(256), 0, s, k);
+  const int tiles = k.tiles_m * k.tiles_n, cus = device_cus();
+  auto go = [&](auto st) {
+    constexpr int S = decltype(st)::value;
+    if (k.sumsq)
+      hipLaunchKernelGGL((gemm_bf16_dl_kernel<BM, BNC, true, S>), dim3(tiles), dim3(256), 0, s, k);
+    else
+      hipLaunchKernelGGL((gemm_bf16_dl_kernel<BM, BNC, false, S>), dim3(tiles), dim3(256), 0, s, k);
+  };
+  // More tiles than CUs but no more than two per CU: shallower stages let two
+  // workgroups share a CU, so the tiles run as one round (each workgroup's
+  // load latency and epilogue under the other's work) instead of two.
+  if constexpr (BM == 64 && dl_stages2<BM, BNC>() >= 2) {
+    if (cus > 0 && tiles > cus && tiles <= 2 * cus) {
+      go(std::integral_constant<int, dl_stages2<BM, BNC>()>());
+      return;
+    }
+  }
+  go(std::integral_constant<int, dl_stages<BM, BNC>()>());
 }
 
 template <int BM, int BNC>
