@@ -1,6 +1,7 @@
 """Cost model on the CPU: the GEMM tile choice mirrors th_gemm's, the calibration fit
 recovers the parameters that generated its samples, and merged sibling launches are
-priced with the fitted merged-launch factor (the planner's merge-or-split decision)."""
+priced with the fitted merged-launch factor (the planner's merge-or-split decision);
+and the counters tool's per-symbol table."""
 
 from __future__ import annotations
 
@@ -108,3 +109,21 @@ def test_merge_decision_follows_merged_launch_factor(mamba_program):
     rep = launch_merge_report([one, big])
     assert f"{big.merged_us:,.1f}" in rep and f"{big.split_us:,.1f}" in rep
     assert rep.rstrip().endswith("| split |")
+
+
+def test_counter_table_groups_by_symbol():
+    """The counters tool's table: one row per kernel symbol (parameters dropped), averaged over
+    its positions, longest total first; a dispatch above --split-us gets a row of its own."""
+    from torch_helion.hip.counters import by_symbol
+
+    def pos(sym, us, util, fetch):
+        return {"symbol": sym, "duration_us": us, "mfma_util": util, "clock_ghz": 2.0, "FETCH_SIZE": fetch,
+                "WRITE_SIZE": 1024.0}
+
+    g = "void th::gemm<256, 1>(th::GemmK)"
+    rows = by_symbol([pos(g, 90.0, 0.3, 2048.0), pos("th::carry(th::SsdK)", 20.0, 0.0, 1024.0), pos(g, 110.0, 0.5, 4096.0),
+                      pos(g, 1800.0, 0.47, 8192.0)], split_us=1000.0).splitlines()
+    assert rows[2] == "| `th::gemm<256, 1> (long)` | 1 | 1800.0 | 47.0% | 2.00 | 8.0 | 1.0 |"
+    assert rows[3] == "| `th::gemm<256, 1>` | 2 | 100.0 | 40.0% | 2.00 | 3.0 | 1.0 |"
+    assert rows[4] == "| `th::carry` | 1 | 20.0 | 0.0% | 2.00 | 1.0 | 1.0 |"
+    assert len(by_symbol([pos(g, 90.0, 0.3, 2048.0), pos(g, 1800.0, 0.4, 2048.0)]).splitlines()) == 3

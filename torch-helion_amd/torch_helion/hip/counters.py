@@ -20,7 +20,11 @@ Derived figures, per position, when the counters are present:
   part held during the kernel;
 FETCH_SIZE / WRITE_SIZE are kept in KiB as read (on this part FETCH_SIZE reads
 half the bytes of a calibrated copy, WRITE_SIZE all of them).
-The result goes to ``10_device_counters.json`` in the run directory.
+The result goes to ``10_device_counters.json`` in the run directory. With
+``--by-symbol`` the tool prints a markdown table instead of the positions:
+one row per kernel symbol (template arguments kept, parameters dropped),
+averaged over its positions; positions of one symbol whose dispatches last more
+than ``--split-us`` (default: never) form a row of their own, marked "long".
 """
 
 from __future__ import annotations
@@ -78,12 +82,38 @@ def per_position(seq, period: int, reps: int, simds: int = 1024, xcds: int = 8) 
     return out
 
 
+def by_symbol(pos: list[dict], split_us: float | None = None) -> str:
+    """Markdown table of the positions grouped by kernel symbol, longest total first."""
+    groups: dict[str, list[dict]] = {}
+    for p in pos:
+        sym = p.get("symbol", "?")
+        sym = sym[5:] if sym.startswith("void ") else sym
+        sym = sym[: sym.index("(")] if "(" in sym else sym
+        if split_us is not None and p.get("duration_us", 0.0) > split_us:
+            sym += " (long)"
+        groups.setdefault(sym, []).append(p)
+
+    def avg(ps: list[dict], k: str) -> float:
+        v = [x[k] for x in ps if k in x]
+        return sum(v) / len(v) if v else float("nan")
+
+    rows = sorted(groups.items(), key=lambda kv: -avg(kv[1], "duration_us") * len(kv[1]))
+    out = ["| kernel symbol | per run | avg us (under counters) | MFMA util | clock GHz | FETCH_SIZE MiB (as read) "
+           "| WRITE_SIZE MiB |", "|---|---:|---:|---:|---:|---:|---:|"]
+    for sym, ps in rows:
+        out.append(f"| `{sym}` | {len(ps)} | {avg(ps, 'duration_us'):.1f} | {100 * avg(ps, 'mfma_util'):.1f}% | "
+                   f"{avg(ps, 'clock_ghz'):.2f} | {avg(ps, 'FETCH_SIZE') / 1024:.1f} | {avg(ps, 'WRITE_SIZE') / 1024:.1f} |")
+    return "\n".join(out)
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("run_dir", type=Path)
     ap.add_argument("csv", nargs="+", type=Path)
     ap.add_argument("--period", type=int, required=True, help="dispatches of one program run")
     ap.add_argument("--reps", type=int, default=3)
+    ap.add_argument("--by-symbol", action="store_true", help="print a markdown table per kernel symbol")
+    ap.add_argument("--split-us", type=float, default=None, help="with --by-symbol: longer dispatches get their own row")
     a = ap.parse_args()
     from ..cost_models.hw_spec import HardwareSpec
 
@@ -97,6 +127,9 @@ def main() -> int:
             for p, l in zip(pos, launches):
                 p["kernel"] = l["kernel"]
     (a.run_dir / "10_device_counters.json").write_text(json.dumps(pos, indent=2))
+    if a.by_symbol:
+        print(by_symbol(pos, a.split_us))
+        return 0
     for p in pos:
         print({k: (round(v, 4) if isinstance(v, float) else v) for k, v in p.items() if k != "symbol"})
     return 0
