@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define TH_ABI_VERSION 5
+#define TH_ABI_VERSION 6
 
 typedef enum th_status {
   TH_OK = 0,
@@ -130,6 +130,15 @@ typedef struct th_gemm_desc {
                              optional for TH_F32 (small grids then split K over workgroups through it) */
   int64_t workspace_bytes;
   const float* lhs_gain;  /* optional [K] fp32 per-column gain of lhs (TH_F8E4M3 only; 16-byte aligned) */
+  const float* rs_parts;  /* optional [M, n_rs_parts] fp32, row stride ld_rs_parts (TH_BF16, with sumsq):
+                             each row's sum of squares is the in-order sum of these parts instead of
+                             sum_k lhs^2, for an lhs whose producer applied an RMSNorm gain and kept
+                             the sums of the unscaled values (th_ssd_chunked's y_gain, rs_parts).
+                             n_rs_parts and ld_rs_parts multiples of 4, 16-byte aligned. No
+                             counterpart in the reference (its RMSNorm is one kernel). */
+  int64_t ld_rs_parts;
+  int32_t n_rs_parts;
+  int32_t pad3_;
 } th_gemm_desc;
 
 /* Per-accumulator column tile th_gemm uses for (N, n_acc, in_dtype) when an
@@ -282,6 +291,13 @@ typedef struct th_ssd_desc {
   float* workspace;                   /* th_ssd_workspace_bytes(...) bytes, or
                                          th_ssd_gtile_workspace_bytes(...) (16-byte aligned) */
   int64_t workspace_bytes;
+  const float* y_gain;                /* optional [H*P] fp32 (16-byte aligned): y is stored times this
+                                         per-column gain (the next RMSNorm's); bf16 y of 16-byte aligned
+                                         rows, no y32 or dskip, head_dim a multiple of 32 (the MFMA path) */
+  float* rs_parts;                    /* with y_gain: [B*S, H*P/32] fp32, row stride ld_rs_parts: per
+                                         token and 32-column block, the sum of squares of y before the
+                                         gain (th_gemm's rs_parts). No counterpart in the reference. */
+  int64_t ld_rs_parts;
 } th_ssd_desc;
 
 int64_t th_ssd_workspace_bytes(int32_t batch, int32_t seq, int32_t heads, int32_t head_dim,

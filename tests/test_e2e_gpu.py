@@ -450,6 +450,14 @@ def test_mamba_lm_merged_in_projection_activation_gain(gpu, tmp_path):
     merged = [l for l in mer.device_program.launches if "+" in l.kernel and l.entry == "th_gemm"]
     assert len(merged) == 2 and all(l.info["gain_on_activation"] for l in merged), \
         [l.kernel for l in mer.device_program.launches]
+    # the gated norm before each out-projection folds into the scan (its gain) and the
+    # GEMM (its row scale): one scan per layer names its GEMM, which has no norm launch
+    for res in (sep, mer):
+        folds = {l.info["norm_gain_for"] for l in res.device_program.launches if l.info.get("norm_gain_for")}
+        assert len(folds) == cfg.n_layers
+        for l in res.device_program.launches:
+            if l.kernel in folds:
+                assert l.entry == "th_gemm" and l.info.get("row_sums_from_producer"), (l.kernel, l.entry, l.info)
     a = sep.run(*ids)[0].float().cpu()
     b = mer.run(*ids)[0].float().cpu()
     assert (a - b).abs().max().item() / a.abs().max().item() < 1e-3

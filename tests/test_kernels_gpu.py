@@ -817,6 +817,62 @@ def test_ssd_shared_g_tiles_bit_exact(gpu, bs, s, h, p, n, g, chunk):
     assert _maxabs(outs[1][1], ref * gate.double()) < BF16_TOL
 
 
+@pytest.mark.parametrize("bs,s,h,p,n,g,chunk", [(1, 512, 8, 64, 128, 1, 256), (2, 200, 4, 32, 64, 2, 64)])
+def test_ssd_output_gain_and_row_sums(gpu, bs, s, h, p, n, g, chunk):
+    """y_gain / rs_parts: the scan stores y times a per-column gain (the next RMSNorm's) and
+    the sums of squares of y per token and 32 columns. Against the same scan's fp32 copy of
+    y: the stored values are bf16(y * g) bit for bit, the sums those of y^2 within fp32
+    rounding (the kernel adds 8 per lane, then across the 4 lanes of a row)."""
+    from torch_helion.hip import ops
+
+    announce(f"ssd output gain + row sums bs={bs} s={s} h={h} p={p} n={n} g={g} chunk={chunk}")
+    x, bm, cm, dt, A, D, gate = _ssd_case(bs, s, h, p, n, g, torch.bfloat16, seed=7 * s + h)
+    args = dict(x=x.to(gpu), b=bm.to(gpu), c=cm.to(gpu), dt=dt.to(gpu), batch=bs, seq=s, heads=h, head_dim=p,
+                state_dim=n, ngroups=g, chunk=chunk, A=A.to(gpu), D=D.to(gpu), gate=gate.to(gpu))
+    ws = torch.empty(ops.ssd_workspace_bytes(bs, s, h, p, n, chunk, g) // 4 + 1, device=gpu)
+    y16 = torch.empty(bs * s, h * p, dtype=torch.bfloat16, device=gpu)
+    y32 = torch.empty(bs * s, h * p, device=gpu)
+    ops.ssd_chunked(out=y16, out32=y32, workspace=ws, **args)
+    gain = (torch.rand(h * p, generator=torch.Generator().manual_seed(5)) + 0.5).to(gpu)
+    yg = torch.empty(bs * s, h * p, dtype=torch.bfloat16, device=gpu)
+    parts = torch.full((bs * s, h * p // 32), float("nan"), device=gpu)
+    ops.ssd_chunked(out=yg, workspace=ws, y_gain=gain, rs_parts=parts, **args)
+    torch.cuda.synchronize()
+    assert torch.equal(yg, (y32 * gain).bfloat16())
+    ref = (y32.double() ** 2).reshape(bs * s, h * p // 32, 32).sum(-1)
+    assert torch.isfinite(parts).all()
+    assert _rel(parts, ref) < 1e-6
+
+
+@pytest.mark.parametrize("M,N,K", [(16384, 1024, 2048), (300, 512, 256)])  # persistent 256 x 256; direct loop
+def test_gemm_row_sums_from_producer(gpu, M, N, K):
+    """rs_parts: the row scale from the lhs producer's partial sums of squares (of the values
+    before its gain) instead of the GEMM's own sum over its lhs. With parts that are the
+    per-32-column sums of x^2 and the lhs x * g, the output is RMSNorm(x) * g times W plus the
+    residual, as the th_rmsnorm-then-GEMM route computes it, within bf16 rounding of the lhs."""
+    from torch_helion.hip import abi, ops
+
+    announce(f"gemm row sums from producer M={M} N={N} K={K}")
+    gen = torch.Generator().manual_seed(M + N)
+    x = torch.randn(M, K, generator=gen)
+    gain = torch.rand(K, generator=gen) + 0.5
+    w = (torch.randn(K, N, generator=gen) * 0.03).bfloat16()
+    res = torch.randn(M, N, generator=gen).bfloat16()
+    lhs = (x * gain).bfloat16()
+    parts = (x * x).reshape(M, K // 32, 32).sum(-1)
+    r = ((x * x).sum(-1, keepdim=True) / K + 1e-5).rsqrt()
+    ref = (lhs.float() @ w.float()) * r + res.float()
+    packed = ops.pack_rhs([w.to(gpu)], torch.bfloat16)
+    out = torch.empty(M, N, device=gpu)
+    ss = torch.empty(M, device=gpu)
+    ops.gemm(ops.GemmCall(M, N, K, 1, lhs.to(gpu), packed, [ops.EpiSpec(abi.EPI_ADD, out, e=0)], sumsq=True,
+                          rscale_mask=1, inv_k=1.0 / K, eps=1e-5, extras=[res.to(gpu)], sumsq_out=ss,
+                          rs_parts=parts.to(gpu)))
+    torch.cuda.synchronize()
+    assert _rel(ss, (x * x).sum(-1)) < 1e-5
+    assert _rel(out, ref) < 1e-5
+
+
 @pytest.mark.parametrize("dtype,bs,s,c,k,col0", [
     (torch.float32, 2, 300, 1152, 4, 0),
     (torch.bfloat16, 2, 300, 1152, 4, 0),     # 16-byte vector path, ragged last token run

@@ -508,8 +508,9 @@ __global__ void __launch_bounds__(256, 1) gemm_bf16_kernel(GemmK p) {
       v += __shfl_xor(v, 4);
       if (lch == 0) {
         const int r = lrow + 32 * i;
-        rs[r] = rsqrtf(v * p.inv_k + p.eps);
         const int64_t gr = m0 + r;
+        v = row_sumsq(p, gr, v);
+        rs[r] = rsqrtf(v * p.inv_k + p.eps);
         if (p.sumsq_out && tni == 0 && gr < p.M) p.sumsq_out[gr] = v;
       }
     }
@@ -711,10 +712,10 @@ __global__ void __launch_bounds__(256, 1) gemm_bf16_dl_kernel(GemmK p) {
   if constexpr (SUMSQ) {
 #pragma unroll
     for (int t = 0; t < TM; ++t) {
-      const float v = ss[t] + __shfl_xor(ss[t], 32);
+      const int64_t gr = m0 + wm * WM + t * 32 + (lane & 31);
+      const float v = row_sumsq(p, gr, ss[t] + __shfl_xor(ss[t], 32));
       rsv[t] = rsqrtf(v * p.inv_k + p.eps);
       if ((t & 1) == wn && lane < 32) {
-        const int64_t gr = m0 + wm * WM + t * 32 + lane;
         if (p.sumsq_out && tni == 0 && gr < p.M) p.sumsq_out[gr] = v;
       }
     }
@@ -989,11 +990,12 @@ __global__ void __launch_bounds__(64 * NW, 1) gemm_bf16_pk_kernel(GemmK p) {
     if constexpr (SUMSQ) {
 #pragma unroll
       for (int j = 0; j < TM / 2; ++j) {
-        const float v = ss[j] + __shfl_xor(ss[j], 32);
+        float v = ss[j] + __shfl_xor(ss[j], 32);
         if (lane < 32) {
           const int r = wm * WM + (2 * j + wn) * 32 + lane;
-          rsx[r] = rsqrtf(v * p.inv_k + p.eps);
           const int64_t gr = (int64_t)tmi * BM + r;
+          if constexpr (!ASPLIT) v = row_sumsq(p, gr, v);
+          rsx[r] = rsqrtf(v * p.inv_k + p.eps);
           if (p.sumsq_out && tni == 0 && gr < p.M) p.sumsq_out[gr] = v;
         }
       }
@@ -1803,6 +1805,13 @@ extern "C" int th_gemm(const th_gemm_desc* d, void* stream) {
     return TH_ERR_UNSUPPORTED;
   }
   TH_CHECK_ARG(d->lhs_gain == nullptr || aligned(d->lhs_gain, 16), "th_gemm: lhs_gain must be 16-byte aligned");
+  if (d->rs_parts != nullptr) {
+    TH_CHECK_ARG(d->in_dtype == TH_BF16, "th_gemm: rs_parts is implemented for TH_BF16 only");
+    TH_CHECK_ARG(d->sumsq, "th_gemm: rs_parts set without sumsq");
+    TH_CHECK_ARG(d->n_rs_parts > 0 && d->n_rs_parts % 4 == 0 && d->ld_rs_parts >= d->n_rs_parts &&
+                     d->ld_rs_parts % 4 == 0 && aligned(d->rs_parts, 16),
+                 "th_gemm: rs_parts needs a positive multiple of 4 parts per row, 16-byte aligned rows");
+  }
   int bn = choose_bn(d->N, d->n_acc, d->in_dtype);
   // One accumulator over 1024 <= N < 2048 columns: 256 x 256 tiles, one per CU
   // per wave, when they make whole waves, instead of twice as many 256 x 128
@@ -1897,6 +1906,9 @@ extern "C" int th_gemm(const th_gemm_desc* d, void* stream) {
   k.period = d->rope_period > 0 ? d->rope_period : 1;
   k.sumsq_out = d->sumsq_out;
   k.gain = d->lhs_gain;
+  k.rs_parts = d->rs_parts;
+  k.ld_rs_parts = d->ld_rs_parts;
+  k.n_rs_parts = d->n_rs_parts;
   if (!device_ready()) {
     set_error("th_gemm: th_init was not called for the current device");
     return TH_ERR_NOT_INIT;
@@ -1984,6 +1996,11 @@ extern "C" int th_gemm(const th_gemm_desc* d, void* stream) {
       for (int o = 0; o < d->n_out; ++o) split &= d->out[o].b < 0;
       k.asplit = split ? 1 : 0;
       wave_epi &= split;
+    }
+    // (the whole-accumulator-per-wave instances leave the row-sum parts out: registers)
+    if (k.asplit && d->rs_parts != nullptr) {
+      set_error("th_gemm: rs_parts is not implemented with whole-head RoPE on two accumulators");
+      return TH_ERR_UNSUPPORTED;
     }
     MainLoop ml = MainLoop::staged;
     if (direct) ml = wave_epi ? MainLoop::persistent : MainLoop::direct;

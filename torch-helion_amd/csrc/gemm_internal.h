@@ -38,7 +38,29 @@ struct GemmK {
   EpiOutK out[TH_MAX_OUT];
   float* sumsq_out;
   const float* gain;  // optional [K]: products use lhs[m, k] * gain[k] (fp8 path); sumsq stays unscaled
+  // optional [M][n_rs_parts] (row stride ld_rs_parts): each row's sum of squares as
+  // partial sums made by the lhs's producer, summed in order instead of sum_k lhs^2
+  const float* rs_parts;
+  int64_t ld_rs_parts;
+  int n_rs_parts;
 };
+
+// Row `row`'s sum of squares: `own` (the kernel's sum over its lhs fragments), or
+// the sum of the producer's partial sums when the caller gave them (four at a
+// time, in order; rows past M read row M - 1, whose scale is never used).
+__device__ __forceinline__ float row_sumsq(const GemmK& p, int64_t row, float own) {
+  if (p.rs_parts == nullptr) return own;
+  const float4* q = (const float4*)(p.rs_parts + (row < p.M ? row : p.M - 1) * p.ld_rs_parts);
+  float v = 0.f;
+  for (int i = 0; i < (p.n_rs_parts >> 2); ++i) {
+    const float4 f = q[i];
+    v += f.x;
+    v += f.y;
+    v += f.z;
+    v += f.w;
+  }
+  return v;
+}
 
 // fp8-weight path (gemm_fp8.hip)
 struct Fp8K {

@@ -40,6 +40,9 @@ struct SsdK {
   int vec_epi;    // bf16 y (and gate), no dskip, 16-byte aligned rows: vector epilogue
   float* gtile;   // optional [B][G][nc][npair][64 lanes][16]: the chunks' G^T tiles (MFMA path)
   int npair;      // tiles per chunk: (Q/32)(Q/32 + 1)/2
+  const float* ygain;  // optional [H*P]: y stored times this gain (vector epilogue), and
+  float* rsp;          // the sums of squares of y before it per (token, 32-column block)
+  int64_t ldrsp;
 };
 
 // Running sum of dA (or the given cum re-based) for chunk ``c`` into cl[0..Q),
@@ -625,6 +628,7 @@ __global__ void __launch_bounds__(256, 2) ssd_out2_kernel(SsdK p, const uint4* h
   uint4* xs = (uint4*)(epi + 4 * 16 * kEpiStride);  // [Q/32][2][PT][64] B fragments of x
   uint4* hs = xs + (p.Q >> 5) * 2 * (p.P >> 5) * 64;  // [PT][KS][64][2] carried-state fragments
   float* wt = (float*)(hs + p.P * p.N / 4);           // decay weights, row tb at 16 tb (tb - 1)
+  float* sg = wt + 16 * (p.Q >> 5) * ((p.Q >> 5) - 1);  // this head's P output gains (ygain)
   const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z, tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = h / p.hpg, gl = lane >> 5, r32 = lane & 31;
@@ -676,6 +680,7 @@ __global__ void __launch_bounds__(256, 2) ssd_out2_kernel(SsdK p, const uint4* h
       xs[((sb * 2 + 1) * PT + pt) * 64 + lane] = __builtin_bit_cast(uint4, pk8(v + 8));
     }
   }
+  if (p.ygain && tid < (p.P >> 2)) ((float4*)sg)[tid] = ((const float4*)(p.ygain + (int64_t)h * p.P))[tid];
   __syncthreads();
   // wt[16 tb (tb - 1) + s] = exp2(cl_t0 - cl_s) dt_s for the s before t0 = 32 tb
   for (int tb = 1; tb < ntb; ++tb)
@@ -942,6 +947,20 @@ __global__ void __launch_bounds__(256, 2) ssd_out2_kernel(SsdK p, const uint4* h
 #pragma unroll
             for (int k2 = 0; k2 < 8; ++k2) v[k2] *= gv[k2];
           }
+          if (p.ygain) {
+            // the next RMSNorm's gain, applied here; its row scale is applied by the
+            // consumer from these sums: a row's 32 columns of p-tile pt are in the
+            // four lanes 4 row .. 4 row + 3, 8 each
+            float s2 = 0.f;
+#pragma unroll
+            for (int k2 = 0; k2 < 8; ++k2) s2 += v[k2] * v[k2];
+            s2 += __shfl_xor(s2, 1);
+            s2 += __shfl_xor(s2, 2);
+            if (ok[hh] && (lane & 3) == 0) p.rsp[tok[hh] * p.ldrsp + (int64_t)h * PT + pt] = s2;
+            const float4 g0 = *(const float4*)&sg[pt * 32 + c0], g1 = *(const float4*)&sg[pt * 32 + c0 + 4];
+            v[0] *= g0.x; v[1] *= g0.y; v[2] *= g0.z; v[3] *= g0.w;
+            v[4] *= g1.x; v[5] *= g1.y; v[6] *= g1.z; v[7] *= g1.w;
+          }
           if (ok[hh]) {
             *(uint4*)((uint16_t*)p.y + tok[hh] * p.ldy + oc) = __builtin_bit_cast(uint4, pk8(v));
             if (p.y32) {
@@ -1080,7 +1099,8 @@ static size_t state_lds(int P, int N) { return (size_t)(256 * 4 + 32 * P + 32 * 
 // carried state | triangular decay-weight table
 static size_t out2_lds(int Q, int P, int N) {
   const size_t nt = Q / 32;
-  return 512 * 4 + 4 * 16 * kEpiStride * 4 + (size_t)Q * P * 2 + (size_t)P * N * 4 + 16 * nt * (nt - 1) * 4;
+  return 512 * 4 + 4 * 16 * kEpiStride * 4 + (size_t)Q * P * 2 + (size_t)P * N * 4 + 16 * nt * (nt - 1) * 4 +
+         (size_t)P * 4;
 }
 static size_t out_lds(int RB, int P, int N) {
   const size_t intra = (size_t)RB * (N + 1) + (size_t)RB * (P + 1) + (size_t)RB * (RB + 1);
@@ -1184,6 +1204,9 @@ extern "C" int th_ssd_chunked(const th_ssd_desc* d, void* stream) {
   k.tot = d->workspace + (int64_t)k.B * k.H * k.nc * k.P * k.N;
   k.gtile = nullptr;
   k.npair = (k.Q / 32) * (k.Q / 32 + 1) / 2;
+  k.ygain = d->y_gain;
+  k.rsp = d->rs_parts;
+  k.ldrsp = d->ld_rs_parts;
   hipStream_t s = (hipStream_t)stream;
   // MFMA path: bf16 operands, 32-wide p / n tiles, 16-byte aligned rows.
   auto al16 = [](const void* q) { return ((uintptr_t)q & 15) == 0; };
@@ -1192,6 +1215,13 @@ extern "C" int th_ssd_chunked(const th_ssd_desc* d, void* stream) {
                     d->ld_b % 8 == 0 && d->ld_c % 8 == 0 && d->ld_b < (1 << 22) && d->ld_x < (1 << 22) && al16(d->x) &&
                     al16(d->b) && al16(d->c) &&
                     out2_lds(k.Q, k.P, k.N) <= kMaxLds;
+  if (d->y_gain) {
+    // the gain and the sums live in the MFMA path's vector epilogue only
+    TH_CHECK_ARG(mfma && k.vec_epi && !d->y32 && d->rs_parts && ((uintptr_t)d->y_gain & 15) == 0 &&
+                     d->ld_rs_parts >= (int64_t)k.H * (k.P / 32),
+                 "th_ssd_chunked: y_gain needs the bf16 MFMA path (16-byte aligned bf16 y, no y32 or dskip, "
+                 "head_dim a multiple of 32), rs_parts and ld_rs_parts >= heads * head_dim / 32");
+  }
   if (mfma) {
     const int64_t bhc = (int64_t)k.B * k.H * k.nc;
     uint4* hf = (uint4*)(d->workspace + bhc * k.P * k.N + ssd_tot_floats(bhc));

@@ -13,7 +13,7 @@ from pathlib import Path
 
 from .build import LIB_PATH
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 # th_status
 TH_OK = 0
@@ -63,6 +63,7 @@ class GemmDesc(C.Structure):
         ("sumsq_out", _p),
         ("rhs_scale", _p), ("workspace", _p), ("workspace_bytes", _i64),
         ("lhs_gain", _p),
+        ("rs_parts", _p), ("ld_rs_parts", _i64), ("n_rs_parts", _i32), ("pad3_", _i32),
     ]
 
 
@@ -105,6 +106,7 @@ class SsdDesc(C.Structure):
         ("cum", _p), ("ld_cum", _i64), ("A", _p), ("D", _p), ("dskip", _p), ("ld_dskip", _i64),
         ("gate", _p), ("ld_gate", _i64), ("gate_dtype", _i32), ("y_dtype", _i32),
         ("y", _p), ("ld_y", _i64), ("y32", _p), ("ld_y32", _i64), ("workspace", _p), ("workspace_bytes", _i64),
+        ("y_gain", _p), ("rs_parts", _p), ("ld_rs_parts", _i64),
     ]
 
 

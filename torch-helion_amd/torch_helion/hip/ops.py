@@ -106,6 +106,8 @@ class GemmCall:
     rhs_scale: torch.Tensor | None = None      # fp8: [n_acc, N] fp32 per-column scales
     workspace: torch.Tensor | None = None      # gemm_workspace_bytes(...) bytes (fp8: required; fp32: optional)
     lhs_gain: torch.Tensor | None = None       # fp8: [K] fp32, products use lhs * gain (RMSNorm gain)
+    rs_parts: torch.Tensor | None = None       # bf16, with sumsq: [M, parts] fp32, the rows' sums of squares
+                                               # as partial sums (the lhs producer's), used instead of sum lhs^2
 
     def descriptor(self) -> abi.GemmDesc:
         d = abi.GemmDesc()
@@ -148,6 +150,11 @@ class GemmCall:
             if self.lhs_gain.dtype != torch.float32 or not self.lhs_gain.is_contiguous() or self.lhs_gain.numel() != self.K:
                 raise abi.HipBackendError("th_gemm", abi.TH_ERR_INVALID, "lhs_gain must be contiguous fp32 [K]")
             d.lhs_gain = self.lhs_gain.data_ptr()
+        if self.rs_parts is not None:
+            if self.rs_parts.dtype != torch.float32 or self.rs_parts.dim() != 2 or self.rs_parts.shape[0] != self.M:
+                raise abi.HipBackendError("th_gemm", abi.TH_ERR_INVALID, "rs_parts must be fp32 [M, parts]")
+            d.rs_parts, d.ld_rs_parts = self.rs_parts.data_ptr(), _row_major(self.rs_parts, "th_gemm rs_parts")
+            d.n_rs_parts = self.rs_parts.shape[1]
         return d
 
 
@@ -284,7 +291,12 @@ def ssd_workspace_bytes(batch: int, seq: int, heads: int, head_dim: int, state_d
 
 
 def ssd_chunked(*, x, b, c, dt, out, workspace, batch, seq, heads, head_dim, state_dim, ngroups, chunk, A=None, D=None,
-                cum=None, dt_stride=1, dskip=None, gate=None, out32=None, kernel: str | None = None) -> None:
+                cum=None, dt_stride=1, dskip=None, gate=None, out32=None, y_gain=None, rs_parts=None,
+                kernel: str | None = None) -> None:
+    """One th_ssd_chunked launch. ``y_gain`` (fp32 [heads * head_dim]) stores y times that
+    per-column gain and writes, into ``rs_parts`` (fp32 [batch * seq, heads * head_dim / 32]),
+    the sums of squares of y before it per token and 32 columns: an RMSNorm whose row scale
+    the consuming th_gemm applies (its ``rs_parts``)."""
     lib = _lib(x)
     d = abi.SsdDesc()
     d.batch, d.seq, d.heads, d.head_dim, d.state_dim, d.ngroups, d.chunk = batch, seq, heads, head_dim, state_dim, ngroups, chunk
@@ -309,6 +321,13 @@ def ssd_chunked(*, x, b, c, dt, out, workspace, batch, seq, heads, head_dim, sta
     d.y, d.ld_y, d.y_dtype = out.data_ptr(), _row_major(out, "ssd y"), th_dtype(out)
     if out32 is not None:
         d.y32, d.ld_y32 = out32.data_ptr(), _row_major(out32, "ssd y32")
+    if y_gain is not None:
+        if y_gain.dtype != torch.float32 or not y_gain.is_contiguous() or y_gain.numel() != heads * head_dim:
+            raise abi.HipBackendError("th_ssd_chunked", abi.TH_ERR_INVALID, "y_gain must be contiguous fp32 [H*P]", kernel)
+        if rs_parts is None or rs_parts.dtype != torch.float32:
+            raise abi.HipBackendError("th_ssd_chunked", abi.TH_ERR_INVALID, "y_gain needs fp32 rs_parts", kernel)
+        d.y_gain = y_gain.data_ptr()
+        d.rs_parts, d.ld_rs_parts = rs_parts.data_ptr(), _row_major(rs_parts, "ssd rs_parts")
     d.workspace, d.workspace_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
     abi.check(lib.th_ssd_chunked(C.byref(d), _stream(x)), "th_ssd_chunked", kernel)
 

@@ -190,6 +190,9 @@ class DeviceProgram:
         self._merge_groups, self._merged_away = groups, away
         # (e4m3 decode GEMMs: a few rows against weight streams, one launch always pays)
         self._fp8_groups = self._plan_fp8_merges(program, self._merged_away) if merge_siblings is not False else {}
+        # scans whose only reader normalises them with a gain: the scan applies it (_plan_norm_folds)
+        self._rs_parts: dict[tuple, torch.Tensor] = {}
+        self._norm_folds = self._plan_norm_folds(program)
         for i, k in enumerate(program.kernels):
             self._cur = i
             if self.reuse:
@@ -615,12 +618,14 @@ class DeviceProgram:
                 extras.append(o.extra)
         if len(extras) > abi.MAX_EXTRA:
             return None
-        norm_launch, normed = None, None
+        norm_launch, normed, rs_parts = None, None, None
         gain = self._unfold_gain(spec, plan, used)
         if gain is not None:
             # (collect mode only asks: the shared buffer is registered when a launch is made)
             norm_launch, normed = self._normed_lhs(spec, lhs_t, gain, plan.rscale, register=collect is None)
             lhs = normed
+            # (the producing scan applied the gain and left the row sums: _plan_norm_folds)
+            rs_parts = self._rs_parts.get(self._norm_key(lhs_t, gain, plan.rscale))
         # (a merged launch packs its own concatenated weights)
         get_packed = self._pack(spec, [rhs_of[i] for i in used], in_dtype, unfold=gain is not None) \
             if collect is None else None
@@ -639,11 +644,13 @@ class DeviceProgram:
                 mask |= 1 << slot[i]
         inv_k, eps = plan.rscale if plan.rscale else (0.0, 0.0)
         sumsq = plan.rscale is not None
-        if normed is not None:   # the row scale is inside the normalised lhs
+        if normed is not None and rs_parts is None:   # the row scale is inside the normalised lhs
             mask, sumsq = 0, False
         rope = next(iter(rope_tables.values())) if rope_tables else None
         info = {"n_acc": len(used), "ops": [op for _, op, *_ in outs], "rscale": plan.rscale is not None,
                 "rope_fused": any(op == abi.EPI_ROPE for _, op, *_ in outs), "gain_on_activation": normed is not None}
+        if rs_parts is not None:
+            info["row_sums_from_producer"] = True
         fp8_kw: dict[str, Any] = {}
         if in_dtype == torch.float32 and collect is None:
             # small fp32 grids split K over workgroups through a workspace (0 bytes otherwise)
@@ -673,7 +680,7 @@ class DeviceProgram:
 
         def run() -> None:
             call = ops.GemmCall(T, N, K, len(used), lhs, get_packed(), epi, sumsq=sumsq,
-                                rscale_mask=mask, inv_k=inv_k, eps=eps, extras=extra_bufs, **fp8_kw)
+                                rscale_mask=mask, inv_k=inv_k, eps=eps, extras=extra_bufs, rs_parts=rs_parts, **fp8_kw)
             if rope is not None:
                 call.rope_cos, call.rope_sin, call.rope_period, call.rope_head_dim = rope[0], rope[1], rope[2], rope[3]
             ops.gemm(call, kernel=spec.name)
@@ -703,6 +710,57 @@ class DeviceProgram:
             return None
         return g0
 
+    @staticmethod
+    def _norm_key(lhs_t: str, gain: torch.Tensor, rscale) -> tuple:
+        """The normalised operand of ``lhs_t`` with this gain and row scale (shared by the
+        kernels that read it)."""
+        return (lhs_t, gain.data_ptr(), float(rscale[0]), float(rscale[1]))
+
+    def _plan_norm_folds(self, program: Program) -> dict[str, dict]:
+        """SSD scans whose output is read by exactly one GEMM, as its lhs, normalised with
+        an RMSNorm gain taken back out of that GEMM's weights (norm_gain='activation': the
+        gated norm before Mamba's out-projection). Such a scan stores y times the gain and
+        the sums of squares of y per token and 32 columns (th_ssd_chunked's y_gain and
+        rs_parts); the GEMM applies the row scale from those sums (th_gemm's rs_parts), and
+        the th_rmsnorm launch between them goes away. Only where the scan runs its MFMA
+        path with the vector epilogue (bf16 operands and output, no fp32 copy of the
+        output, which no other kernel and no program output reads). Returns
+        {scan kernel: {"gemm", "gain", "key", "tensor"}}."""
+        from .ssd import _gate_of
+
+        folds: dict[str, dict] = {}
+        if not self.fold_sources:
+            return folds
+        readers: dict[str, list] = {}
+        for k in program.kernels:
+            for a in k.args:
+                readers.setdefault(a.tensor, []).append((k, a))
+        for k in program.kernels:
+            if k.kind != "ssd_chunked" or len(k.outputs) != 1 or not _gate_of(k)[1]:
+                continue
+            t, at = k.outputs[0].tensor, k.attrs
+            H, P, N = at["heads"], at["head_dim"], at["state_dim"]
+            bf16 = all(program.tensors[k.arg(r).tensor].dtype == "bfloat16" for r in ("x", "b", "c", "dt"))
+            if (t in program.outputs or t in self._shadowed or program.tensors[t].dtype != "bfloat16" or not bf16
+                    or P not in (32, 64, 128) or N not in (32, 64, 128) or int(at.get("chunk", 64)) % 32
+                    or (H * P) % 128):
+                continue
+            rd = readers.get(t, [])
+            if len(rd) != 1 or rd[0][0].kind != "gemm" or rd[0][1].role != "lhs" or not rd[0][0].gemms:
+                continue
+            g = rd[0][0]
+            if g.name in self._merge_groups or g.name in self._merged_away or g.name in self._fp8_groups:
+                continue
+            plan = match_epilogue(g)
+            if not plan.fused or plan.rscale is None or any(o.rope is not None for o in plan.outs):
+                continue
+            used = sorted({i for o in plan.outs for i in (o.a, o.b) if i >= 0})
+            gain = self._unfold_gain(g, plan, used)
+            if gain is None or gain.numel() != H * P:
+                continue
+            folds[k.name] = {"gemm": g.name, "gain": gain, "key": self._norm_key(t, gain, plan.rscale), "tensor": t}
+        return folds
+
     def _normed_lhs(self, spec: KernelSpec, lhs_t: str, gain: torch.Tensor, rscale,
                     register: bool = True) -> tuple[Launch | None, torch.Tensor]:
         """bf16 ``x * r * g`` of this lhs (x read from its fp32 shadow when it has one),
@@ -711,7 +769,7 @@ class DeviceProgram:
         ``register=False``: a probe (collect mode) whose launch may never be emitted,
         so later kernels must not take the buffer as already written."""
         inv_k, eps = rscale
-        key = (lhs_t, gain.data_ptr(), float(inv_k), float(eps))
+        key = self._norm_key(lhs_t, gain, rscale)
         if key in self._normed:
             return None, self._normed[key]
         x = self.operand(lhs_t)

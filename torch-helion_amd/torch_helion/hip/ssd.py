@@ -74,11 +74,22 @@ def lower_ssd(dp, spec: KernelSpec):
         out = dp.buffers[out_name]
         gate = dp.operand(spec.arg(gate_arg).tensor) if gate_arg else None
         out32 = dp.shadow.get(out_name)
+        info = {"gate": gate_arg is not None, "chunk": kw["chunk"]}
+        fold = dp._norm_folds.get(spec.name)
+        if fold is not None:
+            # The only reader normalises this output with a gain: store y times the gain
+            # and the per-32-column sums of squares of y; that GEMM takes this buffer as
+            # its normalised lhs and applies the row scale from the sums.
+            kw["y_gain"] = fold["gain"].float().reshape(-1).to(dp.device).contiguous()
+            kw["rs_parts"] = dp._device_buffer((bs * s, h * p // 32), torch.float32, dp._last.get(out_name, dp._cur))
+            dp._normed[fold["key"]] = out
+            dp._rs_parts[fold["key"]] = kw["rs_parts"]
+            info["norm_gain_for"] = fold["gemm"]
 
         def run() -> None:
             ops.ssd_chunked(x=x, b=bm, c=cm, dt=dt, out=out, workspace=ws, gate=gate, out32=out32, kernel=spec.name, **kw)
 
-        return [Launch(spec.name, spec.kind, run, "th_ssd_chunked", {"gate": gate_arg is not None, "chunk": kw["chunk"]})]
+        return [Launch(spec.name, spec.kind, run, "th_ssd_chunked", info)]
     acc = dp._workspace(bs * s * h * p).view(bs * s, h * p)
 
     def run_acc() -> None:
