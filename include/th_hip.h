@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define TH_ABI_VERSION 6
+#define TH_ABI_VERSION 7
 
 typedef enum th_status {
   TH_OK = 0,
@@ -130,15 +130,26 @@ typedef struct th_gemm_desc {
                              optional for TH_F32 (small grids then split K over workgroups through it) */
   int64_t workspace_bytes;
   const float* lhs_gain;  /* optional [K] fp32 per-column gain of lhs (TH_F8E4M3 only; 16-byte aligned) */
-  const float* rs_parts;  /* optional [M, n_rs_parts] fp32, row stride ld_rs_parts (TH_BF16, with sumsq):
-                             each row's sum of squares is the in-order sum of these parts instead of
-                             sum_k lhs^2, for an lhs whose producer applied an RMSNorm gain and kept
-                             the sums of the unscaled values (th_ssd_chunked's y_gain, rs_parts).
+  const float* rs_parts;  /* optional [M, n_rs_parts] fp32, row stride ld_rs_parts (TH_BF16, or TH_F8E4M3
+                             without lhs_gain; with sumsq): each row's sum of squares is the in-order
+                             sum of these parts instead of sum_k lhs^2, for an lhs whose producer
+                             applied an RMSNorm gain and kept the sums of the unscaled values
+                             (th_ssd_chunked's y_gain, rs_parts; th_gemm's gain_out, ss_parts_out).
                              n_rs_parts and ld_rs_parts multiples of 4, 16-byte aligned. No
                              counterpart in the reference (its RMSNorm is one kernel). */
   int64_t ld_rs_parts;
   int32_t n_rs_parts;
   int32_t pad3_;
+  const float* gain_out;  /* optional [N] fp32, 16-byte aligned (TH_F8E4M3 weights): output gain_out_index,
+                             a bf16 output over all N columns, is stored as bf16(bf16(v) * gain_out[n])
+                             instead of v, and ss_parts_out receives each row's sum of bf16(v)^2 in
+                             parts of 256 columns: the next GEMM's lhs with its RMSNorm gain applied,
+                             and the sums that GEMM's rs_parts takes. N a multiple of 1024. No
+                             counterpart in the reference (its RMSNorm is one kernel). */
+  float* ss_parts_out;    /* with gain_out: [M, N / 256] fp32, row stride ld_ss_parts_out, 16-byte aligned */
+  int64_t ld_ss_parts_out;
+  int32_t gain_out_index;
+  int32_t pad4_;
 } th_gemm_desc;
 
 /* Per-accumulator column tile th_gemm uses for (N, n_acc, in_dtype) when an

@@ -276,17 +276,22 @@ def _spec_quantised(sd: dict[str, torch.Tensor]) -> dict[str, torch.Tensor]:
     return out
 
 
-@pytest.mark.parametrize("which", ["small", "c5"])
+@pytest.mark.parametrize("which", ["small", "medium", "medium_unfolded", "c5"])
 def test_decode_step_fp8_vs_oracle(gpu, which):
     """Decode step with e4m3 weights: the block output and the cache entries it writes at ``pos``
     against the oracle's decode step in fp32 on the BASELINE's quantisation (plain W quantised
-    per output channel, gains on the activations), built by the test itself."""
+    per output channel, gains on the activations), built by the test itself. Hidden sizes that
+    are multiples of 1024 (medium, C5) apply the post-attention gain in the o-projection's
+    finishing pass; medium_unfolded runs the same block with its own pass for it."""
     from oracle.llama import decode_step
     from targets.llama_block import LlamaBlockConfig, config_c5
     from torch_helion.hip.decode import DecodeBlock
 
     if which == "c5":
         cfg, pos = config_c5(), 4096
+    elif which.startswith("medium"):
+        cfg, pos = LlamaBlockConfig(batch=4, seq=80, hidden=1024, heads=8, kv_heads=2, intermediate=2048, causal=True,
+                                    dtype=torch.bfloat16, rope_theta=500000.0), 71
     else:
         cfg, pos = LlamaBlockConfig(batch=4, seq=80, hidden=256, heads=4, kv_heads=2, intermediate=512, causal=True,
                                     dtype=torch.bfloat16, rope_theta=500000.0), 77
@@ -295,7 +300,9 @@ def test_decode_step_fp8_vs_oracle(gpu, which):
     w_spec = _spec_quantised(sd)
     assert w_spec["input_norm.weight"].std() > 0.01      # the gains are not all one: the test sees where they go
     blk = DecodeBlock(sd, hidden=cfg.hidden, heads=cfg.heads, kv_heads=cfg.n_kv, intermediate=cfg.intermediate,
-                      eps=cfg.eps, rope_theta=cfg.rope_theta, batch=cfg.batch, max_len=cfg.seq, device=gpu)
+                      eps=cfg.eps, rope_theta=cfg.rope_theta, batch=cfg.batch, max_len=cfg.seq, device=gpu,
+                      fold_gain=which != "medium_unfolded")
+    assert blk.fold_gain == (which in ("medium", "c5"))
     eff = blk.effective_weights()
     for k, v in w_spec.items():
         assert torch.equal(eff[k], v), k                  # the product quantises exactly as specified

@@ -398,6 +398,82 @@ def test_gemm_fp8_lhs_gain(gpu, M, N, K, n_acc):
     assert _rel(ss, (xf * xf).sum(-1)) < 1e-5
 
 
+@pytest.mark.parametrize("M,N,K", [(64, 4096, 4096), (37, 2048, 1024), (32, 24576, 256)])
+def test_gemm_fp8_gain_out_and_rs_parts(gpu, M, N, K):
+    """The next RMSNorm's gain applied by an e4m3 GEMM's finishing pass (gain_out: the decode
+    step's o-projection feeding gate/up) and consumed through rs_parts. Producer: the gained
+    output is bit-for-bit bf16(bf16(v) * g) of the plain call's output, the fp32 output is
+    unchanged, and each 256-column part is that slice's sum of bf16(v)^2. Consumer: a SwiGLU
+    GEMM on the gained rows with rs_parts matches the lhs_gain path on the plain rows. Covers
+    8 and 2 splits and one split (which gain_out sends through the reduce pass), and consumers
+    finishing in the main kernel and in the reduce pass."""
+    from torch_helion.hip import abi, ops
+
+    announce(f"gemm fp8 gain_out + rs_parts M={M} N={N} K={K}")
+    f8 = torch.float8_e4m3fn
+    g = torch.Generator().manual_seed(M + 3 * N + K)
+    x = torch.randn(M, K, generator=g).bfloat16().to(gpu)
+    res = torch.randn(M, N, generator=g).bfloat16().to(gpu)
+    gain = (torch.rand(N, generator=g) + 0.5).to(gpu)
+    q, s = _quant_e4m3(torch.randn(K, N, generator=g) * 0.02)
+    packed = ops.pack_rhs([q.to(gpu)], f8)
+    scale = s[None, :].to(gpu).contiguous()
+    ws = torch.empty(ops.gemm_workspace_bytes(M, N, K, 1, f8), dtype=torch.uint8, device=gpu)
+
+    def produce(gain_out):
+        o16 = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=gpu)
+        o32 = torch.full((M, N), float("nan"), device=gpu)
+        ops.gemm(ops.GemmCall(M, N, K, 1, x, packed, [ops.EpiSpec(abi.EPI_ADD, o16, e=0),
+                                                      ops.EpiSpec(abi.EPI_ADD, o32, e=0)],
+                              extras=[res], in_dtype=f8, rhs_scale=scale, workspace=ws, gain_out=gain_out))
+        torch.cuda.synchronize()
+        return o16, o32
+
+    plain16, plain32 = produce(None)
+    parts = torch.full((M, N // 256), float("nan"), device=gpu)
+    gained16, gained32 = produce((0, gain, parts))
+    ref32 = x.float().cpu() @ (q.float() * s[None, :]) + res.float().cpu()
+    assert _rel(plain32, ref32) < 1e-4
+    assert torch.equal(gained32, plain32)
+    assert torch.equal(gained16, (plain16.float() * gain).bfloat16())
+    sq = plain16.double() ** 2
+    want = sq.view(M, N // 256, 256).sum(-1)
+    assert ((parts.double() - want).abs() / want).max().item() < 1e-5
+
+    # consumer: gate/up on the gained rows with the producer's row sums (the C5 width runs as one
+    # split finished in the main kernel; 512 columns through the reduce pass)
+    F = 14336 if N == 4096 else 512
+    qs = [_quant_e4m3(torch.randn(N, F, generator=g) * 0.02) for _ in range(2)]
+    pk2 = ops.pack_rhs([qq.to(gpu) for qq, _ in qs], f8)
+    sc2 = torch.stack([ss for _, ss in qs]).to(gpu).contiguous()
+    ws2 = torch.empty(ops.gemm_workspace_bytes(M, F, N, 2, f8), dtype=torch.uint8, device=gpu)
+    norm = dict(sumsq=True, rscale_mask=0b11, inv_k=1.0 / N, eps=1e-5)
+    outs = []
+    for lhs, kw in ((plain16, dict(lhs_gain=gain)), (gained16, dict(rs_parts=parts))):
+        o = torch.full((M, F), float("nan"), device=gpu)
+        ss = torch.full((M,), float("nan"), device=gpu)
+        ops.gemm(ops.GemmCall(M, F, N, 2, lhs, pk2, [ops.EpiSpec(abi.EPI_SWIGLU, o, a=0, b=1)], in_dtype=f8,
+                              rhs_scale=sc2, workspace=ws2, sumsq_out=ss, **norm, **kw))
+        torch.cuda.synchronize()
+        outs.append((o, ss))
+    (o_a, ss_a), (o_b, ss_b) = outs
+    assert _rel(ss_b, ss_a) < 1e-6, _rel(ss_b, ss_a)
+    assert _rel(o_b, o_a) < 1e-5, _rel(o_b, o_a)
+
+
+def test_gemm_gain_out_rejected_for_bf16(gpu):
+    """gain_out exists for e4m3 weights only: a bf16 GEMM asked for it fails loudly."""
+    from torch_helion.hip import abi, ops
+
+    x = torch.randn(64, 256, device=gpu).bfloat16()
+    packed = ops.pack_rhs([torch.randn(256, 1024, device=gpu).bfloat16()], torch.bfloat16)
+    out = torch.empty(64, 1024, dtype=torch.bfloat16, device=gpu)
+    parts = torch.empty(64, 4, device=gpu)
+    with pytest.raises(abi.HipBackendError, match="gain_out"):
+        ops.gemm(ops.GemmCall(64, 1024, 256, 1, x, packed, [ops.EpiSpec(abi.EPI_ACC, out, a=0)],
+                              gain_out=(0, torch.ones(1024, device=gpu), parts)))
+
+
 def test_gemm_lhs_gain_rejected_for_bf16(gpu):
     """lhs_gain exists for e4m3 weights only: a bf16 GEMM asked for it fails loudly."""
     from torch_helion.hip import abi, ops

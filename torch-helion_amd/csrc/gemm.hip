@@ -1806,11 +1806,26 @@ extern "C" int th_gemm(const th_gemm_desc* d, void* stream) {
   }
   TH_CHECK_ARG(d->lhs_gain == nullptr || aligned(d->lhs_gain, 16), "th_gemm: lhs_gain must be 16-byte aligned");
   if (d->rs_parts != nullptr) {
-    TH_CHECK_ARG(d->in_dtype == TH_BF16, "th_gemm: rs_parts is implemented for TH_BF16 only");
+    TH_CHECK_ARG(d->in_dtype == TH_BF16 || (fp8 && d->lhs_gain == nullptr),
+                 "th_gemm: rs_parts is implemented for TH_BF16, and TH_F8E4M3 without lhs_gain");
     TH_CHECK_ARG(d->sumsq, "th_gemm: rs_parts set without sumsq");
     TH_CHECK_ARG(d->n_rs_parts > 0 && d->n_rs_parts % 4 == 0 && d->ld_rs_parts >= d->n_rs_parts &&
                      d->ld_rs_parts % 4 == 0 && aligned(d->rs_parts, 16),
                  "th_gemm: rs_parts needs a positive multiple of 4 parts per row, 16-byte aligned rows");
+  }
+  if (d->gain_out != nullptr) {
+    if (!fp8) {
+      set_error("th_gemm: gain_out is implemented for TH_F8E4M3 weights only");
+      return TH_ERR_UNSUPPORTED;
+    }
+    TH_CHECK_ARG(d->gain_out_index >= 0 && d->gain_out_index < d->n_out, "th_gemm: gain_out_index out of range");
+    const th_epi_out& go = d->out[d->gain_out_index];
+    TH_CHECK_ARG(go.dtype == TH_BF16 && go.col_begin == 0 && (go.col_end == 0 || go.col_end == d->N),
+                 "th_gemm: the gain_out output must be bf16 over all N columns");
+    TH_CHECK_ARG(d->N % 1024 == 0, "th_gemm: gain_out needs N a multiple of 1024 (N=%lld)", (long long)d->N);
+    TH_CHECK_ARG(d->ss_parts_out != nullptr && d->ld_ss_parts_out >= d->N / 256 && d->ld_ss_parts_out % 4 == 0 &&
+                     aligned(d->ss_parts_out, 16) && aligned(d->gain_out, 16),
+                 "th_gemm: gain_out needs ss_parts_out [M, N/256] fp32 (16-byte aligned rows) and an aligned gain");
   }
   int bn = choose_bn(d->N, d->n_acc, d->in_dtype);
   // One accumulator over 1024 <= N < 2048 columns: 256 x 256 tiles, one per CU
@@ -1909,6 +1924,10 @@ extern "C" int th_gemm(const th_gemm_desc* d, void* stream) {
   k.rs_parts = d->rs_parts;
   k.ld_rs_parts = d->ld_rs_parts;
   k.n_rs_parts = d->n_rs_parts;
+  k.gain_out = d->gain_out;
+  k.ss_parts_out = d->ss_parts_out;
+  k.ld_ss_parts_out = d->ld_ss_parts_out;
+  k.gain_index = d->gain_out_index;
   if (!device_ready()) {
     set_error("th_gemm: th_init was not called for the current device");
     return TH_ERR_NOT_INIT;

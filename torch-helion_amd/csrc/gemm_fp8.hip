@@ -268,18 +268,20 @@ __device__ __forceinline__ void fp8_emit(const Fp8K& p, int64_t m, int64_t n, fl
 
 // Every output op of row m, columns n4 .. n4+3 (n4 a multiple of 4, the 4
 // columns inside one packed tile and one RoPE half-head, column windows on
-// multiples of 8); sum4(i, nn) is accumulator i at columns nn .. nn+3,
-// scaled; n_acc is 1 or 2. Two phases: every load (accumulators, the RoPE partner, extras,
-// RoPE tables) is issued before the first store, so a thread waits for one
-// round of memory latency, not one per output; then one 4-wide store per
-// output.
-template <class Sum4>
-__device__ __forceinline__ void fp8_emit4(const Fp8K& p, int64_t m, int64_t n4, float rr, Sum4 sum4) {
+// multiples of 8); sum4(i, nn, rot) is accumulator i at columns nn .. nn+3,
+// scaled (rot: nn is the RoPE partner's columns, not n4); n_acc is 1 or 2;
+// rrf() the row's RMS scale; gather() issues the loads sum4 and rrf fold, if
+// any. Two phases: every load (gather's, then the RoPE tables and the
+// extras) goes out before the stores, so a thread waits for about one round
+// of memory latency per distinct extra, not one per output and split; then
+// one 4-wide store per output. With gain_out, output gain_index is stored as
+// bf16(bf16(v) * gain_out[n]); the return value is the sum of its four
+// bf16(v)^2 (0 without gain_out).
+template <class Sum4, class RowScale, class Gather>
+__device__ __forceinline__ float fp8_emit4(const Fp8K& p, int64_t m, int64_t n4, RowScale rrf, Sum4 sum4,
+                                           Gather gather) {
   const GemmK& g = p.k;
   const int valid = (int)min((int64_t)4, p.N - n4);
-  // gather (the shared-activation kernel's packings have one or two accumulators)
-  const float4 c0 = sum4(0, n4);
-  const float4 c1 = g.n_acc > 1 ? sum4(1, n4) : c0;
   // the rotation partner of each accumulator some ROPE output here reads
   bool rope_acc[2] = {false, false};
   bool tab = false;
@@ -292,26 +294,48 @@ __device__ __forceinline__ void fp8_emit4(const Fp8K& p, int64_t m, int64_t n4, 
   const int within = g.hd > 0 ? (int)n4 % g.hd : 0;
   const int half = g.hd >> 1;
   const int64_t pn = within < half ? n4 + half : n4 - half;
+  const int toff = tab ? ((int)m % g.period) * g.hd + within : 0;
+  gather();
   const float4 zero4 = make_float4(0.f, 0.f, 0.f, 0.f);
-  const float4 rot0 = rope_acc[0] ? sum4(0, pn) : zero4;
-  const float4 rot1 = rope_acc[1] ? sum4(1, pn) : zero4;
   float4 cs = zero4, sn = zero4;
   if (tab) {
-    const int toff = ((int)m % g.period) * g.hd + within;
     cs = make_float4(g.rcos[toff], g.rcos[toff + 1], g.rcos[toff + 2], g.rcos[toff + 3]);
     sn = make_float4(g.rsin[toff], g.rsin[toff + 1], g.rsin[toff + 2], g.rsin[toff + 3]);
   }
+  const float4 gq = g.gain_out != nullptr ? *(const float4*)(g.gain_out + n4) : zero4;
+  // extras (after gather's loads, so the first one's conversion waits for
+  // all of them at once; an extra two outputs share is loaded once)
   float4 xe[TH_MAX_OUT];
 #pragma unroll
   for (int o = 0; o < TH_MAX_OUT; ++o) {
-    xe[o] = make_float4(0.f, 0.f, 0.f, 0.f);
+    xe[o] = zero4;
     if (o >= g.n_out) continue;
     const EpiOutK& eo = g.out[o];
     const bool uses_e = eo.op == TH_EPI_ADD || eo.op == TH_EPI_SOFTPLUS_ADD || eo.op == TH_EPI_MUL;
-    if (uses_e && n4 >= eo.cb && n4 < eo.ce)
+    if (!uses_e || n4 < eo.cb || n4 >= eo.ce) continue;
+    int same = -1;
+#pragma unroll
+    for (int o2 = 0; o2 < o; ++o2) {
+      const EpiOutK& e2 = g.out[o2];
+      const bool u2 = e2.op == TH_EPI_ADD || e2.op == TH_EPI_SOFTPLUS_ADD || e2.op == TH_EPI_MUL;
+      if (same < 0 && u2 && e2.e == eo.e && e2.cb == eo.cb && e2.ce == eo.ce) same = o2;
+    }
+    if (same >= 0) {
+#pragma unroll
+      for (int o2 = 0; o2 < o; ++o2)
+        if (o2 == same) xe[o] = xe[o2];
+    } else {
       xe[o] = load4(g.extra[eo.e], m * g.ld_extra[eo.e] + (n4 - eo.cb), g.extra_dtype[eo.e], g.extra_vec[eo.e] != 0,
                     (int)min((int64_t)valid, eo.ce - n4));
+    }
   }
+  float ssg = 0.f;
+  // the sums (the shared-activation kernel's packings have one or two accumulators)
+  const float4 c0 = sum4(0, n4, false);
+  const float4 c1 = g.n_acc > 1 ? sum4(1, n4, false) : c0;
+  const float4 rot0 = rope_acc[0] ? sum4(0, pn, true) : zero4;
+  const float4 rot1 = rope_acc[1] ? sum4(1, pn, true) : zero4;
+  const float rr = rrf();
   auto sel = [&](int i) { return i == 1 ? c1 : c0; };
   auto scl = [](float4 v, float f) { return make_float4(v.x * f, v.y * f, v.z * f, v.w * f); };
   // emit
@@ -360,8 +384,16 @@ __device__ __forceinline__ void fp8_emit4(const Fp8K& p, int64_t m, int64_t n4, 
         break;
       }
     }
+    if (g.gain_out != nullptr && o == g.gain_index) {
+      // the value the output would hold, then times the next RMSNorm's gain
+      auto rb = [](float f) { return __uint_as_float((uint32_t)f32_to_bf16(f) << 16); };
+      const float4 r = make_float4(rb(v.x), rb(v.y), rb(v.z), rb(v.w));
+      ssg = ((r.x * r.x + r.y * r.y) + r.z * r.z) + r.w * r.w;
+      v = make_float4(r.x * gq.x, r.y * gq.y, r.z * gq.z, r.w * gq.w);
+    }
     store4(eo.ptr, m * eo.ld + (n4 - eo.cb), eo.dtype, eo.vec != 0, (int)min((int64_t)valid, eo.ce - n4), v);
   }
+  return ssg;
 }
 
 // The outputs of packed tile t (output columns t bn .. +bn of every
@@ -379,11 +411,11 @@ __device__ __forceinline__ void fp8_tile_out(const Fp8K& p, int t, int tid, int 
     if (n4 >= p.N) continue;
     const float* row = tl + m * ld - n0;
     const float* scr = sc - n0;
-    fp8_emit4(p, m, n4, rrs[m], [&](int i, int64_t nn) {
+    fp8_emit4(p, m, n4, [&] { return rrs[m]; }, [&](int i, int64_t nn, bool) {
       const float4 v = *(const float4*)(row + i * bn + nn);
       const float4 s4 = *(const float4*)(scr + i * bn + nn);
       return make_float4(v.x * s4.x, v.y * s4.y, v.z * s4.z, v.w * s4.w);
-    });
+    }, [] {});
   }
 }
 
@@ -438,6 +470,19 @@ __global__ void __launch_bounds__(512) gemm_fp8_lds_kernel(Fp8K p) {
   // row sums of squares (unless handed over): every workgroup when it
   // finishes its tile itself, else the first column block of each split
   const bool do_ss = p.k.sumsq && !p.ss_pre && (p.fused || blockIdx.x == 0);
+  // row sums handed over as the lhs producer's parts (up to 16): loaded before
+  // the first slices, added up (in row_sumsq's order) once those are issued
+  const bool pre_rs = p.k.sumsq && p.ss_pre == 2 && p.fused && p.k.n_rs_parts <= 16 && tid % PARTS == 0 &&
+                      tid / PARTS < p.M;
+  float4 rsp[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) rsp[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (pre_rs) {
+    const float4* q = (const float4*)(p.k.rs_parts + (int64_t)(tid / PARTS) * p.k.ld_rs_parts);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (i < (p.k.n_rs_parts >> 2)) rsp[i] = q[i];
+  }
 
   // activation load q of this wave fills slice rows RPI (ALD wave + q) + lane / LPR,
   // slot lane % LPR; rows past M re-read row M - 1 (their sums are dropped)
@@ -542,6 +587,18 @@ __global__ void __launch_bounds__(512) gemm_fp8_lds_kernel(Fp8K p) {
   };
 
   unroll_seq(std::make_integer_sequence<int, P>(), [&](auto s) { issue(min((int)s, nsl - 1), s); });
+  float rs_sum = 0.f;
+  if (pre_rs) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (i < (p.k.n_rs_parts >> 2)) {
+        rs_sum += rsp[i].x;
+        rs_sum += rsp[i].y;
+        rs_sum += rsp[i].z;
+        rs_sum += rsp[i].w;
+      }
+    }
+  }
   // whole trips of NBUF steps (the last one padded): one in-flight pattern at every wait
   for (int j = 0; j < nsl; j += NBUF)
     unroll_seq(std::make_integer_sequence<int, NBUF>(), [&](auto s) { step(j + (int)s, s); });
@@ -625,7 +682,14 @@ __global__ void __launch_bounds__(512) gemm_fp8_lds_kernel(Fp8K p) {
     const int row = tid / PARTS;
     float rr = 1.f;
     if (p.k.sumsq) {
-      const float s = p.ss_pre ? p.sumsq_part[row] : ss;
+      float s = ss;
+      if (pre_rs) {
+        s = rs_sum;
+      } else if (p.ss_pre == 2) {
+        s = row_sumsq(p.k, row, 0.f);
+      } else if (p.ss_pre) {
+        s = p.sumsq_part[row];
+      }
       rr = rsqrtf(s * p.k.inv_k + p.k.eps);
       if (p.k.sumsq_out && blockIdx.x == 0) p.k.sumsq_out[row] = s;
     }
@@ -707,7 +771,10 @@ __global__ void __launch_bounds__(256) gemm_fp8_reduce_kernel(Fp8K p) {
   float rr = 1.f;
   if (g.sumsq) {
     float ss = 0.f;
-    for (int sp = 0; sp < p.splits; ++sp) ss += p.sumsq_part[(int64_t)sp * p.M + m];
+    if (p.ss_pre == 2)
+      ss = row_sumsq(g, m, 0.f);
+    else
+      for (int sp = 0; sp < p.splits; ++sp) ss += p.sumsq_part[(int64_t)sp * p.M + m];
     rr = rsqrtf(ss * g.inv_k + g.eps);
     if (g.sumsq_out && n == 0) g.sumsq_out[m] = ss;
   }
@@ -715,39 +782,127 @@ __global__ void __launch_bounds__(256) gemm_fp8_reduce_kernel(Fp8K p) {
 }
 
 // Second pass after a multi-split launch of the shared-activation kernel:
-// one thread per (row m, 4 consecutive output columns); float4 partial loads
-// (all splits of a column group in flight at once), sums in split order.
-// Requires N % 4 == 0 and a power-of-two bn (so 4 columns share a tile).
+// one thread per (row m, 4 consecutive output columns), float4 partial loads,
+// sums in split order, 4-wide stores. S > 0: exactly S splits, every partial
+// the thread adds (its columns, the RoPE partner's, the row's sums of squares)
+// loaded before the first is added, with the extras and RoPE tables: one
+// memory round trip. S = 0: any split count, a loop per sum. Requires
+// N % 4 == 0 and a power-of-two bn (so 4 columns share a tile). With
+// gain_out (N a multiple of 1024, so every wave is whole and inside one row),
+// each wave sums its 256 columns' bf16(v)^2 into ss_parts_out.
+template <int S>
 __global__ void __launch_bounds__(256) gemm_fp8_reduce4_kernel(Fp8K p) {
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
   const int64_t nq = p.N >> 2;
   if (idx >= p.M * nq) return;
   const int64_t m = idx / nq, n4 = (idx - m * nq) << 2;
   const GemmK& g = p.k;
-  const int S = p.splits, na = g.n_acc;
+  const int na = g.n_acc;
   const int sh = __builtin_ctz((unsigned)p.bn);
   const int64_t plane = p.M * p.Npk;
-  // accumulator i at output columns nn .. nn+3 (nn a multiple of 4), scaled
-  auto sum4 = [&](int i, int64_t nn) {
+  auto part_ptr = [&](int i, int64_t nn) {
     const int64_t t = nn >> sh, j = nn & (p.bn - 1);
-    const float* q = p.part + m * p.Npk + ((t * na + i) << sh) + j;
-    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll 8
-    for (int sp = 0; sp < S; ++sp) {
-      const float4 v = *(const float4*)(q + sp * plane);
-      acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
-    }
-    const float4 sc = *(const float4*)(p.scale + (int64_t)i * p.N + nn);
-    return make_float4(acc.x * sc.x, acc.y * sc.y, acc.z * sc.z, acc.w * sc.w);
+    return p.part + m * p.Npk + ((t * na + i) << sh) + j;
   };
-  float rr = 1.f;
-  if (g.sumsq) {
-    float ss = 0.f;
-    for (int sp = 0; sp < S; ++sp) ss += p.sumsq_part[(int64_t)sp * p.M + m];
-    rr = rsqrtf(ss * g.inv_k + g.eps);
+  auto row_scale = [&](float ss) {
     if (g.sumsq_out && n4 == 0) g.sumsq_out[m] = ss;
+    return rsqrtf(ss * g.inv_k + g.eps);
+  };
+  // the wave's part of the gain output's row sum of squares (lane order fixed)
+  auto store_ss_part = [&](float v) {
+    if (g.gain_out == nullptr) return;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) v += __shfl_xor(v, off);
+    if ((threadIdx.x & 63) == 0) g.ss_parts_out[m * g.ld_ss_parts_out + (n4 >> 8)] = v;
+  };
+  if constexpr (S == 0) {
+    const int ns = p.splits;
+    // accumulator i at output columns nn .. nn+3 (nn a multiple of 4), scaled
+    auto sum4 = [&](int i, int64_t nn, bool) {
+      const float* q = part_ptr(i, nn);
+      float4 acc = *(const float4*)q;
+#pragma unroll 8
+      for (int sp = 1; sp < ns; ++sp) {
+        const float4 v = *(const float4*)(q + sp * plane);
+        acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
+      }
+      const float4 sc = *(const float4*)(p.scale + (int64_t)i * p.N + nn);
+      return make_float4(acc.x * sc.x, acc.y * sc.y, acc.z * sc.z, acc.w * sc.w);
+    };
+    float rr = 1.f;
+    if (g.sumsq) {
+      float ss = 0.f;
+      if (p.ss_pre == 2) {
+        ss = row_sumsq(g, m, 0.f);
+      } else {
+        ss = p.sumsq_part[m];
+        for (int sp = 1; sp < ns; ++sp) ss += p.sumsq_part[(int64_t)sp * p.M + m];
+      }
+      rr = row_scale(ss);
+    }
+    store_ss_part(fp8_emit4(p, m, n4, [&] { return rr; }, sum4, [] {}));
+  } else {
+    // the accumulators and RoPE partners this thread's outputs read
+    bool rope_acc[2] = {false, false};
+    for (int o = 0; o < g.n_out; ++o) {
+      const EpiOutK& eo = g.out[o];
+      if (n4 >= eo.cb && n4 < eo.ce && eo.op == TH_EPI_ROPE) rope_acc[eo.a & 1] = true;
+    }
+    const int within = g.hd > 0 ? (int)n4 % g.hd : 0;
+    const int64_t pn = within < (g.hd >> 1) ? n4 + (g.hd >> 1) : n4 - (g.hd >> 1);
+    // (zero where not loaded: an undefined value there would let the compiler
+    // move the first additions up between the loads, each with its own wait)
+    float4 pa[2][S], pr[2][S], sa[2], sr[2];
+    float ps[S];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) sa[i] = sr[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int sp = 0; sp < S; ++sp) {
+      pa[0][sp] = pa[1][sp] = pr[0][sp] = pr[1][sp] = make_float4(0.f, 0.f, 0.f, 0.f);
+      ps[sp] = 0.f;
+    }
+    auto gather = [&] {
+      if (g.sumsq && p.ss_pre != 2) {
+#pragma unroll
+        for (int sp = 0; sp < S; ++sp) ps[sp] = p.sumsq_part[(int64_t)sp * p.M + m];
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        if (i < na) {
+          const float* q = part_ptr(i, n4);
+#pragma unroll
+          for (int sp = 0; sp < S; ++sp) pa[i][sp] = *(const float4*)(q + sp * plane);
+          sa[i] = *(const float4*)(p.scale + (int64_t)i * p.N + n4);
+        }
+        if (i < na && rope_acc[i]) {
+          const float* q = part_ptr(i, pn);
+#pragma unroll
+          for (int sp = 0; sp < S; ++sp) pr[i][sp] = *(const float4*)(q + sp * plane);
+          sr[i] = *(const float4*)(p.scale + (int64_t)i * p.N + pn);
+        }
+      }
+    };
+    // the same sums, in the same order, as the S = 0 form
+    auto sum4 = [&](int i, int64_t, bool rot) {
+      float4 acc = rot ? pr[i][0] : pa[i][0];
+#pragma unroll
+      for (int sp = 1; sp < S; ++sp) {
+        const float4 v = rot ? pr[i][sp] : pa[i][sp];
+        acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
+      }
+      const float4 sc = rot ? sr[i] : sa[i];
+      return make_float4(acc.x * sc.x, acc.y * sc.y, acc.z * sc.z, acc.w * sc.w);
+    };
+    auto rrf = [&] {
+      if (!g.sumsq) return 1.f;
+      if (p.ss_pre == 2) return row_scale(row_sumsq(g, m, 0.f));
+      float ss = ps[0];
+#pragma unroll
+      for (int sp = 1; sp < S; ++sp) ss += ps[sp];
+      return row_scale(ss);
+    };
+    store_ss_part(fp8_emit4(p, m, n4, rrf, sum4, gather));
   }
-  fp8_emit4(p, m, n4, rr, sum4);
 }
 
 // Split count: about one workgroup per CU, each wave at least 256 of K.
@@ -813,6 +968,18 @@ int launch_gemm_fp8(const GemmK& k, int64_t Npk, const float* scale, float* ws, 
                (long long)need, (long long)ws_bytes);
   p.part = ws;
   p.sumsq_part = k.sumsq ? ws + (int64_t)p.splits * k.M * Npk : nullptr;
+  if (k.rs_parts != nullptr) p.ss_pre = 2;  // the row sums come from the lhs's producer
+  // 4-column output groups: inside one tile and one RoPE half-head
+  bool vec = k.N % 4 == 0 && (k.bn & (k.bn - 1)) == 0;
+  for (int o = 0; o < k.n_out; ++o) {
+    if (k.out[o].op == TH_EPI_ROPE && k.hd % 8 != 0) vec = false;
+    if (k.out[o].op == TH_EPI_ROPE_PAIR && k.hd % 4 != 0) vec = false;
+  }
+  if (k.gain_out != nullptr && !(lds && vec)) {
+    set_error("th_gemm: gain_out needs the shared-activation e4m3 kernel with 4-column outputs "
+              "(K a multiple of 128, 128-column packed tiles)");
+    return TH_ERR_UNSUPPORTED;
+  }
   if (lds) {
     TH_CHECK_ARG(k.lda < (1 << 24), "th_gemm: fp8 lhs row stride must be under 2^24 elements");
     if (k.gain) {
@@ -828,14 +995,9 @@ int launch_gemm_fp8(const GemmK& k, int64_t Npk, const float* scale, float* ws, 
       p.lda = k.K;
       p.ss_pre = 1;
     }
-    // 4-column output groups: inside one tile and one RoPE half-head
-    bool vec = k.N % 4 == 0 && (k.bn & (k.bn - 1)) == 0;
-    for (int o = 0; o < k.n_out; ++o) {
-      if (k.out[o].op == TH_EPI_ROPE && k.hd % 8 != 0) vec = false;
-      if (k.out[o].op == TH_EPI_ROPE_PAIR && k.hd % 4 != 0) vec = false;
-    }
     // one split finishes in the main kernel when RoPE partners stay in a tile
-    bool local = p.splits == 1 && vec;
+    // (and no output's row sums are taken: those need whole waves per row)
+    bool local = p.splits == 1 && vec && k.gain_out == nullptr;
     for (int o = 0; o < k.n_out; ++o)
       if (k.out[o].op == TH_EPI_ROPE && k.bn % k.hd != 0) local = false;
     p.fused = local ? 1 : 0;
@@ -848,8 +1010,19 @@ int launch_gemm_fp8(const GemmK& k, int64_t Npk, const float* scale, float* ws, 
       hipLaunchKernelGGL((gemm_fp8_lds_kernel<4, 1, 128>), g1, dim3(512), 0, stream, p);
     TH_CHECK_LAUNCH();
     if (!p.fused) {
-      if (vec)
-        hipLaunchKernelGGL(gemm_fp8_reduce4_kernel, dim3((unsigned)cdiv(k.M * (k.N / 4), 256)), dim3(256), 0, stream, p);
+      if (vec) {
+        const dim3 gr((unsigned)cdiv(k.M * (k.N / 4), 256));
+        switch (p.splits) {
+#define TH_FP8_RED4(S_) \
+  case S_:              \
+    hipLaunchKernelGGL(gemm_fp8_reduce4_kernel<S_>, gr, dim3(256), 0, stream, p); \
+    break;
+          TH_FP8_RED4(2) TH_FP8_RED4(3) TH_FP8_RED4(4) TH_FP8_RED4(5) TH_FP8_RED4(6) TH_FP8_RED4(7) TH_FP8_RED4(8)
+#undef TH_FP8_RED4
+          default:
+            hipLaunchKernelGGL(gemm_fp8_reduce4_kernel<0>, gr, dim3(256), 0, stream, p);
+        }
+      }
       else
         hipLaunchKernelGGL(gemm_fp8_reduce_kernel, dim3((unsigned)cdiv(k.M * k.N, 256)), dim3(256), 0, stream, p);
       TH_CHECK_LAUNCH();

@@ -43,6 +43,12 @@ struct GemmK {
   const float* rs_parts;
   int64_t ld_rs_parts;
   int n_rs_parts;
+  // optional (fp8 path): output gain_index stored as bf16(bf16(v) * gain_out[n]),
+  // each row's sums of bf16(v)^2 per 256 columns to ss_parts_out
+  const float* gain_out;
+  float* ss_parts_out;
+  int64_t ld_ss_parts_out;
+  int gain_index;
 };
 
 // Row `row`'s sum of squares: `own` (the kernel's sum over its lhs fragments), or

@@ -13,7 +13,7 @@ from pathlib import Path
 
 from .build import LIB_PATH
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 # th_status
 TH_OK = 0
@@ -64,6 +64,7 @@ class GemmDesc(C.Structure):
         ("rhs_scale", _p), ("workspace", _p), ("workspace_bytes", _i64),
         ("lhs_gain", _p),
         ("rs_parts", _p), ("ld_rs_parts", _i64), ("n_rs_parts", _i32), ("pad3_", _i32),
+        ("gain_out", _p), ("ss_parts_out", _p), ("ld_ss_parts_out", _i64), ("gain_out_index", _i32), ("pad4_", _i32),
     ]
 
 

@@ -15,6 +15,13 @@ kernel library. A step is five library calls:
   k3  th_gemm e4m3   act = silu(r2 (x1 g2) Wg) * (r2 (x1 g2) Wu)
   k4  th_gemm e4m3   out = x1 + act Wd
 
+With ``fold_gain`` (the default; hidden a multiple of 1024) k2's finishing pass
+also applies the post-attention norm's gain: it stores bf16(bf16(x1) g2), the
+operand k3 multiplies, and each row's sums of bf16(x1)^2 in parts of 256
+columns, which k3 adds up for r2 (``gain_out`` / ``rs_parts``); k3 then needs no
+pass of its own to scale its rows. The values are the same either way; the
+row sums add the same squares in another order.
+
 Every weight is the model's own ``W`` quantised per output channel,
 ``q = e4m3(W / s_n)`` with ``s_n = max_k |W[k, n]| / 448``. The RMSNorm gains
 stay on the activation side (``lhs_gain``: the GEMM multiplies x by g as it
@@ -60,7 +67,7 @@ class DecodeBlock:
 
     def __init__(self, state_dict: dict[str, torch.Tensor], *, hidden: int, heads: int, kv_heads: int,
                  intermediate: int, eps: float, rope_theta: float, batch: int, max_len: int,
-                 device: int | torch.device = 0) -> None:
+                 device: int | torch.device = 0, fold_gain: bool = True) -> None:
         self.device = torch.device("cuda", device) if isinstance(device, int) else torch.device(device)
         if self.device.type != "cuda":
             raise abi.HipBackendError("DecodeBlock", abi.TH_ERR_INVALID, f"device {device} is not a HIP device")
@@ -99,8 +106,10 @@ class DecodeBlock:
         self.v_cache = torch.zeros_like(self.k_cache)
         self.q = torch.empty(B, heads * self.hd, dtype=bf, device=dev)
         self.attn = torch.empty_like(self.q)
-        self.x1 = torch.empty(B, hidden, dtype=bf, device=dev)
+        self.x1 = torch.empty(B, hidden, dtype=bf, device=dev)  # with fold_gain: bf16(x1) g2
         self.x1_32 = torch.empty(B, hidden, device=dev)
+        self.fold_gain = fold_gain and hidden % 1024 == 0
+        self.x1_parts = torch.empty(B, hidden // 256, device=dev) if self.fold_gain else None
         self.act = torch.empty(B, intermediate, dtype=bf, device=dev)
         self.out = torch.empty(B, hidden, dtype=bf, device=dev)
         self.out32 = torch.empty(B, hidden, device=dev)
@@ -147,10 +156,14 @@ class DecodeBlock:
                    rscale_mask=0b1, lhs_gain=self.g1, **norm, **rope)
         ops.attention_decode(self.q, self.k_cache, self.v_cache, self.attn, scale=1.0 / math.sqrt(self.hd),
                              fixed_len=pos + 1, workspace=self.attn_ws)
-        self._gemm(self.wo, self.attn, [ops.EpiSpec(E.EPI_ADD, self.x1, e=0), ops.EpiSpec(E.EPI_ADD, self.x1_32, e=0)],
-                   extras=[x])
-        self._gemm(self.wgu, self.x1, [ops.EpiSpec(E.EPI_SWIGLU, self.act, a=0, b=1)], rscale_mask=0b11,
-                   lhs_gain=self.g2, **norm)
+        o_outs = [ops.EpiSpec(E.EPI_ADD, self.x1, e=0), ops.EpiSpec(E.EPI_ADD, self.x1_32, e=0)]
+        gu_outs = [ops.EpiSpec(E.EPI_SWIGLU, self.act, a=0, b=1)]
+        if self.fold_gain:
+            self._gemm(self.wo, self.attn, o_outs, extras=[x], gain_out=(0, self.g2, self.x1_parts))
+            self._gemm(self.wgu, self.x1, gu_outs, rscale_mask=0b11, rs_parts=self.x1_parts, **norm)
+        else:
+            self._gemm(self.wo, self.attn, o_outs, extras=[x])
+            self._gemm(self.wgu, self.x1, gu_outs, rscale_mask=0b11, lhs_gain=self.g2, **norm)
         self._gemm(self.wd, self.act, [ops.EpiSpec(E.EPI_ADD, self.out, e=0), ops.EpiSpec(E.EPI_ADD, self.out32, e=0)],
                    extras=[self.x1_32])
         return self.out

@@ -106,8 +106,13 @@ class GemmCall:
     rhs_scale: torch.Tensor | None = None      # fp8: [n_acc, N] fp32 per-column scales
     workspace: torch.Tensor | None = None      # gemm_workspace_bytes(...) bytes (fp8: required; fp32: optional)
     lhs_gain: torch.Tensor | None = None       # fp8: [K] fp32, products use lhs * gain (RMSNorm gain)
-    rs_parts: torch.Tensor | None = None       # bf16, with sumsq: [M, parts] fp32, the rows' sums of squares
-                                               # as partial sums (the lhs producer's), used instead of sum lhs^2
+    rs_parts: torch.Tensor | None = None       # bf16 (fp8 without lhs_gain), with sumsq: [M, parts] fp32, the
+                                               # rows' sums of squares as partial sums (the lhs producer's),
+                                               # used instead of sum lhs^2
+    gain_out: tuple[int, torch.Tensor, torch.Tensor] | None = None
+    # fp8: (output index, gain [N] fp32, ss_parts_out [M, N/256] fp32): that bf16 output is stored as
+    # bf16(bf16(v) * gain) and its rows' sums of bf16(v)^2 go to ss_parts_out, 256 columns per part
+    # (the next GEMM's lhs with its RMSNorm gain applied, and that GEMM's rs_parts)
 
     def descriptor(self) -> abi.GemmDesc:
         d = abi.GemmDesc()
@@ -155,6 +160,15 @@ class GemmCall:
                 raise abi.HipBackendError("th_gemm", abi.TH_ERR_INVALID, "rs_parts must be fp32 [M, parts]")
             d.rs_parts, d.ld_rs_parts = self.rs_parts.data_ptr(), _row_major(self.rs_parts, "th_gemm rs_parts")
             d.n_rs_parts = self.rs_parts.shape[1]
+        if self.gain_out is not None:
+            idx, g, parts = self.gain_out
+            if g.dtype != torch.float32 or not g.is_contiguous() or g.numel() != self.N:
+                raise abi.HipBackendError("th_gemm", abi.TH_ERR_INVALID, "gain_out gain must be contiguous fp32 [N]")
+            if parts.dtype != torch.float32 or parts.dim() != 2 or parts.shape[0] != self.M \
+                    or parts.shape[1] < self.N // 256:
+                raise abi.HipBackendError("th_gemm", abi.TH_ERR_INVALID, "ss_parts_out must be fp32 [M, N/256]")
+            d.gain_out, d.gain_out_index = g.data_ptr(), idx
+            d.ss_parts_out, d.ld_ss_parts_out = parts.data_ptr(), _row_major(parts, "th_gemm ss_parts_out")
         return d
 
 
