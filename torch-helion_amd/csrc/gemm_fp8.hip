@@ -470,18 +470,18 @@ __global__ void __launch_bounds__(512) gemm_fp8_lds_kernel(Fp8K p) {
   // row sums of squares (unless handed over): every workgroup when it
   // finishes its tile itself, else the first column block of each split
   const bool do_ss = p.k.sumsq && !p.ss_pre && (p.fused || blockIdx.x == 0);
-  // row sums handed over as the lhs producer's parts (up to 16): loaded before
-  // the first slices, added up (in row_sumsq's order) once those are issued
-  const bool pre_rs = p.k.sumsq && p.ss_pre == 2 && p.fused && p.k.n_rs_parts <= 16 && tid % PARTS == 0 &&
-                      tid / PARTS < p.M;
+  // row sums handed over as the lhs producer's parts (up to 16): loaded by
+  // every thread at the start (rows and parts clamped into range: no branch,
+  // so the compiler keeps its additions, and their wait, at the tile's end)
+  // and added up there, in row_sumsq's order, by the row's first thread
+  const bool pre_rs = p.k.sumsq && p.ss_pre == 2 && p.fused && p.k.n_rs_parts <= 16;
   float4 rsp[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) rsp[i] = make_float4(0.f, 0.f, 0.f, 0.f);
   if (pre_rs) {
-    const float4* q = (const float4*)(p.k.rs_parts + (int64_t)(tid / PARTS) * p.k.ld_rs_parts);
+    const int64_t rr = min((int64_t)(tid / PARTS), p.M - 1);
+    const float4* q = (const float4*)(p.k.rs_parts + rr * p.k.ld_rs_parts);
+    const int nq4 = p.k.n_rs_parts >> 2;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      if (i < (p.k.n_rs_parts >> 2)) rsp[i] = q[i];
+    for (int i = 0; i < 4; ++i) rsp[i] = q[i < nq4 ? i : 0];
   }
 
   // activation load q of this wave fills slice rows RPI (ALD wave + q) + lane / LPR,
@@ -587,18 +587,6 @@ __global__ void __launch_bounds__(512) gemm_fp8_lds_kernel(Fp8K p) {
   };
 
   unroll_seq(std::make_integer_sequence<int, P>(), [&](auto s) { issue(min((int)s, nsl - 1), s); });
-  float rs_sum = 0.f;
-  if (pre_rs) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      if (i < (p.k.n_rs_parts >> 2)) {
-        rs_sum += rsp[i].x;
-        rs_sum += rsp[i].y;
-        rs_sum += rsp[i].z;
-        rs_sum += rsp[i].w;
-      }
-    }
-  }
   // whole trips of NBUF steps (the last one padded): one in-flight pattern at every wait
   for (int j = 0; j < nsl; j += NBUF)
     unroll_seq(std::make_integer_sequence<int, NBUF>(), [&](auto s) { step(j + (int)s, s); });
@@ -684,7 +672,19 @@ __global__ void __launch_bounds__(512) gemm_fp8_lds_kernel(Fp8K p) {
     if (p.k.sumsq) {
       float s = ss;
       if (pre_rs) {
-        s = rs_sum;
+        s = rsp[0].x;
+        s += rsp[0].y;
+        s += rsp[0].z;
+        s += rsp[0].w;
+#pragma unroll
+        for (int i = 1; i < 4; ++i) {
+          const bool in = i < (p.k.n_rs_parts >> 2);
+          float t = s + rsp[i].x;
+          t += rsp[i].y;
+          t += rsp[i].z;
+          t += rsp[i].w;
+          s = in ? t : s;
+        }
       } else if (p.ss_pre == 2) {
         s = row_sumsq(p.k, row, 0.f);
       } else if (p.ss_pre) {
