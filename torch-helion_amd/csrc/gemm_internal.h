@@ -52,18 +52,29 @@ struct GemmK {
 };
 
 // Row `row`'s sum of squares: `own` (the kernel's sum over its lhs fragments), or
-// the sum of the producer's partial sums when the caller gave them (four at a
-// time, in order; rows past M read row M - 1, whose scale is never used).
+// the sum of the producer's partial sums when the caller gave them, added one
+// after another in order; rows past M read row M - 1, whose scale is never
+// used. The parts are fetched 32 at a time, every load issued before the
+// first addition (indices clamped, additions past the end selected away: no
+// branch for the compiler to put a wait into), so a row costs one memory
+// round trip per 32 parts instead of one per 4.
 __device__ __forceinline__ float row_sumsq(const GemmK& p, int64_t row, float own) {
   if (p.rs_parts == nullptr) return own;
   const float4* q = (const float4*)(p.rs_parts + (row < p.M ? row : p.M - 1) * p.ld_rs_parts);
+  const int n4 = p.n_rs_parts >> 2;
   float v = 0.f;
-  for (int i = 0; i < (p.n_rs_parts >> 2); ++i) {
-    const float4 f = q[i];
-    v += f.x;
-    v += f.y;
-    v += f.z;
-    v += f.w;
+  for (int i0 = 0; i0 < n4; i0 += 8) {
+    float4 f[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) f[j] = q[i0 + j < n4 ? i0 + j : n4 - 1];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      float t = v + f[j].x;
+      t += f[j].y;
+      t += f[j].z;
+      t += f[j].w;
+      v = i0 + j < n4 ? t : v;
+    }
   }
   return v;
 }
