@@ -541,11 +541,13 @@ __global__ void __launch_bounds__(256, NTW <= 2 ? 4 : 1) ssd_state2_kernel(SsdK 
 // H_0 = 0, H_{c+1} = exp(tot_c) H_c + S_c, written for c >= 1 as the hi/lo bf16
 // B fragments of the out kernel's state term: fragment (pt, ks, lane) is
 // H[pt*32 + lane%32][16 ks + 8 (lane/32) + j], j < 8, hi (16 bytes) then lo.
-// One thread per (p, 8 consecutive n), sequential over the chunks.
+// One thread per (p, 8 consecutive n), sequential over the chunks; blocks of
+// 256 threads, or of 64 when that many would not reach every CU (the loads of
+// a small grid then come from all of them: C2's carry 7.9 -> about 6 us).
 __global__ void __launch_bounds__(256) ssd_carry2_kernel(SsdK p, uint4* hf) {
   const int h = blockIdx.y, b = blockIdx.z;
   const int N8 = p.N >> 3, KS = p.N >> 4, PN = p.P * p.N;
-  const int e = blockIdx.x * 256 + threadIdx.x;
+  const int e = blockIdx.x * blockDim.x + threadIdx.x;
   if (e >= p.P * N8) return;
   const int pp = e / N8, n8 = e - pp * N8;
   const int frag = ((pp >> 5) * KS + (n8 >> 1)) * 64 + (pp & 31) + 32 * (n8 & 1);
@@ -1243,7 +1245,9 @@ extern "C" int th_ssd_chunked(const th_ssd_desc* d, void* stream) {
     else hipLaunchKernelGGL((ssd_state2_kernel<4, 4>), grid, dim3(256), lring, s, k);
     TH_CHECK_LAUNCH();
     if (k.nc > 1) {
-      hipLaunchKernelGGL(ssd_carry2_kernel, dim3((unsigned)cdiv(k.P * k.N / 8, 256), k.H, k.B), dim3(256), 0, s, k, hf);
+      const int64_t cus = device_cus() > 0 ? device_cus() : 256;
+      const int ct = cdiv(k.P * k.N / 8, 256) * k.H * k.B < cus ? 64 : 256;
+      hipLaunchKernelGGL(ssd_carry2_kernel, dim3((unsigned)cdiv(k.P * k.N / 8, ct), k.H, k.B), dim3(ct), 0, s, k, hf);
       TH_CHECK_LAUNCH();
     }
     const size_t l3 = out2_lds(k.Q, k.P, k.N);
