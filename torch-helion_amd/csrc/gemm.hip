@@ -1478,8 +1478,21 @@ __global__ void __launch_bounds__(256) gemm_f32_ksr_kernel(F32Ksp q) {
     *(float4*)(slab + r * SROW + c4) = a;
   }
   if (p.sumsq && tid < RB) {
+    // the slices' row sums in order, eight loads in flight at a time (indices
+    // clamped and additions past the end selected away: no branch between the
+    // loads for the compiler to wait in)
+    const float* sq = q.ssq + r0 + tid;
     float v = 0.f;
-    for (int g = 0; g < q.ksg; ++g) v += q.ssq[(int64_t)g * q.Mp + r0 + tid];
+    for (int g0 = 0; g0 < q.ksg; g0 += 8) {
+      float x[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) x[u] = sq[(int64_t)min(g0 + u, q.ksg - 1) * q.Mp];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const float t = v + x[u];
+        v = g0 + u < q.ksg ? t : v;
+      }
+    }
     rs[tid] = rsqrtf(v * p.inv_k + p.eps);
     const int64_t gr = r0 + tid;
     if (p.sumsq_out && tn == 0 && gr < p.M) p.sumsq_out[gr] = v;
