@@ -680,10 +680,13 @@ def test_attention_bf16(gpu, B, S, Hq, Hkv, hd, causal):
 
 
 @pytest.mark.parametrize("B,S,Hq,Hkv,hd,causal", [(1, 128, 8, 8, 64, True), (2, 200, 4, 2, 128, True),
-                                                  (1, 77, 4, 1, 64, False), (2, 33, 2, 2, 32, True)])
+                                                  (1, 77, 4, 1, 64, False), (2, 33, 2, 2, 32, True),
+                                                  (1, 700, 2, 1, 128, False), (1, 300, 2, 2, 64, True)])
 def test_attention_f32(gpu, B, S, Hq, Hkv, hd, causal):
     """fp32 prefill attention: the matrix-core kernel (head_dim 64/128; C1 is the first case),
-    ragged query and key blocks, grouped KV heads, and the scalar kernel (head_dim 32)."""
+    ragged query and key blocks, grouped KV heads, and the scalar kernel (head_dim 32). The
+    matrix-core kernel deals a query block's key blocks over four waves and merges them: query
+    blocks with fewer key blocks than waves (causal), and with several per wave (S = 700)."""
     from torch_helion.hip import ops
 
     announce(f"attention f32 B={B} S={S} Hq={Hq} Hkv={Hkv} hd={hd} causal={causal}")

@@ -336,8 +336,11 @@ __global__ void __launch_bounds__(64) attn_fwd_f32_kernel(AttnF32K p) {
   for (int d = 0; d < D; ++d) orow[d] = acc[d] * inv;
 }
 
-// fp32 attention on the matrix cores (head_dim 64 or 128): one wave per 32
-// queries of one (batch, q head), keys in blocks of 32 with an online softmax.
+// fp32 attention on the matrix cores (head_dim 64 or 128): one workgroup of KW
+// waves per 32 queries of one (batch, q head); wave w takes the key blocks
+// w, w + KW, ... (32 keys each) with its own online softmax, and the waves'
+// partial results are merged through LDS at the end, in wave order. (One wave
+// walking every block serially left C1's 8 x 4 query blocks latency-bound.)
 // S^T = K Q^T and O^T += V^T P^T run on v_mfma_f32_32x32x2f32, so a lane owns
 // one query column (l % 32) and the softmax statistics need one lane^32
 // exchange, as in the bf16 kernel. Operands come straight from memory in the
@@ -348,16 +351,18 @@ __global__ void __launch_bounds__(64) attn_fwd_f32_kernel(AttnF32K p) {
 //   O^T step (register r of S^T): lane l supplies P for key
 //     8(r/4) + 4(l/32) + r%4 (its own S^T register) and V[that key][32t + l%32].
 // The result goes out through LDS as whole rows.
-template <int D>
-__global__ void __launch_bounds__(64, 1) attn_fwd_f32_mfma_kernel(AttnF32K p) {
+template <int D, int KW>
+__global__ void __launch_bounds__(64 * KW, 1) attn_fwd_f32_mfma_kernel(AttnF32K p) {
   constexpr int NCH = D / 8;   // float4 chunks per lane of a Q or K row
   constexpr int NDT = D / 32;  // 32-row tiles of O^T
-  constexpr int OROW = D + 4;  // LDS row stride (floats) of the output staging
-  __shared__ __attribute__((aligned(16))) float so[32 * OROW];
+  constexpr int OROW = D + 4;  // LDS row stride (floats) of a wave's partial output
+  __shared__ __attribute__((aligned(16))) float so[KW * 32 * OROW];
+  __shared__ float sm[KW * 32], sl[KW * 32];
   const int bh = blockIdx.y;
   const int b = bh / p.Hq, hq = bh - b * p.Hq, hk = hq / p.group;
   const int q0 = blockIdx.x * 32;
-  const int lane = threadIdx.x, qc = lane & 31, half = lane >> 5;
+  const int tid = threadIdx.x, lane = tid & 63, qc = lane & 31, half = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const float* qb = p.q + (int64_t)b * p.Sq * p.ldq + (int64_t)hq * D;
   const float* kbase = p.k + (int64_t)b * p.Skv * p.ldk + (int64_t)hk * D;
   const float* vbase = p.v + (int64_t)b * p.Skv * p.ldv + (int64_t)hk * D;
@@ -376,8 +381,8 @@ __global__ void __launch_bounds__(64, 1) attn_fwd_f32_mfma_kernel(AttnF32K p) {
   if (p.causal) kend = min(kend, q0 + 31 + p.off + 1);
   const int myq = q0 + qc;
   // K rows of a block (rows past Skv re-read the last key; masked below) and its
-  // V operands (register r's key, columns 32t + l%32); the next block's are
-  // loaded while this one computes
+  // V operands (register r's key, columns 32t + l%32); the wave's next block's
+  // are loaded while this one computes
   float4 kf[NCH], kn[NCH];
   float vf[NDT][16], vn[NDT][16];
   auto load_block = [&](int kb, float4 (&kx)[NCH], float (&vx)[NDT][16]) {
@@ -391,15 +396,16 @@ __global__ void __launch_bounds__(64, 1) attn_fwd_f32_mfma_kernel(AttnF32K p) {
       for (int t = 0; t < NDT; ++t) vx[t][r] = vbase[(int64_t)key * p.ldv + 32 * t + qc];
     }
   };
-  if (kend > 0) load_block(0, kn, vn);
-  for (int kb = 0; kb < kend; kb += 32) {
+  const int kfirst = 32 * wave;
+  if (kfirst < kend) load_block(kfirst, kn, vn);
+  for (int kb = kfirst; kb < kend; kb += 32 * KW) {
 #pragma unroll
     for (int i = 0; i < NCH; ++i) kf[i] = kn[i];
 #pragma unroll
     for (int t = 0; t < NDT; ++t)
 #pragma unroll
       for (int r = 0; r < 16; ++r) vf[t][r] = vn[t][r];
-    if (kb + 32 < kend) load_block(kb + 32, kn, vn);
+    if (kb + 32 * KW < kend) load_block(kb + 32 * KW, kn, vn);
     f32x16_t st;
 #pragma unroll
     for (int r = 0; r < 16; ++r) st[r] = 0.f;
@@ -440,23 +446,43 @@ __global__ void __launch_bounds__(64, 1) attn_fwd_f32_mfma_kernel(AttnF32K p) {
       for (int r = 0; r < 16; ++r) o[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(vf[t][r], st[r], o[t], 0, 0, 0);
     }
   }
-  // O = O^T / l, transposed through LDS: lane l holds column (query) l%32, rows
-  // d = 32t + 8(r/4) + 4(l/32) + r%4
-  const float inv = l > 0.f ? 1.f / l : 0.f;
+  // the wave's partial O^T (unnormalised; lane l holds column (query) l%32, rows
+  // d = 32t + 8(r/4) + 4(l/32) + r%4) as rows of its LDS slab, with m and l
+  float* sw = so + wave * 32 * OROW;
 #pragma unroll
   for (int t = 0; t < NDT; ++t)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) so[qc * OROW + 32 * t + 8 * (r >> 2) + 4 * half + (r & 3)] = o[t][r] * inv;
+    for (int r = 0; r < 16; ++r) sw[qc * OROW + 32 * t + 8 * (r >> 2) + 4 * half + (r & 3)] = o[t][r];
+  if (half == 0) {
+    sm[wave * 32 + qc] = m;
+    sl[wave * 32 + qc] = l;
+  }
   __syncthreads();
-  // each pass: 64 lanes write D/4 float4 of 256 / D rows
-  constexpr int F4 = D / 4, RPP = 64 / F4;
+  // merge, in wave order: O = sum_w 2^(m_w - m) O_w / sum_w 2^(m_w - m) l_w, m = max_w m_w;
+  // each thread writes float4s of whole rows
+  constexpr int F4 = D / 4;
   float* ob = p.o + (int64_t)b * p.Sq * p.ldo + (int64_t)hq * D;
-  for (int rr = lane / F4; rr < 32; rr += RPP) {
+  for (int e = tid; e < 32 * F4; e += 64 * KW) {
+    const int rr = e / F4, c4 = e - rr * F4;
     const int qi = q0 + rr;
-    if (qi < p.Sq) {
-      const int c4 = lane % F4;
-      *(float4*)(ob + (int64_t)qi * p.ldo + 4 * c4) = *(const float4*)(so + rr * OROW + 4 * c4);
+    if (qi >= p.Sq) continue;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < KW; ++w) mx = fmaxf(mx, sm[w * 32 + rr]);
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    float lt = 0.f;
+    if (mx != -INFINITY) {
+#pragma unroll
+      for (int w = 0; w < KW; ++w) {
+        const float mw = sm[w * 32 + rr];
+        const float sc = mw == -INFINITY ? 0.f : exp2f(mw - mx);
+        const float4 x = *(const float4*)(so + (w * 32 + rr) * OROW + 4 * c4);
+        lt += sc * sl[w * 32 + rr];
+        acc.x += sc * x.x; acc.y += sc * x.y; acc.z += sc * x.z; acc.w += sc * x.w;
+      }
     }
+    const float inv = lt > 0.f ? 1.f / lt : 0.f;
+    *(float4*)(ob + (int64_t)qi * p.ldo + 4 * c4) = make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
   }
 }
 
@@ -528,9 +554,9 @@ extern "C" int th_attention_prefill(const th_attn_desc* d, void* stream) {
     if (mfma) {
       const dim3 grid((unsigned)cdiv(d->seq_q, 32), (unsigned)(d->batch * d->heads_q));
       if (hd == 64)
-        hipLaunchKernelGGL(attn_fwd_f32_mfma_kernel<64>, grid, dim3(64), 0, s, k);
+        hipLaunchKernelGGL((attn_fwd_f32_mfma_kernel<64, 4>), grid, dim3(256), 0, s, k);
       else
-        hipLaunchKernelGGL(attn_fwd_f32_mfma_kernel<128>, grid, dim3(64), 0, s, k);
+        hipLaunchKernelGGL((attn_fwd_f32_mfma_kernel<128, 4>), grid, dim3(256), 0, s, k);
     } else {
       const dim3 grid((unsigned)cdiv(d->seq_q, 64), (unsigned)(d->batch * d->heads_q));
       switch (hd) {
