@@ -362,6 +362,11 @@ def test_compile_model_decode_fp8_vs_oracle(gpu, tmp_path, which):
     # q and k|v read the same input: one e4m3 launch over both, on column windows
     assert any(l.info.get("weights") == "float8_e4m3fn" and len(l.info.get("merged", [])) == 2
                for l in dp.launches), [l.kernel for l in dp.launches]
+    # hidden a multiple of 1024 (C5): the o-projection stores gate/up's gained operand and its row
+    # sums, so gate/up has no gain pre-pass; at hidden 256 gate/up scales its rows itself
+    folded = [l.info.get("gain_out_for") for l in dp.launches if l.info.get("gain_out_for")]
+    from_producer = [l.kernel for l in dp.launches if l.info.get("row_sums_from_producer")]
+    assert len(folded) == (1 if which == "c5" else 0) and from_producer == folded, (folded, from_producer)
     dp.run([x, kc, vc])
     torch.cuda.synchronize()
     out, k_dev, v_dev = (t.double().cpu() for t in dp.outputs(fp32=True))

@@ -193,6 +193,9 @@ class DeviceProgram:
         # scans whose only reader normalises them with a gain: the scan applies it (_plan_norm_folds)
         self._rs_parts: dict[tuple, torch.Tensor] = {}
         self._norm_folds = self._plan_norm_folds(program)
+        # e4m3 GEMMs whose gained lhs the producing e4m3 GEMM stores (_plan_fp8_gain_folds)
+        self._fp8_gain_folds = self._plan_fp8_gain_folds(program)
+        self._fp8_gained: dict[str, tuple[torch.Tensor, torch.Tensor]] = {}
         for i, k in enumerate(program.kernels):
             self._cur = i
             if self.reuse:
@@ -636,6 +639,20 @@ class DeviceProgram:
             for out_buf in dsts:
                 epi.append(ops.EpiSpec(op, out_buf, a=slot[a], b=slot[b] if b >= 0 else -1,
                                        e=extras.index(o.extra) if o.extra is not None else -1))
+        gain_out = None
+        fold = self._fp8_gain_folds.get(spec.name) if fp8 and collect is None else None
+        if fold is not None:
+            # the consumer's operand: this output again, times its norm gain, with the row sums
+            g = next(k for k in self.program.kernels if k.name == fold["consumer"])
+            o, op, a, b, _ = next(x for x in outs if x[0].tensor == fold["tensor"])
+            last = self._last.get(fold["tensor"], self._cur)
+            xg = self._device_buffer((T, N), torch.bfloat16, last)
+            parts = self._device_buffer((T, N // 256), torch.float32, last)
+            gvec = self.buffers[g.arg("gain").tensor].float().reshape(-1).contiguous()
+            epi.append(ops.EpiSpec(op, xg, a=slot[a], b=slot[b] if b >= 0 else -1,
+                                   e=extras.index(o.extra) if o.extra is not None else -1))
+            gain_out = (len(epi) - 1, gvec, parts)
+            self._fp8_gained[fold["consumer"]] = (xg, parts)
         if len(epi) > abi.MAX_OUT:
             return None
         mask = 0
@@ -666,10 +683,18 @@ class DeviceProgram:
             ws = self._workspace(max(ops.gemm_workspace_bytes(T, N, K, len(used), _FP8), 16), torch.uint8) \
                 if collect is None else None
             fp8_kw = dict(in_dtype=_FP8, rhs_scale=scale, workspace=ws)
-            if "gain" in names:
+            gained = self._fp8_gained.get(spec.name) if collect is None else None
+            if gained is not None:
+                # the producer stored lhs * g and the rows' sums of squares (_plan_fp8_gain_folds)
+                lhs, rs_parts = gained
+                info["row_sums_from_producer"] = True
+            elif "gain" in names:
                 # activation-side norm gain: the products see lhs * g, the sum of squares lhs
                 fp8_kw["lhs_gain"] = self.buffers[spec.arg("gain").tensor].float().reshape(-1).contiguous()
-            info.update({"weights": "float8_e4m3fn", "lhs_gain": "gain" in names})
+            if gain_out is not None:
+                fp8_kw["gain_out"] = gain_out
+                info["gain_out_for"] = self._fp8_gain_folds[spec.name]["consumer"]
+            info.update({"weights": "float8_e4m3fn", "lhs_gain": "gain" in names and gained is None})
 
         if collect is not None:
             collect.append(dict(T=T, N=N, K=K, lhs=lhs, fp8=fp8, rhs=[spec.arg(rhs_of[i]).tensor for i in used],
@@ -759,6 +784,50 @@ class DeviceProgram:
             if gain is None or gain.numel() != H * P:
                 continue
             folds[k.name] = {"gemm": g.name, "gain": gain, "key": self._norm_key(t, gain, plan.rscale), "tensor": t}
+        return folds
+
+    def _plan_fp8_gain_folds(self, program: Program) -> dict[str, dict]:
+        """e4m3 GEMMs with an activation-side norm gain (a ``gain`` argument) whose lhs is a
+        bf16 output, over all its columns, of another e4m3 GEMM: the decode step's gate/up
+        reading the o-projection's x1. The producer's finishing pass also stores x1 with the
+        gain applied and its rows' sums of squares (th_gemm's gain_out), and the consumer
+        multiplies that copy, taking the sums as its rs_parts, instead of scaling x1 in a
+        pre-pass of its own. Neither kernel may be part of a merged launch; the producer's
+        width must be a multiple of 1024 and it must run through its split reduction with
+        4-column outputs (whole 128-column packed tiles, K a multiple of 128).
+        Returns {producer kernel: {"consumer", "tensor"}}."""
+        folds: dict[str, dict] = {}
+        writer: dict[str, KernelSpec] = {}
+        for k in program.kernels:
+            for o in k.outputs:
+                writer[o.tensor] = k
+
+        def e4m3(k: KernelSpec) -> bool:
+            return k.kind == "gemm" and bool(k.gemms) and all(
+                program.tensors[k.arg(g.rhs).tensor].dtype == "float8_e4m3fn" for g in k.gemms)
+
+        def alone(k: KernelSpec) -> bool:
+            return k.name not in self._merge_groups and k.name not in self._merged_away and not any(
+                k.name == m[0].name for v in self._fp8_groups.values() for m in v)
+
+        taken: set[str] = set()
+        for g in program.kernels:
+            if not e4m3(g) or "gain" not in {a.name for a in g.args} or not alone(g):
+                continue
+            t = g.arg("lhs").tensor
+            pk = writer.get(t)
+            if pk is None or pk.name in taken or not e4m3(pk) or not alone(pk) or program.tensors[t].dtype != "bfloat16":
+                continue
+            N, K = pk.grid["cols"], pk.k_extent
+            if N % 1024 or K % 128 or g.grid["cols"] <= 0:
+                continue
+            pp, pg = match_epilogue(pk), match_epilogue(g)
+            if not pp.fused or not pg.fused or pg.rscale is None or any(o.rope is not None for o in pp.outs):
+                continue
+            if sum(1 for o in pp.outs if o.tensor == t) != 1:
+                continue
+            folds[pk.name] = {"consumer": g.name, "tensor": t}
+            taken.add(pk.name)
         return folds
 
     def _normed_lhs(self, spec: KernelSpec, lhs_t: str, gain: torch.Tensor, rscale,
