@@ -1375,7 +1375,7 @@ __global__ void __launch_bounds__(1024, 1) gemm_f32_sk_kernel(GemmK p) {
 // operand layout and wave-private LDS ring as gemm_f32_sk_kernel, and stores its
 // partial tile to part[g][row][column] (rows of the padded row count Mp); the
 // column-0 workgroups also store the slice's row sums of squares ssq[g][row].
-// Pass 2 (gemm_f32_ksr_kernel): one workgroup per 8 rows x BNC columns sums the
+// Pass 2 (gemm_f32_ksr_kernel): one workgroup per 8 (or 2) rows x BNC columns sums the
 // KSG partials in slice order (deterministic) into an LDS slab and runs the
 // slab epilogue. Enough pass-1 workgroups to cover the GPU (about one per CU)
 // for the fp32 block's GEMMs of 128 rows, which one workgroup per tile cannot.
@@ -1449,9 +1449,9 @@ __global__ void __launch_bounds__(BNC * 2) gemm_f32_ksp_kernel(F32Ksp q) {
 #endif
 }
 
-template <int BNC>
+template <int BNC, int RB>
 __global__ void __launch_bounds__(256) gemm_f32_ksr_kernel(F32Ksp q) {
-  constexpr int RB = 8, SROW = BNC + 8, V4 = RB * BNC / 4;  // float4s of the 8-row slab
+  constexpr int SROW = BNC + 8, V4 = RB * BNC / 4;  // float4s of the RB-row slab
   __shared__ __attribute__((aligned(16))) float slab[RB * SROW];
   __shared__ float rs[RB];
   const GemmK& p = q.k;
@@ -1790,7 +1790,13 @@ static void launch_f32_sk(const GemmK& k, hipStream_t s) {
 template <int BNC>
 static void launch_f32_ksp(const F32Ksp& q, hipStream_t s) {
   hipLaunchKernelGGL((gemm_f32_ksp_kernel<BNC>), dim3(q.k.tiles_m * q.k.tiles_n, q.ksg), dim3(2 * BNC), 0, s, q);
-  hipLaunchKernelGGL((gemm_f32_ksr_kernel<BNC>), dim3((unsigned)(q.Mp / 8 * q.k.tiles_n)), dim3(256), 0, s, q);
+  // 8-row slabs, or 2-row ones when 8-row ones would leave CUs without a
+  // workgroup (the partials are then fetched by every CU)
+  const int64_t cus = device_cus() > 0 ? device_cus() : 256;
+  if (q.Mp / 8 * q.k.tiles_n < cus)
+    hipLaunchKernelGGL((gemm_f32_ksr_kernel<BNC, 2>), dim3((unsigned)(q.Mp / 2 * q.k.tiles_n)), dim3(256), 0, s, q);
+  else
+    hipLaunchKernelGGL((gemm_f32_ksr_kernel<BNC, 8>), dim3((unsigned)(q.Mp / 8 * q.k.tiles_n)), dim3(256), 0, s, q);
 }
 
 extern "C" int th_gemm(const th_gemm_desc* d, void* stream) {
